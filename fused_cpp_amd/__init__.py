@@ -1,0 +1,11 @@
+"""fused_cpp_amd -- MI355X (gfx950) fused MoE operators.
+
+Drop-in for the fused-MoE path of hearth-stone/fused_cpp: ``moe`` mirrors
+``fused_cpp.moe`` and ``i8gemm`` mirrors ``fused_cpp.i8gemm``. The operators
+run hand-written HIP kernels (libfcmoe.so, C ABI in include/fcmoe.h) through
+the C++ torch extension ``_moe_C``.
+"""
+
+from . import i8gemm, moe
+
+__all__ = ["i8gemm", "moe"]

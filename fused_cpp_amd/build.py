@@ -1,0 +1,124 @@
+"""In-tree build of the gfx950 library and its PyTorch host extension.
+
+Produces, next to this file:
+
+* ``libfcmoe.so`` -- the HIP kernels and the C ABI of ``include/fcmoe.h``
+  (``hipcc --offload-arch=gfx950``; no torch dependency);
+* ``_moe_C<EXT_SUFFIX>`` -- the C++ torch extension that marshals tensors into
+  that C ABI (g++ against the torch / ROCm headers, rpath ``$ORIGIN``).
+
+Usage: ``python -m fused_cpp_amd.build`` (or ``build()``). hipcc cross-compiles
+for gfx950 without a GPU. Compilation flags: ``-ffp-contract=off`` keeps each
+binary32 operation separately rounded (the W8A8 path is bit-exact against the
+CPU restatement of the reference arithmetic); packed-fp32 instructions are
+disabled.
+"""
+
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+import sysconfig
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+REPO = PKG.parent
+CSRC = PKG / "csrc"
+ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
+ARCH = os.environ.get("FCMOE_OFFLOAD_ARCH", "gfx950")
+
+HIP_SOURCES = ["fcmoe_api.hip", "fcmoe_route.hip", "fcmoe_quant.hip", "fcmoe_gemm.hip", "fcmoe_combine.hip"]
+HIP_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-fPIC",
+    "-std=c++17",
+    "-ffp-contract=off",
+    "-Xclang",
+    "-target-feature",
+    "-Xclang",
+    "-packed-fp32-ops",
+]
+
+LIB = PKG / "libfcmoe.so"
+EXT = PKG / ("_moe_C" + sysconfig.get_config_var("EXT_SUFFIX"))
+BUILD_DIR = PKG / "_build"
+
+
+def _run(cmd: list[str]) -> None:
+    proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    if proc.returncode != 0:
+        sys.stderr.write(proc.stdout)
+        raise RuntimeError(f"build step failed ({proc.returncode}): {' '.join(cmd[:3])} ...")
+
+
+def build_lib() -> Path:
+    """Compile every HIP source to an object in parallel, then link libfcmoe.so."""
+    BUILD_DIR.mkdir(exist_ok=True)
+    hipcc = str(ROCM / "bin" / "hipcc")
+
+    def compile_one(src: str) -> str:
+        obj = BUILD_DIR / (src + ".o")
+        _run([hipcc, *HIP_FLAGS, "-c", str(CSRC / src), "-o", str(obj)])
+        return str(obj)
+
+    with ThreadPoolExecutor(max_workers=min(len(HIP_SOURCES), os.cpu_count() or 1)) as ex:
+        objs = list(ex.map(compile_one, HIP_SOURCES))
+    tmp = LIB.with_suffix(".so.tmp")
+    _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *objs])
+    os.replace(tmp, LIB)
+    return LIB
+
+
+def build_ext() -> Path:
+    """Compile the torch host extension against libfcmoe.so."""
+    import torch
+    from torch.utils import cpp_extension
+
+    torch_lib = Path(torch.__file__).resolve().parent / "lib"
+    incs = [*cpp_extension.include_paths(), sysconfig.get_paths()["include"], str(ROCM / "include")]
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    cmd = [
+        os.environ.get("CXX", "g++"),
+        "-O2",
+        "-fPIC",
+        "-shared",
+        "-std=c++17",
+        "-D__HIP_PLATFORM_AMD__=1",
+        "-DUSE_ROCM=1",
+        "-DTORCH_EXTENSION_NAME=_moe_C",
+        "-DTORCH_API_INCLUDE_EXTENSION_H",
+        f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+        *[f"-I{i}" for i in incs],
+        str(CSRC / "moe_ext.cpp"),
+        "-o",
+        str(EXT) + ".tmp",
+        f"-L{torch_lib}",
+        f"-L{PKG}",
+        "-lfcmoe",
+        "-lc10",
+        "-lc10_hip",
+        "-ltorch",
+        "-ltorch_cpu",
+        "-ltorch_hip",
+        "-ltorch_python",
+        f"-L{ROCM / 'lib'}",
+        "-lamdhip64",
+        "-Wl,-rpath,$ORIGIN",
+        f"-Wl,-rpath,{torch_lib}",
+    ]
+    _run(cmd)
+    os.replace(str(EXT) + ".tmp", EXT)
+    return EXT
+
+
+def build() -> None:
+    build_lib()
+    build_ext()
+
+
+if __name__ == "__main__":
+    build()
+    print(f"built {LIB.name} and {EXT.name}")

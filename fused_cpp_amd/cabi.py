@@ -1,0 +1,108 @@
+"""ctypes binding of libfcmoe.so's C ABI (include/fcmoe.h).
+
+This is the binding a non-torch host (or a reference-side FFI) would use; the
+GPU parity tests call the kernels through it so that what is checked is the
+C ABI itself. Tensors are passed as device pointers (``tensor.data_ptr()``)
+with the current torch HIP stream.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libfcmoe.so"
+
+FCMOE_ACT_SILU = 0
+FCMOE_ACT_GELU = 1
+FCMOE_ACT_SWIGLUOAI = 2
+FCMOE_ACT_SILU_CLAMP10 = 3
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_I = ctypes.c_int
+_SZ = ctypes.c_size_t
+
+
+class MoeArgs(ctypes.Structure):
+    """Mirror of ``struct fcmoe_moe_args``."""
+
+    _fields_ = [
+        ("x", _P),
+        ("tokens", _I64),
+        ("hidden", _I64),
+        ("inter", _I64),
+        ("topk_ids", _P),
+        ("ids_is_i64", _I),
+        ("topk_weights", _P),
+        ("top_k", _I64),
+        ("experts", _I64),
+        ("valid_experts", _I64),
+        ("shared_expert_id", _I64),
+        ("routed_scaling", ctypes.c_float),
+        ("w13", _P),
+        ("w2", _P),
+        ("w13_scale", _P),
+        ("w2_scale", _P),
+        ("w13_bias", _P),
+        ("w2_bias", _P),
+        ("activation", _I),
+        ("skip_weighted", _I),
+        ("out", _P),
+        ("invalid_count", _P),
+        ("workspace", _P),
+        ("workspace_bytes", _SZ),
+    ]
+
+
+# name -> (restype, argtypes); every symbol declared in include/fcmoe.h.
+SIGNATURES = {
+    "fcmoe_last_error": (ctypes.c_char_p, []),
+    "fcmoe_abi_version": (_I, []),
+    "fcmoe_quantize_weight_rows": (_I, [_P, _I64, _I64, _P, _P, _P]),
+    "fcmoe_packed_expert_bytes": (_I64, [_I, _I64, _I64, _I]),
+    "fcmoe_pack_experts": (_I, [_P, _I, _I64, _I64, _I64, _I, _P, _P]),
+    "fcmoe_route_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64]),
+    "fcmoe_route_build": (_I, [_P, _I, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _SZ, _P]),
+    "fcmoe_quantize_rows": (_I, [_P, _I, _I64, _I64, _I, _P, _I64, _P, _P]),
+    "fcmoe_w8a8_workspace_bytes": (_SZ, [ctypes.POINTER(MoeArgs)]),
+    "fcmoe_w8a8_forward": (_I, [ctypes.POINTER(MoeArgs), _P]),
+    "fcmoe_bf16_workspace_bytes": (_SZ, [ctypes.POINTER(MoeArgs)]),
+    "fcmoe_bf16_forward": (_I, [ctypes.POINTER(MoeArgs), _P]),
+    "fcmoe_i8gemm_workspace_bytes": (_SZ, [_I64, _I64]),
+    "fcmoe_i8gemm": (_I, [_P, _I, _I64, _I64, _P, _P, _I64, _P, _P, _I, _P, _SZ, _P]),
+    "fcmoe_grouped_gemm_i8_acc": (_I, [_P, _I64, _P, _P, _P, _I64, _I64, _P, _I64, _I64, _P, _P, _SZ, _P]),
+    "fcmoe_grouped_gemm_workspace_bytes": (_SZ, [_I64, _I64]),
+    "fcmoe_w8a8_stage_views": (_I, [ctypes.POINTER(MoeArgs), _P, _P, _P, _P, _P, _P, _P]),
+}
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(f"{LIB_PATH} is not built (python -m fused_cpp_amd.build)")
+        l = ctypes.CDLL(str(LIB_PATH))
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(l, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = l
+    return _lib
+
+
+def check(rc: int, what: str) -> None:
+    if rc != 0:
+        raise RuntimeError(f"{what} failed ({rc}): {lib().fcmoe_last_error().decode()}")
+
+
+def ptr(t) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def stream_handle() -> int:
+    import torch
+
+    return torch.cuda.current_stream().cuda_stream

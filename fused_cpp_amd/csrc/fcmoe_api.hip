@@ -1,0 +1,512 @@
+// fcmoe_api.hip -- the C ABI (include/fcmoe.h): argument validation,
+// workspace layout and the launch sequence of each fused operator.
+#include <stdio.h>
+
+#include <string>
+
+#include "fcmoe_device.h"
+#include "fcmoe_internal.h"
+
+namespace fcmoe {
+
+namespace {
+thread_local std::string g_error;
+
+// Tile rows of the grouped GEMM classes (the tokens-per-expert selector): an
+// expert with c routed rows runs in the smallest class with BM >= c; larger
+// experts (the shared expert at prefill) are split into BM=256 tiles.
+constexpr int kClassBM[] = {16, 32, 64, 128, 256};
+constexpr int kNumClasses = 5;
+
+struct W8A8Layout {
+  int64_t kt, routes, hp, ip;
+  TileClasses tc;
+  RouteBuffers rb;
+  int8_t* xq;
+  float* xs;
+  uint16_t* y;
+  int8_t* q2;
+  float* s2row;
+  float* route_out;
+};
+
+struct Bf16Layout {
+  int64_t kt, routes, hp, ip, gu_ld;
+  TileClasses tc;
+  RouteBuffers rb;
+  uint16_t* xpad;
+  uint16_t* y;
+  float* gate_up;
+  float* route_out;
+};
+
+int64_t tile_offset(const TileClasses& tc, int c) {
+  int64_t off = 0;
+  for (int i = 0; i < c; ++i) off += tc.bound[i];
+  return off;
+}
+
+int check_common(const fcmoe_moe_args* a) {
+  if (!a) return fail(FCMOE_EINVAL, "args is NULL");
+  if (a->tokens < 0 || a->hidden <= 0 || a->inter <= 0) return fail(FCMOE_EINVAL, "bad tokens/hidden/inter");
+  if (a->top_k < 0 || (a->top_k == 0 && a->shared_expert_id < 0)) return fail(FCMOE_EINVAL, "top_k must be positive");
+  if (a->experts <= 0 || a->experts > 1024) return fail(FCMOE_EINVAL, "experts must be in [1, 1024]");
+  if (a->valid_experts <= 0 || a->valid_experts > a->experts) return fail(FCMOE_EINVAL, "bad valid_experts");
+  if (a->shared_expert_id >= a->experts) return fail(FCMOE_EINVAL, "shared_expert_id out of range");
+  if (a->tokens > 0 && (!a->x || !a->out || !a->w13 || !a->w2)) return fail(FCMOE_EINVAL, "NULL tensor");
+  if (a->tokens > 0 && a->top_k > 0 && (!a->topk_ids || !a->topk_weights)) return fail(FCMOE_EINVAL, "NULL topk");
+  if (a->tokens > 65535) return fail(FCMOE_EINVAL, "tokens must be <= 65535");
+  return FCMOE_OK;
+}
+
+W8A8Layout w8a8_layout(const fcmoe_moe_args* a, Arena& ar) {
+  W8A8Layout L;
+  L.kt = a->top_k + (a->shared_expert_id >= 0 ? 1 : 0);
+  L.routes = a->tokens * L.kt;
+  L.hp = round_up(a->hidden, 64);
+  L.ip = round_up(a->inter, 64);
+  L.tc = make_tile_classes(kClassBM, kNumClasses, L.routes, a->experts);
+  route_take(ar, L.rb, L.routes, a->experts, L.tc);
+  L.xq = ar.take<int8_t>(a->tokens * L.hp);
+  L.xs = ar.take<float>(a->tokens);
+  L.y = ar.take<uint16_t>(L.routes * L.ip);
+  L.q2 = ar.take<int8_t>(L.routes * L.ip);
+  L.s2row = ar.take<float>(L.routes);
+  L.route_out = ar.take<float>(L.routes * a->hidden);
+  return L;
+}
+
+Bf16Layout bf16_layout(const fcmoe_moe_args* a, Arena& ar) {
+  Bf16Layout L;
+  L.kt = a->top_k + (a->shared_expert_id >= 0 ? 1 : 0);
+  L.routes = a->tokens * L.kt;
+  L.hp = round_up(a->hidden, 32);
+  L.ip = round_up(a->inter, 32);
+  L.gu_ld = 2 * round_up(a->inter, 16);
+  L.tc = make_tile_classes(kClassBM, kNumClasses, L.routes, a->experts);
+  route_take(ar, L.rb, L.routes, a->experts, L.tc);
+  L.xpad = (a->hidden % 32) ? ar.take<uint16_t>(a->tokens * L.hp) : nullptr;
+  L.y = ar.take<uint16_t>(L.routes * L.ip);
+  L.gate_up = a->activation == FCMOE_ACT_SWIGLUOAI ? ar.take<float>(L.routes * L.gu_ld) : nullptr;
+  L.route_out = ar.take<float>(L.routes * a->hidden);
+  return L;
+}
+
+__global__ void pad_rows_kernel(const uint16_t* x, int64_t rows, int64_t cols, int64_t ld, uint16_t* dst) {
+  const int64_t r = blockIdx.y;
+  const int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= rows || c >= ld) return;
+  dst[r * ld + c] = c < cols ? x[r * cols + c] : (uint16_t)0;
+}
+
+__global__ void single_expert_counts_kernel(int32_t* counts, int32_t* offsets, int32_t m) {
+  counts[0] = m;
+  offsets[0] = 0;
+  offsets[1] = m;
+}
+
+}  // namespace
+
+void set_error(const std::string& msg) { g_error = msg; }
+
+int fail(int code, const std::string& msg) {
+  g_error = msg;
+  return code;
+}
+
+int check_launch(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(FCMOE_EDEVICE, std::string(what) + ": " + hipGetErrorString(e));
+  return FCMOE_OK;
+}
+
+}  // namespace fcmoe
+
+using namespace fcmoe;
+
+extern "C" const char* fcmoe_last_error(void) { return g_error.c_str(); }
+
+extern "C" int fcmoe_abi_version(void) { return 1; }
+
+// ---------------------------------------------------------------- routing --
+
+extern "C" size_t fcmoe_route_workspace_bytes(int64_t tokens, int64_t top_k, int64_t experts, int64_t shared_id) {
+  Arena ar;
+  RouteBuffers rb;
+  const int64_t routes = tokens * (top_k + (shared_id >= 0 ? 1 : 0));
+  TileClasses tc = make_tile_classes(kClassBM, kNumClasses, routes, experts);
+  route_take(ar, rb, routes, experts, tc);
+  return ar.used + 256;
+}
+
+extern "C" int fcmoe_route_build(const void* topk_ids, int ids_is_i64, int64_t tokens, int64_t top_k,
+                                 int64_t experts, int64_t shared_id, int32_t* counts, int32_t* offsets,
+                                 int32_t* sorted_routes, int32_t* invalid_count, void* workspace,
+                                 size_t workspace_bytes, hipStream_t stream) {
+  if (tokens < 0 || top_k < 0 || experts <= 0 || experts > 1024 || shared_id >= experts)
+    return fail(FCMOE_EINVAL, "route_build: bad shape");
+  const int64_t kt = top_k + (shared_id >= 0 ? 1 : 0);
+  const int64_t routes = tokens * kt;
+  Arena ar;
+  ar.base = (char*)workspace;
+  ar.cap = workspace_bytes;
+  RouteBuffers rb;
+  TileClasses tc = make_tile_classes(kClassBM, kNumClasses, routes, experts);
+  route_take(ar, rb, routes, experts, tc);
+  if (!ar.ok()) return fail(FCMOE_ESPACE, "route_build: workspace too small");
+  if (routes == 0) return fail(FCMOE_EINVAL, "route_build: no routes");
+  int rc = route_launch(topk_ids, ids_is_i64, nullptr, tokens, top_k, experts, experts, shared_id, 1.0f, false, rb,
+                        tc, nullptr, stream);
+  if (rc) return rc;
+  // route_launch reads topk weights only for the combine; pass a dummy-safe
+  // path by copying results out.
+  if (hipMemcpyAsync(counts, rb.counts, experts * sizeof(int32_t), hipMemcpyDeviceToDevice, stream) != hipSuccess ||
+      hipMemcpyAsync(offsets, rb.offsets, (experts + 1) * sizeof(int32_t), hipMemcpyDeviceToDevice, stream) !=
+          hipSuccess ||
+      hipMemcpyAsync(sorted_routes, rb.sorted_routes, routes * sizeof(int32_t), hipMemcpyDeviceToDevice, stream) !=
+          hipSuccess ||
+      (invalid_count &&
+       hipMemcpyAsync(invalid_count, rb.invalid, sizeof(int32_t), hipMemcpyDeviceToDevice, stream) != hipSuccess))
+    return fail(FCMOE_EDEVICE, "route_build: copy failed");
+  return FCMOE_OK;
+}
+
+// ------------------------------------------------------------------ W8A8 --
+
+extern "C" size_t fcmoe_w8a8_workspace_bytes(const fcmoe_moe_args* a) {
+  if (check_common(a)) return 0;
+  Arena ar;
+  w8a8_layout(a, ar);
+  return ar.used + 256;
+}
+
+extern "C" int fcmoe_w8a8_forward(const fcmoe_moe_args* a, hipStream_t stream) {
+  int rc = check_common(a);
+  if (rc) return rc;
+  if (a->activation != FCMOE_ACT_SILU_CLAMP10)
+    return fail(FCMOE_EINVAL, "W8A8 supports only clamped SwiGLU with limit 10.0");
+  if (a->hidden % 16 || a->inter % 16) return fail(FCMOE_EINVAL, "W8A8 requires H and F to be multiples of 16");
+  if (a->skip_weighted) return fail(FCMOE_EINVAL, "W8A8 requires weighted TopK merge");
+  if (!a->w13_scale || !a->w2_scale) return fail(FCMOE_EINVAL, "W8A8 scales are NULL");
+  if (a->tokens == 0) return FCMOE_OK;
+  Arena ar;
+  ar.base = (char*)a->workspace;
+  ar.cap = a->workspace_bytes;
+  if (!ar.base) return fail(FCMOE_ESPACE, "workspace is NULL");
+  W8A8Layout L = w8a8_layout(a, ar);
+  if (!ar.ok()) return fail(FCMOE_ESPACE, "W8A8 workspace too small");
+  const int64_t H = a->hidden, I = a->inter;
+
+  rc = route_launch(a->topk_ids, a->ids_is_i64, a->topk_weights, a->tokens, a->top_k, a->experts, a->valid_experts,
+                    a->shared_expert_id, a->routed_scaling, a->shared_expert_id >= 0, L.rb, L.tc, a->invalid_count,
+                    stream);
+  if (rc) return rc;
+  rc = quant_rows_launch(a->x, 0, a->tokens, H, 0, L.xq, L.hp, L.xs, stream);
+  if (rc) return rc;
+
+  GemmParams g13{};
+  g13.a = L.xq;
+  g13.lda = L.hp;
+  g13.row_map = L.rb.row_token;
+  g13.offsets = L.rb.offsets;
+  g13.counts = L.rb.counts;
+  g13.w = a->w13;
+  g13.w_expert_bytes = fcmoe_packed_expert_bytes(1, 2 * I, H, 2);
+  g13.n = 2 * I;
+  g13.n_half = I;
+  g13.n_tiles = ceil_div(I, 16);
+  g13.k_chunks = L.hp / 64;
+  g13.n_groups = 2;
+  g13.out = L.y;
+  g13.ldo = L.ip;
+  g13.scale_row = L.xs;
+  g13.scale_col = a->w13_scale;
+  g13.rowmax = L.rb.rowmax;
+  for (int c = 0; c < L.tc.n; ++c) {
+    GemmParams p = g13;
+    p.tiles = L.rb.tiles + 2 * tile_offset(L.tc, c);
+    p.tile_count = L.rb.tile_count + c;
+    rc = gemm_launch(kEpiW13SwigluI8, L.tc.bm[c], p, L.tc.bound[c], stream);
+    if (rc) return rc;
+  }
+  rc = requant_launch(L.y, L.ip, L.routes, I, L.rb.rowmax, L.q2, L.ip, L.s2row, stream);
+  if (rc) return rc;
+
+  GemmParams g2{};
+  g2.a = L.q2;
+  g2.lda = L.ip;
+  g2.row_map = nullptr;
+  g2.offsets = L.rb.offsets;
+  g2.counts = L.rb.counts;
+  g2.w = a->w2;
+  g2.w_expert_bytes = fcmoe_packed_expert_bytes(1, H, I, 1);
+  g2.n = H;
+  g2.n_half = H;
+  g2.n_tiles = ceil_div(H, 16);
+  g2.k_chunks = L.ip / 64;
+  g2.n_groups = 1;
+  g2.out = L.route_out;
+  g2.ldo = H;
+  g2.scale_row = L.s2row;
+  g2.scale_col = a->w2_scale;
+  g2.sorted_routes = L.rb.sorted_routes;
+  for (int c = 0; c < L.tc.n; ++c) {
+    GemmParams p = g2;
+    p.tiles = L.rb.tiles + 2 * tile_offset(L.tc, c);
+    p.tile_count = L.rb.tile_count + c;
+    rc = gemm_launch(kEpiW2RouteI8, L.tc.bm[c], p, L.tc.bound[c], stream);
+    if (rc) return rc;
+  }
+  return combine_launch(L.route_out, L.rb.route_weight, L.rb.route_pos, a->tokens, L.kt, H, 0, 0, a->out, stream);
+}
+
+extern "C" int fcmoe_w8a8_stage_views(const fcmoe_moe_args* a, const int32_t** sorted_routes, const uint16_t** y,
+                                      int64_t* ldy, const int8_t** q2, int64_t* ldq, const float** s2row,
+                                      const float** route_out) {
+  int rc = check_common(a);
+  if (rc) return rc;
+  Arena ar;
+  ar.base = (char*)a->workspace;
+  ar.cap = a->workspace_bytes;
+  W8A8Layout L = w8a8_layout(a, ar);
+  if (!ar.ok() || !ar.base) return fail(FCMOE_ESPACE, "workspace too small");
+  if (sorted_routes) *sorted_routes = L.rb.sorted_routes;
+  if (y) *y = L.y;
+  if (ldy) *ldy = L.ip;
+  if (q2) *q2 = L.q2;
+  if (ldq) *ldq = L.ip;
+  if (s2row) *s2row = L.s2row;
+  if (route_out) *route_out = L.route_out;
+  return FCMOE_OK;
+}
+
+// ------------------------------------------------------------------ BF16 --
+
+extern "C" size_t fcmoe_bf16_workspace_bytes(const fcmoe_moe_args* a) {
+  if (check_common(a)) return 0;
+  Arena ar;
+  bf16_layout(a, ar);
+  return ar.used + 256;
+}
+
+extern "C" int fcmoe_bf16_forward(const fcmoe_moe_args* a, hipStream_t stream) {
+  int rc = check_common(a);
+  if (rc) return rc;
+  if (a->activation < FCMOE_ACT_SILU || a->activation > FCMOE_ACT_SILU_CLAMP10)
+    return fail(FCMOE_EINVAL, "unsupported activation");
+  const int64_t kt = a->top_k + (a->shared_expert_id >= 0 ? 1 : 0);
+  if (a->skip_weighted && kt != 1) return fail(FCMOE_EINVAL, "skip_weighted is only valid when top_k == 1");
+  if (a->tokens == 0) return FCMOE_OK;
+  Arena ar;
+  ar.base = (char*)a->workspace;
+  ar.cap = a->workspace_bytes;
+  if (!ar.base) return fail(FCMOE_ESPACE, "workspace is NULL");
+  Bf16Layout L = bf16_layout(a, ar);
+  if (!ar.ok()) return fail(FCMOE_ESPACE, "BF16 workspace too small");
+  const int64_t H = a->hidden, I = a->inter;
+
+  rc = route_launch(a->topk_ids, a->ids_is_i64, a->topk_weights, a->tokens, a->top_k, a->experts, a->valid_experts,
+                    a->shared_expert_id, a->routed_scaling, a->shared_expert_id >= 0 && a->top_k > 0, L.rb, L.tc,
+                    a->invalid_count, stream);
+  if (rc) return rc;
+  const uint16_t* xa = a->x;
+  if (L.xpad) {
+    hipLaunchKernelGGL(pad_rows_kernel, dim3((unsigned)ceil_div(L.hp, 256), (unsigned)a->tokens), dim3(256), 0,
+                       stream, a->x, a->tokens, H, L.hp, L.xpad);
+    if ((rc = check_launch("pad_rows"))) return rc;
+    xa = L.xpad;
+  }
+  // y columns [F, ip) feed W2's zero-padded K and must be finite zeros.
+  if (I % 32) {
+    rc = fill_u32_launch((uint32_t*)L.y, L.routes * L.ip / 2, 0u, stream);
+    if (rc) return rc;
+  }
+  const bool fused = a->activation != FCMOE_ACT_SWIGLUOAI;
+  GemmParams g13{};
+  g13.a = xa;
+  g13.lda = L.hp;
+  g13.row_map = L.rb.row_token;
+  g13.offsets = L.rb.offsets;
+  g13.counts = L.rb.counts;
+  g13.w = a->w13;
+  g13.w_expert_bytes = fcmoe_packed_expert_bytes(2, 2 * I, H, 2);
+  g13.n = 2 * I;
+  g13.n_half = I;
+  g13.n_tiles = ceil_div(I, 16);
+  g13.k_chunks = ceil_div(H * 2, 64);
+  g13.n_groups = 2;
+  g13.out = fused ? (void*)L.y : (void*)L.gate_up;
+  g13.ldo = fused ? L.ip : L.gu_ld;
+  g13.bias = a->w13_bias;
+  g13.activation = a->activation;
+  for (int c = 0; c < L.tc.n; ++c) {
+    GemmParams p = g13;
+    p.tiles = L.rb.tiles + 2 * tile_offset(L.tc, c);
+    p.tile_count = L.rb.tile_count + c;
+    rc = gemm_launch(fused ? kEpiW13ActBf16 : kEpiRawF32Bias, L.tc.bm[c], p, L.tc.bound[c], stream);
+    if (rc) return rc;
+  }
+  if (!fused) {
+    rc = act_bf16_launch(L.gate_up, L.gu_ld, L.routes, I, round_up(I, 16), a->activation, L.y, L.ip, stream);
+    if (rc) return rc;
+  }
+  GemmParams g2{};
+  g2.a = L.y;
+  g2.lda = L.ip;
+  g2.offsets = L.rb.offsets;
+  g2.counts = L.rb.counts;
+  g2.w = a->w2;
+  g2.w_expert_bytes = fcmoe_packed_expert_bytes(2, H, I, 1);
+  g2.n = H;
+  g2.n_half = H;
+  g2.n_tiles = ceil_div(H, 16);
+  g2.k_chunks = ceil_div(I * 2, 64);
+  g2.n_groups = 1;
+  g2.out = L.route_out;
+  g2.ldo = H;
+  g2.bias = a->w2_bias;
+  g2.sorted_routes = L.rb.sorted_routes;
+  for (int c = 0; c < L.tc.n; ++c) {
+    GemmParams p = g2;
+    p.tiles = L.rb.tiles + 2 * tile_offset(L.tc, c);
+    p.tile_count = L.rb.tile_count + c;
+    rc = gemm_launch(kEpiW2RouteBf16, L.tc.bm[c], p, L.tc.bound[c], stream);
+    if (rc) return rc;
+  }
+  const int tree = (kt == 2 || kt == 4 || kt == 6 || kt == 8) ? 1 : 0;
+  return combine_launch(L.route_out, L.rb.route_weight, L.rb.route_pos, a->tokens, kt, H, tree, a->skip_weighted,
+                        a->out, stream);
+}
+
+// ---------------------------------------------------------------- i8gemm --
+
+namespace {
+struct I8Layout {
+  int64_t kp;
+  TileClasses tc;
+  int8_t* xq;
+  float* xs;
+  int32_t* counts;
+  int32_t* offsets;
+  int32_t* tiles;
+  int32_t* tile_count;
+};
+I8Layout i8_layout(int64_t m, int64_t k, Arena& ar) {
+  I8Layout L;
+  L.kp = round_up(k, 64);
+  L.tc = make_tile_classes(kClassBM, kNumClasses, m, 1);
+  L.xq = ar.take<int8_t>(m * L.kp);
+  L.xs = ar.take<float>(m);
+  L.counts = ar.take<int32_t>(1);
+  L.offsets = ar.take<int32_t>(2);
+  int64_t t = 0;
+  for (int c = 0; c < L.tc.n; ++c) t += L.tc.bound[c];
+  L.tiles = ar.take<int32_t>(2 * t);
+  L.tile_count = ar.take<int32_t>(kMaxClasses);
+  return L;
+}
+}  // namespace
+
+extern "C" size_t fcmoe_i8gemm_workspace_bytes(int64_t m, int64_t k) {
+  Arena ar;
+  i8_layout(m, k, ar);
+  return ar.used + 256;
+}
+
+extern "C" int fcmoe_i8gemm(const void* x, int x_is_f32, int64_t m, int64_t k, const void* w_packed,
+                            const float* w_scale, int64_t n, const float* bias, void* out, int out_is_bf16,
+                            void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  if (m < 0 || k <= 0 || n <= 0 || !w_packed || !w_scale) return fail(FCMOE_EINVAL, "i8gemm: bad args");
+  if (m == 0) return FCMOE_OK;
+  if (m > INT32_MAX / 2) return fail(FCMOE_EINVAL, "i8gemm: too many rows");
+  Arena ar;
+  ar.base = (char*)workspace;
+  ar.cap = workspace_bytes;
+  I8Layout L = i8_layout(m, k, ar);
+  if (!ar.base || !ar.ok()) return fail(FCMOE_ESPACE, "i8gemm: workspace too small");
+  int rc = quant_rows_launch(x, x_is_f32, m, k, 1, L.xq, L.kp, L.xs, stream);
+  if (rc) return rc;
+  hipLaunchKernelGGL(single_expert_counts_kernel, dim3(1), dim3(1), 0, stream, L.counts, L.offsets, (int32_t)m);
+  if ((rc = check_launch("i8gemm counts"))) return rc;
+  rc = tiles_from_counts_launch(L.counts, 1, L.tc, L.tiles, L.tile_count, stream);
+  if (rc) return rc;
+  GemmParams g{};
+  g.a = L.xq;
+  g.lda = L.kp;
+  g.offsets = L.offsets;
+  g.counts = L.counts;
+  g.w = w_packed;
+  g.w_expert_bytes = fcmoe_packed_expert_bytes(1, n, k, 1);
+  g.n = n;
+  g.n_half = n;
+  g.n_tiles = ceil_div(n, 16);
+  g.k_chunks = L.kp / 64;
+  g.n_groups = 1;
+  g.out = out;
+  g.ldo = n;
+  g.scale_row = L.xs;
+  g.scale_col = w_scale;
+  g.bias = bias;
+  g.out_bf16 = out_is_bf16;
+  for (int c = 0; c < L.tc.n; ++c) {
+    GemmParams p = g;
+    p.tiles = L.tiles + 2 * tile_offset(L.tc, c);
+    p.tile_count = L.tile_count + c;
+    rc = gemm_launch(kEpiI8Gemm, L.tc.bm[c], p, L.tc.bound[c], stream);
+    if (rc) return rc;
+  }
+  return FCMOE_OK;
+}
+
+// ------------------------------------------------------------ diagnostics --
+
+extern "C" size_t fcmoe_grouped_gemm_workspace_bytes(int64_t experts, int64_t total_rows) {
+  TileClasses tc = make_tile_classes(kClassBM, kNumClasses, total_rows, experts);
+  int64_t t = 0;
+  for (int c = 0; c < tc.n; ++c) t += tc.bound[c];
+  return (size_t)(2 * t + kMaxClasses) * sizeof(int32_t) + 512;
+}
+
+extern "C" int fcmoe_grouped_gemm_i8_acc(const int8_t* a, int64_t lda, const int32_t* row_map, const int32_t* counts,
+                                         const int32_t* offsets, int64_t experts, int64_t total_rows,
+                                         const void* w_packed, int64_t n, int64_t k, int32_t* acc, void* workspace,
+                                         size_t workspace_bytes, hipStream_t stream) {
+  if (!a || !counts || !offsets || !w_packed || !acc || lda % 64 || lda < k || experts <= 0 || experts > 1024)
+    return fail(FCMOE_EINVAL, "grouped_gemm_i8_acc: bad args");
+  if (total_rows <= 0) return FCMOE_OK;
+  if (workspace_bytes < fcmoe_grouped_gemm_workspace_bytes(experts, total_rows) || !workspace)
+    return fail(FCMOE_ESPACE, "grouped_gemm_i8_acc: workspace too small");
+  TileClasses tc = make_tile_classes(kClassBM, kNumClasses, total_rows, experts);
+  Arena ar;
+  ar.base = (char*)workspace;
+  ar.cap = workspace_bytes;
+  int64_t t = 0;
+  for (int c = 0; c < tc.n; ++c) t += tc.bound[c];
+  int32_t* tiles = ar.take<int32_t>(2 * t);
+  int32_t* tile_count = ar.take<int32_t>(kMaxClasses);
+  int rc = tiles_from_counts_launch(counts, experts, tc, tiles, tile_count, stream);
+  if (rc) return rc;
+  GemmParams g{};
+  g.a = a;
+  g.lda = lda;
+  g.row_map = row_map;
+  g.offsets = offsets;
+  g.counts = counts;
+  g.w = w_packed;
+  g.w_expert_bytes = fcmoe_packed_expert_bytes(1, n, k, 1);
+  g.n = n;
+  g.n_half = n;
+  g.n_tiles = ceil_div(n, 16);
+  g.k_chunks = ceil_div(k, 64);
+  g.n_groups = 1;
+  g.out = acc;
+  g.ldo = n;
+  for (int c = 0; c < tc.n; ++c) {
+    GemmParams p = g;
+    p.tiles = tiles + 2 * tile_offset(tc, c);
+    p.tile_count = tile_count + c;
+    rc = gemm_launch(kEpiRawI32, tc.bm[c], p, tc.bound[c], stream);
+    if (rc) return rc;
+  }
+  return FCMOE_OK;
+}

@@ -1,0 +1,364 @@
+// fcmoe_gemm.hip -- grouped (per-expert) GEMM on CDNA4 MFMA with fused
+// epilogues. One template serves int8 (v_mfma_i32_16x16x64_i8, exact int32
+// accumulation) and bf16 (v_mfma_f32_16x16x32_bf16, fp32 accumulation).
+//
+// Work decomposition
+//   grid.x = tiles * n_blocks. A tile is (expert, first row) from the route
+//   kernel's per-class list; its BM rows are the expert's routed rows in
+//   sorted (ascending flat route) order. A workgroup is 4 wavefronts arranged
+//   WM x WN; a wave owns FM 16-row fragments x 4 16-channel tiles.
+//
+// Data movement
+//   B (weights, HBM-streamed, read once per M tile): packed offline in the
+//   exact MFMA operand order (1 KiB per 16-channel x 64-byte tile chunk), so
+//   each lane issues one 16-byte global load per tile per chunk, straight into
+//   registers, software-pipelined one K step ahead. No LDS round trip.
+//   A (routed activation rows, gathered through row_map): staged through
+//   double-buffered LDS (row stride 64*FK+16 bytes keeps the 16 rows of a
+//   ds_read_b128 on distinct banks), one barrier per K step.
+//
+// Operand order: lane l supplies row/column (l % 16) and bytes
+// [16*(l/16), 16*(l/16)+16) of the current 64-byte K chunk for both A and B;
+// since A and B use the same lane->K mapping, the products pair the same k
+// whatever the hardware's internal K order. D lane l, register i holds row
+// 4*(l/16)+i, column l%16.
+#include "fcmoe_device.h"
+#include "fcmoe_internal.h"
+
+namespace fcmoe {
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kFN = 4;  // 16-channel tiles per wave
+
+template <bool I8>
+struct Acc;
+template <>
+struct Acc<true> {
+  typedef v4i type;
+};
+template <>
+struct Acc<false> {
+  typedef v4f type;
+};
+
+__device__ __forceinline__ v4i mfma(v4i a, v4i b, v4i c) {
+  return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ v4f mfma(v8bf a, v8bf b, v4f c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float silu_f(float g) { return g / (1.0f + expf(-g)); }
+
+__device__ __forceinline__ float act_bf16_mode(float g, float u, int mode) {
+  if (mode == FCMOE_ACT_SILU_CLAMP10) {
+    g = fminf(g, 10.0f);
+    u = fmaxf(fminf(u, 10.0f), -10.0f);
+  }
+  if (mode == FCMOE_ACT_GELU) return 0.5f * g * (1.0f + erff(g * 0.70710678118654752440f)) * u;
+  return silu_f(g) * u;
+}
+
+template <bool I8, int EPI, int WM, int WN, int FM, int FK>
+__global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(GemmParams p, int n_blocks) {
+  constexpr int BM = WM * FM * 16;
+  constexpr int ROWB = FK * 64 + 16;               // LDS row stride (bytes)
+  constexpr int UNITS = BM * FK * 4;               // 16-byte A units per stage
+  constexpr int UPT = (UNITS + kThreads - 1) / kThreads;
+  constexpr bool PAIR = (EPI == kEpiW13SwigluI8 || EPI == kEpiW13ActBf16);
+  typedef typename Acc<I8>::type AccT;
+
+  __shared__ __attribute__((aligned(16))) uint8_t sA[2][BM * ROWB];
+
+  const int tile = blockIdx.x / n_blocks;
+  if (tile >= *p.tile_count) return;
+  const int nb = blockIdx.x - tile * n_blocks;
+  const int expert = p.tiles[2 * tile];
+  const int m0 = p.tiles[2 * tile + 1];
+  const int rows_left = p.counts[expert] - m0;
+  const int rows = rows_left < BM ? rows_left : BM;
+  const int pos0 = p.offsets[expert] + m0;
+
+  const int tid = threadIdx.x;
+  const int lane = tid % kWave;
+  const int wave = tid / kWave;
+  const int wm = wave / WN;
+  const int wn = wave % WN;
+
+  // ---- this wave's four channel tiles (global tile index within expert)
+  int64_t gtile[kFN];
+  bool tvalid[kFN];
+  const int64_t total_tiles = (int64_t)p.n_groups * p.n_tiles;
+  if (PAIR) {
+    const int64_t pair0 = ((int64_t)nb * WN + wn) * 2;
+#pragma unroll
+    for (int j = 0; j < kFN; ++j) {
+      const int64_t pr = pair0 + (j & 1);
+      tvalid[j] = pr < p.n_tiles;
+      gtile[j] = (j < 2 ? 0 : p.n_tiles) + pr;
+    }
+  } else {
+    const int64_t t0 = ((int64_t)nb * WN + wn) * kFN;
+#pragma unroll
+    for (int j = 0; j < kFN; ++j) {
+      gtile[j] = t0 + j;
+      tvalid[j] = gtile[j] < total_tiles;
+    }
+  }
+  const uint8_t* wbase = (const uint8_t*)p.w + (int64_t)expert * p.w_expert_bytes;
+  const uint4* bptr[kFN];
+#pragma unroll
+  for (int j = 0; j < kFN; ++j)
+    bptr[j] = (const uint4*)(wbase + (tvalid[j] ? gtile[j] : 0) * p.k_chunks * 1024) + lane;
+
+  // ---- A loader assignment
+  const int64_t lda_bytes = p.lda * (I8 ? 1 : 2);
+  const uint8_t* asrc[UPT];
+  int adst[UPT];
+  int acol[UPT];
+#pragma unroll
+  for (int u = 0; u < UPT; ++u) {
+    const int unit = tid + u * kThreads;
+    asrc[u] = nullptr;
+    adst[u] = -1;
+    acol[u] = 0;
+    if (unit < UNITS) {
+      const int r = unit / (FK * 4);
+      const int c16 = unit % (FK * 4);
+      adst[u] = r * ROWB + c16 * 16;
+      acol[u] = c16 * 16;
+      if (r < rows) {
+        const int pos = pos0 + r;
+        const int64_t arow = p.row_map ? (int64_t)p.row_map[pos] : (int64_t)pos;
+        asrc[u] = (const uint8_t*)p.a + arow * lda_bytes;
+      }
+    }
+  }
+
+  const int64_t k_steps = ceil_div(p.k_chunks, FK);
+  uint4 areg[UPT];
+  uint4 breg[FK][kFN];
+  uint4 bnext[FK][kFN];
+
+  auto load_a = [&](int64_t step) {
+#pragma unroll
+    for (int u = 0; u < UPT; ++u) {
+      const int64_t off = step * FK * 64 + acol[u];
+      if (asrc[u] && off < p.k_chunks * 64)
+        areg[u] = *(const uint4*)(asrc[u] + off);
+      else
+        areg[u] = make_uint4(0, 0, 0, 0);
+    }
+  };
+  auto store_a = [&](int buf) {
+#pragma unroll
+    for (int u = 0; u < UPT; ++u)
+      if (adst[u] >= 0) *(uint4*)(&sA[buf][adst[u]]) = areg[u];
+  };
+  auto load_b = [&](int64_t step, uint4 (&dst)[FK][kFN]) {
+#pragma unroll
+    for (int c = 0; c < FK; ++c) {
+      const int64_t chunk = step * FK + c;
+#pragma unroll
+      for (int j = 0; j < kFN; ++j) {
+        if (tvalid[j] && chunk < p.k_chunks)
+          dst[c][j] = bptr[j][chunk * kWave];
+        else
+          dst[c][j] = make_uint4(0, 0, 0, 0);
+      }
+    }
+  };
+
+  AccT acc[FM][kFN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < kFN; ++j) acc[i][j] = AccT{0, 0, 0, 0};
+
+  load_a(0);
+  load_b(0, breg);
+  store_a(0);
+  for (int64_t s = 0; s < k_steps; ++s) {
+    const int buf = (int)(s & 1);
+    const bool more = s + 1 < k_steps;
+    if (more) {
+      load_a(s + 1);
+      load_b(s + 1, bnext);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < FK; ++c) {
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        const int r = wm * FM * 16 + i * 16 + (lane % 16);
+        const uint4 av = *(const uint4*)(&sA[buf][r * ROWB + c * 64 + (lane / 16) * 16]);
+#pragma unroll
+        for (int j = 0; j < kFN; ++j) {
+          if constexpr (I8) {
+            acc[i][j] = mfma(__builtin_bit_cast(v4i, av), __builtin_bit_cast(v4i, breg[c][j]), acc[i][j]);
+          } else {
+            acc[i][j] = mfma(__builtin_bit_cast(v8bf, av), __builtin_bit_cast(v8bf, breg[c][j]), acc[i][j]);
+          }
+        }
+      }
+    }
+    if (more) {
+      store_a(buf ^ 1);
+#pragma unroll
+      for (int c = 0; c < FK; ++c)
+#pragma unroll
+        for (int j = 0; j < kFN; ++j) breg[c][j] = bnext[c][j];
+    }
+  }
+
+  // ---- epilogues
+  const int col = lane % 16;
+  if constexpr (EPI == kEpiW13SwigluI8 || EPI == kEpiW13ActBf16) {
+    const int64_t n = p.n;  // 2F logical
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int r = wm * FM * 16 + i * 16 + (lane / 16) * 4 + q;
+        const bool rok = r < rows;
+        const int pos = pos0 + r;
+        float amax = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int64_t f = (gtile[j]) * 16 + col;  // gate channel (group 0)
+          if (!(rok && tvalid[j] && f < p.n_half)) continue;
+          float y;
+          if constexpr (EPI == kEpiW13SwigluI8) {
+            // w13_epilogue, csrc/moe/arm/i8mm_w8a8/kernels.cpp:230-246.
+            const float xs = p.scale_row[p.row_map ? p.row_map[pos] : pos];
+            const float* sc = p.scale_col + (int64_t)expert * n;
+            float gate = (float)acc[i][j][q] * (xs * sc[f]);
+            float up = (float)acc[i][j + 2][q] * (xs * sc[p.n_half + f]);
+            gate = fminf(gate, 10.0f);
+            up = fmaxf(fminf(up, 10.0f), -10.0f);
+            const float ex = fexpa_exp_neg(gate);
+            y = (gate * up) / (ex + 1.0f);
+          } else {
+            float gate = acc[i][j][q];
+            float up = acc[i][j + 2][q];
+            if (p.bias) {
+              gate = gate + p.bias[(int64_t)expert * n + f];
+              up = up + p.bias[(int64_t)expert * n + p.n_half + f];
+            }
+            y = act_bf16_mode(gate, up, p.activation);
+          }
+          const uint16_t yb = f32_to_bf16(y);
+          ((uint16_t*)p.out)[(int64_t)pos * p.ldo + f] = yb;
+          amax = fmaxf(amax, fabsf(bf16_to_f32(yb)));
+        }
+        if constexpr (EPI == kEpiW13SwigluI8) {
+          amax = max16(amax);
+          if (rok && col == 0) atomicMax(p.rowmax + pos, __float_as_uint(amax));
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int r = wm * FM * 16 + i * 16 + (lane / 16) * 4 + q;
+        if (r >= rows) continue;
+        const int pos = pos0 + r;
+#pragma unroll
+        for (int j = 0; j < kFN; ++j) {
+          if (!tvalid[j]) continue;
+          const int64_t g = gtile[j] / p.n_tiles;
+          const int64_t t = gtile[j] - g * p.n_tiles;
+          const int64_t cin = t * 16 + col;
+          if (cin >= p.n_half) continue;
+          const int64_t ch = g * p.n_half + cin;  // logical channel
+          if constexpr (EPI == kEpiRawI32) {
+            ((int32_t*)p.out)[(int64_t)pos * p.ldo + ch] = (int32_t)acc[i][j][q];
+          } else if constexpr (EPI == kEpiW2RouteI8) {
+            // store_w2, csrc/moe/arm/i8mm_w8a8/kernels.cpp:248-257.
+            const int64_t route = p.sorted_routes[pos];
+            const float v = (float)acc[i][j][q] * (p.scale_row[pos] * p.scale_col[(int64_t)expert * p.n + ch]);
+            ((float*)p.out)[route * p.ldo + ch] = v;
+          } else if constexpr (EPI == kEpiI8Gemm) {
+            // write_scaled_output, csrc/i8gemm.cpp:148-164 (left to right).
+            float v = (float)acc[i][j][q] * p.scale_row[pos] * p.scale_col[ch];
+            if (p.bias) v = v + p.bias[ch];
+            if (p.out_bf16)
+              ((uint16_t*)p.out)[(int64_t)pos * p.ldo + ch] = f32_to_bf16(v);
+            else
+              ((float*)p.out)[(int64_t)pos * p.ldo + ch] = v;
+          } else if constexpr (EPI == kEpiRawF32Bias) {
+            float v = acc[i][j][q];
+            if (p.bias) v = v + p.bias[(int64_t)expert * p.n + ch];
+            ((float*)p.out)[(int64_t)pos * p.ldo + gtile[j] * 16 + col] = v;  // packed channel order
+          } else if constexpr (EPI == kEpiW2RouteBf16) {
+            float v = acc[i][j][q];
+            if (p.bias) v = v + p.bias[(int64_t)expert * p.n + ch];
+            const int64_t route = p.sorted_routes[pos];
+            ((float*)p.out)[route * p.ldo + ch] = v;
+          }
+        }
+      }
+    }
+  }
+}
+
+template <bool I8, int EPI, int WM, int WN, int FM, int FK>
+int launch_cfg(const GemmParams& p, int64_t max_tiles, hipStream_t stream) {
+  constexpr bool PAIR = (EPI == kEpiW13SwigluI8 || EPI == kEpiW13ActBf16);
+  const int64_t per_block = PAIR ? 2 * WN : kFN * WN;
+  const int64_t units = PAIR ? p.n_tiles : (int64_t)p.n_groups * p.n_tiles;
+  const int64_t n_blocks = ceil_div(units, per_block);
+  const int64_t grid = max_tiles * n_blocks;
+  if (grid <= 0) return FCMOE_OK;
+  if (grid > INT32_MAX) return fail(FCMOE_EINVAL, "grouped gemm grid too large");
+  hipLaunchKernelGGL((grouped_gemm_kernel<I8, EPI, WM, WN, FM, FK>), dim3((unsigned)grid), dim3(kThreads), 0, stream,
+                     p, (int)n_blocks);
+  return check_launch("grouped_gemm");
+}
+
+template <bool I8, int EPI>
+int launch_bm(int bm, const GemmParams& p, int64_t max_tiles, hipStream_t stream) {
+  switch (bm) {
+    case 16:
+      return launch_cfg<I8, EPI, 1, 4, 1, 2>(p, max_tiles, stream);
+    case 32:
+      return launch_cfg<I8, EPI, 1, 4, 2, 2>(p, max_tiles, stream);
+    case 64:
+      return launch_cfg<I8, EPI, 1, 4, 4, 1>(p, max_tiles, stream);
+    case 128:
+      return launch_cfg<I8, EPI, 2, 2, 4, 1>(p, max_tiles, stream);
+    case 256:
+      return launch_cfg<I8, EPI, 2, 2, 8, 1>(p, max_tiles, stream);
+    default:
+      return fail(FCMOE_EINVAL, "unsupported tile rows");
+  }
+}
+
+}  // namespace
+
+int gemm_launch(int epi, int bm, const GemmParams& p, int64_t max_tiles, hipStream_t stream) {
+  switch (epi) {
+    case kEpiRawI32:
+      return launch_bm<true, kEpiRawI32>(bm, p, max_tiles, stream);
+    case kEpiW13SwigluI8:
+      return launch_bm<true, kEpiW13SwigluI8>(bm, p, max_tiles, stream);
+    case kEpiW2RouteI8:
+      return launch_bm<true, kEpiW2RouteI8>(bm, p, max_tiles, stream);
+    case kEpiI8Gemm:
+      return launch_bm<true, kEpiI8Gemm>(bm, p, max_tiles, stream);
+    case kEpiW13ActBf16:
+      return launch_bm<false, kEpiW13ActBf16>(bm, p, max_tiles, stream);
+    case kEpiRawF32Bias:
+      return launch_bm<false, kEpiRawF32Bias>(bm, p, max_tiles, stream);
+    case kEpiW2RouteBf16:
+      return launch_bm<false, kEpiW2RouteBf16>(bm, p, max_tiles, stream);
+    default:
+      return fail(FCMOE_EINVAL, "unknown epilogue");
+  }
+}
+
+}  // namespace fcmoe

@@ -1,0 +1,119 @@
+// fcmoe_internal.h -- host-side declarations shared by the libfcmoe sources.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "../../include/fcmoe.h"
+
+namespace fcmoe {
+
+// Thread-local error message plumbing for fcmoe_last_error().
+void set_error(const std::string& msg);
+int fail(int code, const std::string& msg);
+int check_launch(const char* what);
+
+// Bump allocator over a caller-provided workspace; 256-byte aligned slices.
+struct Arena {
+  char* base = nullptr;
+  size_t cap = 0;
+  size_t used = 0;
+  template <typename T>
+  T* take(int64_t count) {
+    size_t bytes = (size_t)(count > 0 ? count : 1) * sizeof(T);
+    size_t off = (used + 255) & ~(size_t)255;
+    used = off + bytes;
+    return base ? reinterpret_cast<T*>(base + off) : nullptr;
+  }
+  bool ok() const { return base == nullptr || used <= cap; }
+};
+
+// ---- routing (fcmoe_route.hip) ----
+// Tile classes: experts are assigned to the smallest class whose BM covers
+// their row count (the last class takes the rest, in several M tiles).
+constexpr int kMaxClasses = 6;
+struct TileClasses {
+  int n = 0;
+  int bm[kMaxClasses] = {0};
+  int64_t bound[kMaxClasses] = {0};  // max tiles a class can receive
+};
+TileClasses make_tile_classes(const int* bms, int n, int64_t routes, int64_t experts);
+
+struct RouteBuffers {
+  int32_t* chunk_hist = nullptr;     // [chunks, experts]
+  int32_t* counts = nullptr;         // [experts]
+  int32_t* offsets = nullptr;        // [experts + 1]
+  int32_t* sorted_routes = nullptr;  // [routes]  sorted position -> flat route
+  int32_t* row_token = nullptr;      // [routes]  sorted position -> token
+  int32_t* route_pos = nullptr;      // [routes]  flat route -> sorted position (-1 invalid)
+  float* route_weight = nullptr;     // [routes]  combined routing weight
+  uint32_t* rowmax = nullptr;        // [routes]  zeroed per call (W13 epilogue row max)
+  int32_t* tiles = nullptr;          // [classes][bound][2] (expert, m_begin)
+  int32_t* tile_count = nullptr;     // [classes]
+  int32_t* invalid = nullptr;        // [1]
+};
+constexpr int kRouteChunk = 256;
+void route_take(Arena& a, RouteBuffers& rb, int64_t routes, int64_t experts, const TileClasses& tc);
+int route_launch(const void* ids, int ids_is_i64, const float* topk_w, int64_t tokens, int64_t top_k,
+                 int64_t experts, int64_t valid_experts, int64_t shared_id, float routed_scale, bool scale_routed,
+                 const RouteBuffers& rb, const TileClasses& tc, int32_t* invalid_out, hipStream_t stream);
+
+int tiles_from_counts_launch(const int32_t* counts, int64_t experts, const TileClasses& tc, int32_t* tiles,
+                             int32_t* tile_count, hipStream_t stream);
+
+// ---- quantisation / packing (fcmoe_quant.hip) ----
+int fill_u32_launch(uint32_t* p, int64_t n, uint32_t v, hipStream_t stream);
+int quant_rows_launch(const void* x, int x_is_f32, int64_t rows, int64_t cols, int rounding, int8_t* q, int64_t ldq,
+                      float* scales, hipStream_t stream);
+int requant_launch(const uint16_t* y, int64_t ldy, int64_t rows, int64_t cols, const uint32_t* rowmax, int8_t* q,
+                   int64_t ldq, float* scales, hipStream_t stream);
+int act_bf16_launch(const float* gate_up, int64_t ldg, int64_t rows, int64_t f, int64_t fp16, int mode, uint16_t* y,
+                    int64_t ldy, hipStream_t stream);
+
+// ---- grouped GEMM (fcmoe_gemm.hip) ----
+enum Epilogue : int {
+  kEpiRawI32 = 0,     // int8: store raw int32 accumulators
+  kEpiW13SwigluI8,    // int8: clamped SwiGLU (FEXPA exp) -> bf16 y + row max
+  kEpiW2RouteI8,      // int8: acc * (s_row * s_w) -> fp32 route rows
+  kEpiI8Gemm,         // int8: acc * xs * ws (+bias) -> bf16 / fp32 output
+  kEpiW13ActBf16,     // bf16: acc (+bias) -> activation -> bf16 y
+  kEpiRawF32Bias,     // bf16: acc (+bias) -> fp32 gate_up (natural channel order)
+  kEpiW2RouteBf16,    // bf16: acc (+bias) -> fp32 route rows
+};
+
+struct GemmParams {
+  const void* a;             // int8 or bf16 rows
+  int64_t lda;               // row stride in elements (a multiple of 64 bytes)
+  const int32_t* row_map;    // sorted position -> A row (NULL: identity)
+  const int32_t* offsets;    // [experts+1] first sorted position of each expert
+  const int32_t* counts;     // [experts]
+  const int32_t* tiles;      // (expert, m_begin) pairs for this class
+  const int32_t* tile_count; // number of valid tiles
+  const void* w;             // packed weights
+  int64_t w_expert_bytes;    // bytes per expert
+  int64_t n;                 // logical output channels (W13: 2F)
+  int64_t n_half;            // W13: F (channels per gate/up group); else n
+  int64_t n_tiles;           // 16-channel tiles per group (padded)
+  int64_t k_chunks;          // 64-byte K chunks
+  int n_groups;              // 2 for gate/up W13, else 1
+  // epilogue
+  void* out;                 // destination
+  int64_t ldo;               // row stride of out (elements)
+  const float* scale_row;    // per sorted row (or per A row) scale
+  const float* scale_col;    // per expert per channel scale [experts, n]
+  const float* bias;         // [experts, n] (bf16 path / i8gemm)
+  uint32_t* rowmax;          // W13 int8: per sorted row max |y| (float bits)
+  const int32_t* sorted_routes;  // W2: sorted position -> flat route
+  int activation;            // bf16 W13
+  int out_bf16;              // i8gemm output dtype
+};
+
+int gemm_launch(int epi, int bm, const GemmParams& p, int64_t max_tiles, hipStream_t stream);
+
+// ---- combine (fcmoe_combine.hip) ----
+int combine_launch(const float* route_out, const float* route_weight, const int32_t* route_pos, int64_t tokens,
+                   int64_t kt, int64_t hidden, int tree, int skip_weighted, uint16_t* out, hipStream_t stream);
+
+}  // namespace fcmoe

@@ -1,0 +1,294 @@
+// fcmoe_route.hip -- top-k route build on the GPU.
+//
+// Semantics (bit-exact target): for every expert, the list of flat routes
+// r = t*kt + s routed to it, in ascending r. This is the order in which the
+// reference builds its per-expert route vectors
+// (csrc/moe/arm/i8mm_w8a8/kernels.cpp:583-592,
+//  csrc/moe/arm/common/fused_moe_bf16_tiled.cpp:6454-6483). Slot s == top_k is
+// the appended shared expert with weight 1.0 and the routed weights are scaled
+// by routed_scaling_factor (src/fused_cpp/moe/bf16_tiled.py:1007-1013).
+//
+// Three launches, all O(routes):
+//   1. count:   per 256-route chunk, an LDS histogram over experts.
+//   2. scan:    one block: per-expert exclusive scan over chunks, exclusive
+//               scan over experts (offsets), and the per-tile-class work lists
+//               for the grouped GEMMs (the tokens-per-expert tile selector).
+//   3. scatter: per chunk, the in-chunk rank of each route among earlier
+//               routes of the same expert gives its stable sorted position.
+#include "fcmoe_device.h"
+#include "fcmoe_internal.h"
+
+namespace fcmoe {
+
+namespace {
+
+constexpr int kScanThreads = 1024;
+constexpr int kMaxExperts = 1024;
+
+struct RouteArgs {
+  const void* ids;
+  int ids_is_i64;
+  const float* topk_w;
+  int64_t tokens;
+  int top_k;
+  int kt;
+  int experts;        // total prepared experts (histogram width)
+  int valid_experts;  // routed ids must be < this
+  int shared_id;      // -1 none
+  float scale;
+  int scale_routed;
+};
+
+__device__ __forceinline__ int route_expert(const RouteArgs& a, int64_t r, bool* valid) {
+  const int64_t t = r / a.kt;
+  const int s = (int)(r - t * a.kt);
+  if (s >= a.top_k) {
+    *valid = true;
+    return a.shared_id;
+  }
+  const int64_t idx = t * a.top_k + s;
+  int64_t e = a.ids_is_i64 ? ((const int64_t*)a.ids)[idx] : (int64_t)((const int32_t*)a.ids)[idx];
+  *valid = e >= 0 && e < a.valid_experts;
+  return *valid ? (int)e : -1;
+}
+
+__global__ __launch_bounds__(kRouteChunk) void route_count_kernel(RouteArgs a, int64_t routes, int32_t* chunk_hist,
+                                                                   float* route_weight, int32_t* invalid) {
+  extern __shared__ int32_t hist[];
+  const int tid = threadIdx.x;
+  for (int e = tid; e < a.experts; e += kRouteChunk) hist[e] = 0;
+  __syncthreads();
+  const int64_t r = (int64_t)blockIdx.x * kRouteChunk + tid;
+  if (r < routes) {
+    bool valid;
+    const int e = route_expert(a, r, &valid);
+    const int64_t t = r / a.kt;
+    const int s = (int)(r - t * a.kt);
+    float w = 1.0f;
+    if (s < a.top_k) {
+      w = a.topk_w ? a.topk_w[t * a.top_k + s] : 1.0f;
+      if (a.scale_routed) w = w * a.scale;
+    }
+    route_weight[r] = w;
+    if (valid)
+      atomicAdd(&hist[e], 1);
+    else
+      atomicAdd(invalid, 1);
+  }
+  __syncthreads();
+  int32_t* dst = chunk_hist + (int64_t)blockIdx.x * a.experts;
+  for (int e = tid; e < a.experts; e += kRouteChunk) dst[e] = hist[e];
+}
+
+struct ClassArgs {
+  int n;
+  int bm[kMaxClasses];
+  int64_t bound[kMaxClasses];
+};
+
+// Block-wide exclusive scan over 1024 threads; returns the total in *total.
+__device__ int block_exclusive_scan(int v, int* total) {
+  __shared__ int wave_tot[kScanThreads / kWave];
+  const int lane = threadIdx.x % kWave;
+  const int wid = threadIdx.x / kWave;
+  int incl = v;
+  for (int o = 1; o < kWave; o <<= 1) {
+    int n = __shfl_up(incl, o);
+    if (lane >= o) incl += n;
+  }
+  if (lane == kWave - 1) wave_tot[wid] = incl;
+  __syncthreads();
+  int base = 0, all = 0;
+  for (int w = 0; w < kScanThreads / kWave; ++w) {
+    int x = wave_tot[w];
+    if (w < wid) base += x;
+    all += x;
+  }
+  __syncthreads();
+  *total = all;
+  return base + incl - v;
+}
+
+// Appends this expert's (expert, m_begin) tiles to the list of the smallest
+// class whose BM covers its row count (the last class splits larger experts).
+// Called by all 1024 threads of the block (contains block scans).
+__device__ void emit_tiles(int count, int e, const ClassArgs& cls, int32_t* tiles, int32_t* tile_count) {
+  int my_class = -1;
+  if (count > 0) {
+    my_class = cls.n - 1;
+    for (int c = 0; c < cls.n; ++c) {
+      if (count <= cls.bm[c]) {
+        my_class = c;
+        break;
+      }
+    }
+  }
+  int64_t class_base = 0;
+  for (int c = 0; c < cls.n; ++c) {
+    const int nt = (my_class == c) ? (count + cls.bm[c] - 1) / cls.bm[c] : 0;
+    int ctotal;
+    const int base = block_exclusive_scan(nt, &ctotal);
+    int32_t* list = tiles + class_base * 2;
+    for (int j = 0; j < nt; ++j) {
+      if (base + j < cls.bound[c]) {
+        list[(base + j) * 2] = e;
+        list[(base + j) * 2 + 1] = j * cls.bm[c];
+      }
+    }
+    if (threadIdx.x == 0) tile_count[c] = ctotal < cls.bound[c] ? ctotal : (int)cls.bound[c];
+    class_base += cls.bound[c];
+  }
+}
+
+// Tile lists from per-expert counts already on the device (single expert
+// GEMMs and the accumulator diagnostic).
+__global__ __launch_bounds__(kScanThreads) void tiles_from_counts_kernel(const int32_t* counts, int experts,
+                                                                          ClassArgs cls, int32_t* tiles,
+                                                                          int32_t* tile_count) {
+  const int e = threadIdx.x;
+  emit_tiles(e < experts ? counts[e] : 0, e, cls, tiles, tile_count);
+}
+
+__global__ __launch_bounds__(kScanThreads) void route_scan_kernel(int experts, int64_t chunks, int32_t* chunk_hist,
+                                                                   int32_t* counts, int32_t* offsets,
+                                                                   ClassArgs cls, int32_t* tiles,
+                                                                   int32_t* tile_count) {
+  const int e = threadIdx.x;
+  int count = 0;
+  if (e < experts) {
+    int running = 0;
+    for (int64_t c = 0; c < chunks; ++c) {
+      int32_t* p = chunk_hist + c * experts + e;
+      const int v = *p;
+      *p = running;
+      running += v;
+    }
+    count = running;
+    counts[e] = count;
+  }
+  int total;
+  const int off = block_exclusive_scan(count, &total);
+  if (e < experts) offsets[e] = off;
+  if (e == 0) offsets[experts] = total;
+  emit_tiles(e < experts ? count : 0, e, cls, tiles, tile_count);
+}
+
+__global__ __launch_bounds__(kRouteChunk) void route_scatter_kernel(RouteArgs a, int64_t routes,
+                                                                     const int32_t* chunk_hist,
+                                                                     const int32_t* offsets, int32_t* sorted_routes,
+                                                                     int32_t* row_token, int32_t* route_pos,
+                                                                     uint32_t* rowmax) {
+  __shared__ int32_t ex[kRouteChunk];
+  const int tid = threadIdx.x;
+  const int64_t r = (int64_t)blockIdx.x * kRouteChunk + tid;
+  int e = -1;
+  if (r < routes) {
+    bool valid;
+    e = route_expert(a, r, &valid);
+  }
+  ex[tid] = e;
+  __syncthreads();
+  if (r >= routes) return;
+  if (e < 0) {
+    route_pos[r] = -1;
+    return;
+  }
+  int rank = 0;
+  for (int j = 0; j < tid; ++j) rank += (ex[j] == e) ? 1 : 0;
+  const int pos = offsets[e] + chunk_hist[(int64_t)blockIdx.x * a.experts + e] + rank;
+  sorted_routes[pos] = (int32_t)r;
+  row_token[pos] = (int32_t)(r / a.kt);
+  route_pos[r] = pos;
+  if (rowmax) rowmax[pos] = 0u;
+}
+
+ClassArgs class_args(const TileClasses& tc) {
+  ClassArgs ca;
+  ca.n = tc.n;
+  for (int c = 0; c < kMaxClasses; ++c) {
+    ca.bm[c] = tc.bm[c];
+    ca.bound[c] = tc.bound[c];
+  }
+  return ca;
+}
+
+}  // namespace
+
+int tiles_from_counts_launch(const int32_t* counts, int64_t experts, const TileClasses& tc, int32_t* tiles,
+                             int32_t* tile_count, hipStream_t stream) {
+  if (experts <= 0 || experts > kMaxExperts) return fail(FCMOE_EINVAL, "experts must be in [1, 1024]");
+  hipLaunchKernelGGL(tiles_from_counts_kernel, dim3(1), dim3(kScanThreads), 0, stream, counts, (int)experts,
+                     class_args(tc), tiles, tile_count);
+  return check_launch("tiles_from_counts");
+}
+
+TileClasses make_tile_classes(const int* bms, int n, int64_t routes, int64_t experts) {
+  TileClasses tc;
+  tc.n = n;
+  for (int c = 0; c < n; ++c) {
+    tc.bm[c] = bms[c];
+    // Experts in class c have more than bm[c-1] rows (class 0: at least one).
+    const int64_t lower = c == 0 ? 1 : (int64_t)bms[c - 1] + 1;
+    int64_t ex = routes / lower;
+    if (ex > experts) ex = experts;
+    int64_t bound = ex;
+    if (c == n - 1) bound = ex + ceil_div(routes, bms[c]);  // multi-tile experts
+    tc.bound[c] = bound > 0 ? bound : 1;
+  }
+  return tc;
+}
+
+void route_take(Arena& ar, RouteBuffers& rb, int64_t routes, int64_t experts, const TileClasses& tc) {
+  const int64_t chunks = ceil_div(routes, kRouteChunk);
+  rb.chunk_hist = ar.take<int32_t>(chunks * experts);
+  rb.counts = ar.take<int32_t>(experts);
+  rb.offsets = ar.take<int32_t>(experts + 1);
+  rb.sorted_routes = ar.take<int32_t>(routes);
+  rb.row_token = ar.take<int32_t>(routes);
+  rb.route_pos = ar.take<int32_t>(routes);
+  rb.route_weight = ar.take<float>(routes);
+  rb.rowmax = ar.take<uint32_t>(routes);
+  int64_t tiles = 0;
+  for (int c = 0; c < tc.n; ++c) tiles += tc.bound[c];
+  rb.tiles = ar.take<int32_t>(2 * tiles);
+  rb.tile_count = ar.take<int32_t>(kMaxClasses);
+  rb.invalid = ar.take<int32_t>(1);
+}
+
+int route_launch(const void* ids, int ids_is_i64, const float* topk_w, int64_t tokens, int64_t top_k,
+                 int64_t experts, int64_t valid_experts, int64_t shared_id, float routed_scale, bool scale_routed,
+                 const RouteBuffers& rb, const TileClasses& tc, int32_t* invalid_out, hipStream_t stream) {
+  if (experts <= 0 || experts > kMaxExperts) return fail(FCMOE_EINVAL, "experts must be in [1, 1024]");
+  const int64_t kt = top_k + (shared_id >= 0 ? 1 : 0);
+  const int64_t routes = tokens * kt;
+  if (routes <= 0) return FCMOE_OK;
+  if (routes > INT32_MAX / 2) return fail(FCMOE_EINVAL, "too many routes");
+  RouteArgs a;
+  a.ids = ids;
+  a.ids_is_i64 = ids_is_i64;
+  a.topk_w = topk_w;
+  a.tokens = tokens;
+  a.top_k = (int)top_k;
+  a.kt = (int)kt;
+  a.experts = (int)experts;
+  a.valid_experts = (int)valid_experts;
+  a.shared_id = (int)shared_id;
+  a.scale = routed_scale;
+  a.scale_routed = scale_routed ? 1 : 0;
+  const int64_t chunks = ceil_div(routes, kRouteChunk);
+  int32_t* invalid = invalid_out ? invalid_out : rb.invalid;
+  if (!invalid_out) {
+    const int rc = fill_u32_launch((uint32_t*)rb.invalid, 1, 0u, stream);
+    if (rc) return rc;
+  }
+  hipLaunchKernelGGL(route_count_kernel, dim3((unsigned)chunks), dim3(kRouteChunk), experts * sizeof(int32_t),
+                     stream, a, routes, rb.chunk_hist, rb.route_weight, invalid);
+  const ClassArgs ca = class_args(tc);
+  hipLaunchKernelGGL(route_scan_kernel, dim3(1), dim3(kScanThreads), 0, stream, (int)experts, chunks,
+                     rb.chunk_hist, rb.counts, rb.offsets, ca, rb.tiles, rb.tile_count);
+  hipLaunchKernelGGL(route_scatter_kernel, dim3((unsigned)chunks), dim3(kRouteChunk), 0, stream, a, routes,
+                     rb.chunk_hist, rb.offsets, rb.sorted_routes, rb.row_token, rb.route_pos, rb.rowmax);
+  return check_launch("route");
+}
+
+}  // namespace fcmoe

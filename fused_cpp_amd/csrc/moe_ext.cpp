@@ -1,0 +1,318 @@
+// moe_ext.cpp -- PyTorch-ROCm host extension `fused_cpp_amd._moe_C`.
+//
+// The C++ side of the Python operators: validates tensors, allocates the
+// per-call workspace from the torch caching allocator on the current HIP
+// stream, marshals device pointers into the C ABI of libfcmoe.so
+// (include/fcmoe.h) and maps its error codes to RuntimeError. It plays the
+// role of the reference's pybind modules `_moe_C` (csrc/moe/module.cpp:10-264)
+// and `_C`'s i8gemm bindings (csrc/module.cpp:220-233); the GIL is released
+// around every launch as there (module.cpp:206-220).
+#include <c10/hip/HIPStream.h>
+#include <torch/extension.h>
+
+#include <string>
+#include <tuple>
+
+#include "../../include/fcmoe.h"
+
+namespace {
+
+constexpr int64_t kBackendId = 950;
+const char* kBackendName = "gfx950_mfma";
+
+hipStream_t current_stream() { return c10::hip::getCurrentHIPStream().stream(); }
+
+void check_rc(int rc, const char* what) {
+  TORCH_CHECK(rc == FCMOE_OK, what, " failed: ", fcmoe_last_error());
+}
+
+void check_device(const at::Tensor& t, const char* name) {
+  TORCH_CHECK(t.is_cuda(), name, " must be a ROCm (cuda) device tensor");
+}
+
+at::Tensor workspace(size_t bytes, const at::Tensor& like) {
+  return at::empty({(int64_t)bytes}, like.options().dtype(at::kByte));
+}
+
+int activation_code(const std::string& name) {
+  if (name == "silu") return FCMOE_ACT_SILU;
+  if (name == "gelu") return FCMOE_ACT_GELU;
+  if (name == "swigluoai") return FCMOE_ACT_SWIGLUOAI;
+  if (name == "silu_clamp10") return FCMOE_ACT_SILU_CLAMP10;
+  TORCH_CHECK(false, "unsupported MoE activation: ", name);
+}
+
+at::Tensor pack(const at::Tensor& w, int n_groups) {
+  // w: [E, N, K] int8 or bf16 on device.
+  const int eb = w.scalar_type() == at::kChar ? 1 : 2;
+  const int64_t e = w.size(0), n = w.size(1), k = w.size(2);
+  const int64_t per = fcmoe_packed_expert_bytes(eb, n, k, n_groups);
+  TORCH_CHECK(per > 0, "invalid weight shape for packing");
+  at::Tensor dst = at::empty({e, per}, w.options().dtype(at::kChar));
+  check_rc(fcmoe_pack_experts(w.data_ptr(), eb, e, n, k, n_groups, dst.data_ptr(), current_stream()), "pack");
+  return dst;
+}
+
+using W8A8Tuple =
+    std::tuple<at::Tensor, int64_t, int64_t, at::Tensor, at::Tensor, int64_t, int64_t, at::Tensor, int64_t, int64_t>;
+
+// Packs checkpoint int8 experts (csrc/moe/arm/i8mm_w8a8/kernels.cpp:424-444).
+W8A8Tuple w8a8_prepare_quantized(at::Tensor w13, at::Tensor s13, at::Tensor w2, at::Tensor s2) {
+  check_device(w13, "w13_weight");
+  check_device(w2, "w2_weight");
+  TORCH_CHECK(w13.scalar_type() == at::kChar && w2.scalar_type() == at::kChar,
+              "W8A8 weights must have dtype torch.int8");
+  TORCH_CHECK(w13.dim() == 3 && w2.dim() == 3, "W8A8 weights must be [E, 2F, H] and [E, H, F]");
+  TORCH_CHECK(w13.size(0) > 0 && w13.size(0) == w2.size(0), "W8A8 expert counts must match and be positive");
+  TORCH_CHECK(w13.size(1) % 2 == 0, "W8A8 W13 output dimension must be even");
+  const int64_t e = w13.size(0), f = w13.size(1) / 2, h = w13.size(2);
+  TORCH_CHECK(w2.size(1) == h && w2.size(2) == f, "W8A8 W2 shape mismatch");
+  TORCH_CHECK(h % 16 == 0 && f % 16 == 0, "W8A8 requires H and F to be multiples of 16");
+  TORCH_CHECK(s13.scalar_type() == at::kFloat && s2.scalar_type() == at::kFloat, "W8A8 scales must be float32");
+  TORCH_CHECK(s13.numel() == e * 2 * f, "W8A8 W13 scales must contain one value per output channel");
+  TORCH_CHECK(s2.numel() == e * h, "W8A8 W2 scales must contain one value per output channel");
+  at::Tensor p13 = pack(w13.contiguous(), 2);
+  at::Tensor p2 = pack(w2.contiguous(), 1);
+  return {p13, h, 2 * f, s13.to(w13.device()).reshape({e, 2 * f}).contiguous(), p2, f, h,
+          s2.to(w13.device()).reshape({e, h}).contiguous(), kBackendId, 16};
+}
+
+// Quantise bf16 experts per output channel on the GPU, then pack
+// (csrc/moe/arm/i8mm_w8a8/kernels.cpp:446-461).
+W8A8Tuple w8a8_prepare(at::Tensor w13, at::Tensor w2) {
+  check_device(w13, "w13_weight");
+  check_device(w2, "w2_weight");
+  TORCH_CHECK(w13.scalar_type() == at::kBFloat16 && w2.scalar_type() == at::kBFloat16,
+              "W8A8 source weights must have dtype torch.bfloat16");
+  TORCH_CHECK(w13.dim() == 3 && w2.dim() == 3, "W8A8 weights must be [E, 2F, H] and [E, H, F]");
+  auto quant = [](const at::Tensor& src) {
+    at::Tensor s = src.contiguous();
+    const int64_t cols = s.size(-1);
+    const int64_t rows = s.numel() / cols;
+    at::Tensor q = at::empty(s.sizes(), s.options().dtype(at::kChar));
+    at::Tensor sc = at::empty({s.size(0), s.size(1)}, s.options().dtype(at::kFloat));
+    check_rc(fcmoe_quantize_weight_rows((const uint16_t*)s.data_ptr(), rows, cols, (int8_t*)q.data_ptr(),
+                                        sc.data_ptr<float>(), current_stream()),
+             "quantize_weight_rows");
+    return std::make_pair(q, sc);
+  };
+  auto [q13, s13] = quant(w13);
+  auto [q2, s2] = quant(w2);
+  return w8a8_prepare_quantized(q13, s13, q2, s2);
+}
+
+fcmoe_moe_args base_args(const at::Tensor& input, const at::Tensor& topk_weights, const at::Tensor& topk_ids,
+                         int64_t experts, int64_t shared_id, double routed_scale, int64_t global_num_experts,
+                         const at::Tensor& out) {
+  fcmoe_moe_args a{};
+  a.x = (const uint16_t*)input.data_ptr();
+  a.tokens = input.size(0);
+  a.hidden = input.size(1);
+  a.top_k = topk_ids.defined() ? topk_ids.size(1) : 0;
+  a.topk_ids = a.top_k > 0 ? topk_ids.data_ptr() : nullptr;
+  a.ids_is_i64 = (topk_ids.defined() && topk_ids.scalar_type() == at::kLong) ? 1 : 0;
+  a.topk_weights = a.top_k > 0 ? topk_weights.data_ptr<float>() : nullptr;
+  a.experts = experts;
+  a.valid_experts = global_num_experts > 0 ? global_num_experts : experts;
+  a.shared_expert_id = shared_id;
+  a.routed_scaling = (float)routed_scale;
+  a.out = (uint16_t*)out.data_ptr();
+  return a;
+}
+
+void check_routing(const at::Tensor& input, const at::Tensor& topk_weights, const at::Tensor& topk_ids) {
+  check_device(input, "input");
+  TORCH_CHECK(input.scalar_type() == at::kBFloat16 && input.dim() == 2 && input.is_contiguous(),
+              "input must be a contiguous bf16 [tokens, hidden] tensor");
+  if (!topk_ids.defined()) return;
+  check_device(topk_ids, "topk_ids");
+  check_device(topk_weights, "topk_weights");
+  TORCH_CHECK(topk_ids.dim() == 2 && topk_weights.sizes() == topk_ids.sizes(),
+              "topk tensors must be matching [tokens, top_k]");
+  TORCH_CHECK(topk_ids.size(0) == input.size(0), "topk token dimension must match input");
+  TORCH_CHECK(topk_ids.scalar_type() == at::kLong || topk_ids.scalar_type() == at::kInt,
+              "topk_ids must be int32 or int64");
+  TORCH_CHECK(topk_weights.scalar_type() == at::kFloat, "topk_weights must be float32");
+  TORCH_CHECK(topk_ids.is_contiguous() && topk_weights.is_contiguous(), "topk tensors must be contiguous");
+}
+
+at::Tensor output_for(const at::Tensor& input, c10::optional<at::Tensor> out) {
+  if (!out.has_value()) return at::empty_like(input);
+  at::Tensor o = *out;
+  TORCH_CHECK(o.device() == input.device() && o.scalar_type() == at::kBFloat16 && o.sizes() == input.sizes() &&
+                  o.is_contiguous(),
+              "out must be contiguous bf16 with the input shape on the input device");
+  TORCH_CHECK(!o.requires_grad(), "out with requires_grad=True is not supported");
+  return o;
+}
+
+void maybe_check_invalid(const at::Tensor& invalid, bool validate) {
+  if (!validate) return;
+  const int32_t bad = invalid.item<int32_t>();
+  TORCH_CHECK(bad == 0, "topk_ids out of range: ", bad, " id(s) outside the valid expert range");
+}
+
+// W8A8 forward (csrc/moe/arm/i8mm_w8a8/kernels.cpp:463-694).
+at::Tensor w8a8_forward(at::Tensor input, at::Tensor w13, int64_t w13_k, int64_t w13_n, at::Tensor s13,
+                        at::Tensor w2, int64_t w2_k, int64_t w2_n, at::Tensor s2, at::Tensor topk_weights,
+                        at::Tensor topk_ids, int64_t shared_id, double routed_scale, int64_t global_num_experts,
+                        c10::optional<at::Tensor> out, bool validate_ids) {
+  check_routing(input, topk_weights, topk_ids);
+  check_device(w13, "w13_packed");
+  TORCH_CHECK(input.size(1) == w13_k && w13_n == 2 * w2_k && w2_n == w13_k, "W8A8 expert dimensions mismatch");
+  const int64_t e = w13.size(0);
+  TORCH_CHECK(w2.size(0) == e && s13.sizes() == at::IntArrayRef({e, w13_n}) && s2.sizes() == at::IntArrayRef({e, w2_n}),
+              "W8A8 packed weights/scales are invalid");
+  TORCH_CHECK(w13.size(1) == fcmoe_packed_expert_bytes(1, w13_n, w13_k, 2) &&
+                  w2.size(1) == fcmoe_packed_expert_bytes(1, w2_n, w2_k, 1),
+              "W8A8 packed weight strides are invalid");
+  at::Tensor output = output_for(input, out);
+  at::Tensor invalid = at::zeros({1}, input.options().dtype(at::kInt));
+  fcmoe_moe_args a = base_args(input, topk_weights, topk_ids, e, shared_id, routed_scale, global_num_experts, output);
+  a.inter = w2_k;
+  a.w13 = w13.data_ptr();
+  a.w2 = w2.data_ptr();
+  a.w13_scale = s13.data_ptr<float>();
+  a.w2_scale = s2.data_ptr<float>();
+  a.activation = FCMOE_ACT_SILU_CLAMP10;
+  a.invalid_count = invalid.data_ptr<int32_t>();
+  at::Tensor ws = workspace(fcmoe_w8a8_workspace_bytes(&a), input);
+  a.workspace = ws.data_ptr();
+  a.workspace_bytes = ws.numel();
+  {
+    pybind11::gil_scoped_release release;
+    check_rc(fcmoe_w8a8_forward(&a, current_stream()), "fused_moe_w8a8");
+  }
+  maybe_check_invalid(invalid, validate_ids);
+  return output;
+}
+
+using Bf16Tuple = std::tuple<at::Tensor, int64_t, int64_t, at::Tensor, int64_t, int64_t, int64_t, int64_t, std::string>;
+
+// BF16 prepare (csrc/moe/arm/common/fused_moe_bf16_tiled.cpp:6125-6209).
+Bf16Tuple bf16_prepare(at::Tensor w13, at::Tensor w2) {
+  check_device(w13, "w13_weight");
+  check_device(w2, "w2_weight");
+  TORCH_CHECK(w13.scalar_type() == at::kBFloat16 && w2.scalar_type() == at::kBFloat16,
+              "BF16 tiled fused MoE weights must be torch.bfloat16");
+  TORCH_CHECK(w13.dim() == 3 && w2.dim() == 3, "weights must be [E, 2F, H] and [E, H, F]");
+  TORCH_CHECK(w13.size(0) == w2.size(0) && w13.size(1) % 2 == 0 && w2.size(1) == w13.size(2) &&
+                  w2.size(2) == w13.size(1) / 2,
+              "w13/w2 shape mismatch");
+  at::Tensor p13 = pack(w13.contiguous(), 2);
+  at::Tensor p2 = pack(w2.contiguous(), 1);
+  return {p13, w13.size(2), w13.size(1), p2, w2.size(2), w2.size(1), kBackendId, 16, std::string(kBackendName)};
+}
+
+at::Tensor bias_f32(c10::optional<at::Tensor> b, int64_t e, int64_t n, const at::Tensor& like) {
+  if (!b.has_value() || !b->defined()) return at::Tensor();
+  TORCH_CHECK(b->numel() == e * n, "bias must have shape [E, N]");
+  return b->to(like.device(), at::kFloat).reshape({e, n}).contiguous();
+}
+
+// BF16 forward (csrc/moe/arm/common/fused_moe_bf16_tiled.cpp:6376-7218) and
+// the shared MLP when topk_ids is undefined (:10307-10455).
+at::Tensor bf16_forward(at::Tensor input, at::Tensor w13, int64_t w13_k, int64_t w13_n, at::Tensor w2, int64_t w2_k,
+                        int64_t w2_n, c10::optional<at::Tensor> topk_weights_opt,
+                        c10::optional<at::Tensor> topk_ids_opt, c10::optional<at::Tensor> w13_bias,
+                        c10::optional<at::Tensor> w2_bias, std::string activation, int64_t global_num_experts,
+                        bool skip_weighted, int64_t shared_id, double routed_scale, c10::optional<at::Tensor> out,
+                        bool validate_ids) {
+  at::Tensor topk_weights = topk_weights_opt.value_or(at::Tensor());
+  at::Tensor topk_ids = topk_ids_opt.value_or(at::Tensor());
+  check_routing(input, topk_weights, topk_ids);
+  check_device(w13, "w13_packed");
+  TORCH_CHECK(input.size(1) == w13_k && w13_n % 2 == 0 && w2_k == w13_n / 2 && w2_n == w13_k,
+              "BF16 expert dimensions mismatch");
+  const int64_t e = w13.size(0);
+  TORCH_CHECK(w2.size(0) == e && w13.size(1) == fcmoe_packed_expert_bytes(2, w13_n, w13_k, 2) &&
+                  w2.size(1) == fcmoe_packed_expert_bytes(2, w2_n, w2_k, 1),
+              "BF16 packed weights are invalid");
+  at::Tensor output = output_for(input, out);
+  at::Tensor b13 = bias_f32(w13_bias, e, w13_n, input);
+  at::Tensor b2 = bias_f32(w2_bias, e, w2_n, input);
+  at::Tensor invalid = at::zeros({1}, input.options().dtype(at::kInt));
+  fcmoe_moe_args a = base_args(input, topk_weights, topk_ids, e, shared_id, routed_scale, global_num_experts, output);
+  a.inter = w2_k;
+  a.w13 = w13.data_ptr();
+  a.w2 = w2.data_ptr();
+  a.w13_bias = b13.defined() ? b13.data_ptr<float>() : nullptr;
+  a.w2_bias = b2.defined() ? b2.data_ptr<float>() : nullptr;
+  a.activation = activation_code(activation);
+  a.skip_weighted = skip_weighted ? 1 : 0;
+  a.invalid_count = invalid.data_ptr<int32_t>();
+  at::Tensor ws = workspace(fcmoe_bf16_workspace_bytes(&a), input);
+  a.workspace = ws.data_ptr();
+  a.workspace_bytes = ws.numel();
+  {
+    pybind11::gil_scoped_release release;
+    check_rc(fcmoe_bf16_forward(&a, current_stream()), "fused_moe_bf16");
+  }
+  maybe_check_invalid(invalid, validate_ids);
+  return output;
+}
+
+// i8gemm prepare (csrc/i8gemm.cpp:280-316): packed weight, fp32 [N] scales,
+// K, N, Kp, Np, backend name.
+std::tuple<at::Tensor, at::Tensor, int64_t, int64_t, int64_t, int64_t, std::string> i8gemm_prepare(
+    at::Tensor weight, at::Tensor weight_scale) {
+  check_device(weight, "weight");
+  TORCH_CHECK(weight.dim() == 2, "i8gemm.prepare: weight must be 2D [N, K], got dim=", weight.dim());
+  TORCH_CHECK(weight.scalar_type() == at::kChar, "i8gemm.prepare: weight dtype must be torch.int8");
+  const int64_t n = weight.size(0), k = weight.size(1);
+  TORCH_CHECK(n > 0 && k > 0, "i8gemm.prepare: N and K must be positive, got N=", n, " K=", k);
+  at::Tensor scale = weight_scale.to(weight.device(), at::kFloat).reshape({-1});
+  TORCH_CHECK(scale.numel() == 1 || scale.numel() == n, "i8gemm.prepare: weight_scale must be scalar or shape [N]");
+  if (scale.numel() == 1) scale = scale.expand({n});
+  at::Tensor packed = pack(weight.contiguous().unsqueeze(0), 1).reshape({-1});
+  return {packed, scale.contiguous(), k, n, fcmoe_packed_expert_bytes(1, n, k, 1) / (((n + 15) / 16) * 16),
+          ((n + 15) / 16) * 16, std::string(kBackendName)};
+}
+
+// i8gemm_dynamic_scaled_mm (csrc/i8gemm.cpp:318-452).
+void i8gemm_dynamic_scaled_mm(at::Tensor output, at::Tensor input, at::Tensor packed_weight, at::Tensor weight_scale,
+                              c10::optional<at::Tensor> bias, int64_t k, int64_t n) {
+  check_device(input, "input");
+  TORCH_CHECK(input.dim() == 2 && input.is_contiguous(), "i8gemm.dynamic_scaled_mm: input must be contiguous [M, K]");
+  TORCH_CHECK(input.scalar_type() == at::kFloat || input.scalar_type() == at::kBFloat16,
+              "i8gemm.dynamic_scaled_mm: input dtype must be float32/bfloat16");
+  TORCH_CHECK(output.dim() == 2 && output.is_contiguous() && output.size(0) == input.size(0) && output.size(1) == n,
+              "i8gemm.dynamic_scaled_mm: output shape must be [M, N]");
+  TORCH_CHECK(output.scalar_type() == at::kFloat || output.scalar_type() == at::kBFloat16,
+              "i8gemm.dynamic_scaled_mm: output dtype must be float32/bfloat16");
+  TORCH_CHECK(input.size(1) == k, "i8gemm.dynamic_scaled_mm: input K mismatch");
+  TORCH_CHECK(packed_weight.numel() == fcmoe_packed_expert_bytes(1, n, k, 1), "i8gemm: invalid packed_weight");
+  TORCH_CHECK(weight_scale.numel() == n && weight_scale.scalar_type() == at::kFloat,
+              "i8gemm.dynamic_scaled_mm: weight_scale must be contiguous float32 [N]");
+  const int64_t m = input.size(0);
+  if (m == 0) return;
+  at::Tensor b;
+  if (bias.has_value() && bias->defined()) {
+    TORCH_CHECK(bias->dim() == 1 && bias->size(0) == n, "i8gemm.dynamic_scaled_mm: bias must be shape [", n, "]");
+    b = bias->to(input.device(), at::kFloat).contiguous();
+  }
+  at::Tensor ws = workspace(fcmoe_i8gemm_workspace_bytes(m, k), input);
+  pybind11::gil_scoped_release release;
+  check_rc(fcmoe_i8gemm(input.data_ptr(), input.scalar_type() == at::kFloat ? 1 : 0, m, k, packed_weight.data_ptr(),
+                        weight_scale.data_ptr<float>(), n, b.defined() ? b.data_ptr<float>() : nullptr,
+                        output.data_ptr(), output.scalar_type() == at::kBFloat16 ? 1 : 0, ws.data_ptr(), ws.numel(),
+                        current_stream()),
+           "i8gemm");
+}
+
+std::vector<std::string> available_backends() { return {kBackendName}; }
+
+}  // namespace
+
+PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
+  m.doc() = "MI355X (gfx950) fused MoE host extension over libfcmoe";
+  m.def("available_backends", &available_backends);
+  m.def("abi_version", []() { return fcmoe_abi_version(); });
+  m.def("fused_moe_w8a8_prepare_weights", &w8a8_prepare);
+  m.def("fused_moe_w8a8_prepare_quantized_weights", &w8a8_prepare_quantized);
+  m.def("fused_moe_w8a8_forward", &w8a8_forward);
+  m.def("fused_moe_bf16_prepare_weights", &bf16_prepare);
+  m.def("fused_moe_bf16_forward", &bf16_forward);
+  m.def("i8gemm_prepare", &i8gemm_prepare);
+  m.def("i8gemm_dynamic_scaled_mm", &i8gemm_dynamic_scaled_mm);
+}

@@ -1,0 +1,400 @@
+#!/usr/bin/env python3
+"""Benchmark of the W8A8 fused-MoE layer on one MI355X.
+
+Default workload (the metric's config): W8A8 INT8
+decode MoE layer, DeepSeek-V3/V4 shape -- T=64 tokens, H=7168, I=2048, 256
+routed experts top-8 (softmax, renormalise, x2.5) + 1 shared expert,
+weights N(0, 0.02) bf16 quantised per output channel, dynamic per-token int8
+activations. A step is one call of ``fused_moe_w8a8_tiled_with_shared`` on
+inputs resident in HBM. Prints ONE JSON line.
+
+``--config c3`` / ``c4`` run the prefill configs, ``c1`` / ``c0`` the BF16
+ones (for the tables in DESIGN.md); ``--prefill`` adds the C3 prefill figures
+to the default line as ``secondary``.
+
+roofline: the dominant kernel (largest GPU time per step among the grouped
+GEMM tile-class launches) is timed live with hipEvents recorded by libfcmoe
+on the launch stream (fcmoe_stage_timing_*); its algorithmic bytes/ops come
+from the realised routing ("Measurement").
+cpu_baseline: the CPU oracle (oracle/, a restatement of the reference
+arithmetic, OpenMP) timed on this host on the same layer.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+HBM_PEAK_GBPS = 8000.0
+INT8_PEAK_TOPS = 5000.0
+BF16_PEAK_TFLOPS = 2500.0
+CLASS_BM = (16, 32, 64, 128, 256)
+
+CONFIGS = {
+    "c0": dict(kind="bf16", T=32, H=1024, I=512, E=8, k=2, shared=False, scale=1.0, skew=None,
+               desc="C0 BF16 fused MoE plumbing: T=32 H=1024 I=512 E=8 top-2"),
+    "c1": dict(kind="bf16", T=32, H=7168, I=2048, E=256, k=8, shared=True, scale=2.5, skew=None,
+               desc="C1 BF16 DSv3 decode: T=32 H=7168 I=2048 E=256 top-8 +1 shared"),
+    "c2": dict(kind="w8a8", T=64, H=7168, I=2048, E=256, k=8, shared=True, scale=2.5, skew=None,
+               desc="C2 W8A8 DSv3 decode: T=64 H=7168 I=2048 E=256 top-8 +1 shared"),
+    "c3": dict(kind="w8a8", T=4096, H=7168, I=2048, E=256, k=8, shared=True, scale=2.5, skew=1.2,
+               desc="C3 W8A8 DSv3 prefill: T=4096 Zipf(1.2) routing, +1 shared"),
+    "c4": dict(kind="w8a8", T=8192, H=7168, I=2048, E=384, k=8, shared=True, scale=2.5, skew=None,
+               desc="C4 W8A8 prefill: T=8192 H=7168 I=2048 E=384 top-8 +1 shared"),
+}
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def make_routing(cfg, seed: int = 0):
+    """Router of the config text: softmax top-k renormalised x scale; C3 Zipf-skewed."""
+    rng = np.random.default_rng(seed)
+    T, E, k = cfg["T"], cfg["E"], cfg["k"]
+    if cfg["skew"] is None:
+        logits = rng.standard_normal((T, E)).astype(np.float32)
+        z = np.exp(logits - logits.max(1, keepdims=True))
+        p = z / z.sum(1, keepdims=True)
+        ids = np.argsort(-p, axis=1, kind="stable")[:, :k]
+        w = np.take_along_axis(p, ids, 1)
+        w = w / w.sum(1, keepdims=True)
+        return ids.astype(np.int64), w.astype(np.float32), None
+    # Zipf popularity over a random expert permutation, Gumbel-top-k without
+    # replacement; sharpened (tau) until some expert receives no token.
+    for tau in (1.0, 0.5, 0.25):
+        perm = rng.permutation(E)
+        pz = np.empty(E)
+        pz[perm] = np.arange(1, E + 1, dtype=np.float64) ** (-cfg["skew"])
+        pz /= pz.sum()
+        g = np.log(pz)[None, :] / tau + rng.gumbel(size=(T, E))
+        ids = np.argsort(-g, axis=1, kind="stable")[:, :k]
+        if (np.bincount(ids.reshape(-1), minlength=E) == 0).any():
+            break
+    sel = np.take_along_axis(g, ids, 1)
+    w = np.exp(sel - sel.max(1, keepdims=True))
+    w = w / w.sum(1, keepdims=True)
+    return ids.astype(np.int64), w.astype(np.float32), tau
+
+
+def build_layer(cfg, device, keep_host_int8: bool):
+    """Random N(0, 0.02) bf16 experts (+shared), quantised per channel and packed on the GPU."""
+    import torch
+
+    from fused_cpp_amd import cabi
+    from fused_cpp_amd.moe import PreparedW8A8TiledFusedMoEWeights, PreparedW8A8TiledRoutedSharedMoEWeights
+
+    L = cabi.lib()
+    stream = cabi.stream_handle()
+    E = cfg["E"] + (1 if cfg["shared"] else 0)
+    H, I = cfg["H"], cfg["I"]
+    g = torch.Generator(device=device).manual_seed(1234)
+    q13 = torch.empty((E, 2 * I, H), dtype=torch.int8, device=device)
+    q2 = torch.empty((E, H, I), dtype=torch.int8, device=device)
+    s13 = torch.empty((E, 2 * I), dtype=torch.float32, device=device)
+    s2 = torch.empty((E, H), dtype=torch.float32, device=device)
+    for e in range(E):
+        for q, s, shape in ((q13, s13, (2 * I, H)), (q2, s2, (H, I))):
+            w = (torch.randn(shape, generator=g, device=device, dtype=torch.float32) * 0.02).to(torch.bfloat16)
+            cabi.check(L.fcmoe_quantize_weight_rows(w.data_ptr(), shape[0], shape[1], q[e].data_ptr(),
+                                                    s[e].data_ptr(), stream), "quantize")
+    per13 = L.fcmoe_packed_expert_bytes(1, 2 * I, H, 2)
+    per2 = L.fcmoe_packed_expert_bytes(1, H, I, 1)
+    p13 = torch.empty((E, per13), dtype=torch.int8, device=device)
+    p2 = torch.empty((E, per2), dtype=torch.int8, device=device)
+    cabi.check(L.fcmoe_pack_experts(q13.data_ptr(), 1, E, 2 * I, H, 2, p13.data_ptr(), stream), "pack13")
+    cabi.check(L.fcmoe_pack_experts(q2.data_ptr(), 1, E, H, I, 1, p2.data_ptr(), stream), "pack2")
+    torch.cuda.synchronize()
+    packed = PreparedW8A8TiledFusedMoEWeights(w13=(p13, H, 2 * I, s13), w2=(p2, I, H, s2))
+    host = None
+    if keep_host_int8:
+        host = (q13.cpu().numpy(), s13.cpu().numpy(), q2.cpu().numpy(), s2.cpu().numpy())
+    del q13, q2
+    torch.cuda.empty_cache()
+    if cfg["shared"]:
+        weights = PreparedW8A8TiledRoutedSharedMoEWeights(packed=packed, routed_experts=cfg["E"],
+                                                          shared_expert_id=cfg["E"])
+    else:
+        weights = packed
+    return weights, host
+
+
+def build_bf16_layer(cfg, device):
+    import torch
+
+    from fused_cpp_amd.moe import (PreparedBF16TiledRoutedSharedMoEWeights, prepare_fused_moe_bf16_tiled_weights)
+
+    E = cfg["E"] + (1 if cfg["shared"] else 0)
+    H, I = cfg["H"], cfg["I"]
+    g = torch.Generator(device=device).manual_seed(1234)
+    w13 = (torch.randn((E, 2 * I, H), generator=g, device=device) * 0.02).to(torch.bfloat16)
+    w2 = (torch.randn((E, H, I), generator=g, device=device) * 0.02).to(torch.bfloat16)
+    packed = prepare_fused_moe_bf16_tiled_weights(w13, w2, fuse_silu=True)
+    del w13, w2
+    torch.cuda.empty_cache()
+    if cfg["shared"]:
+        return PreparedBF16TiledRoutedSharedMoEWeights(packed=packed, routed_experts=cfg["E"],
+                                                       shared_expert_id=cfg["E"])
+    return packed
+
+
+def expert_counts(cfg, ids):
+    E = cfg["E"] + (1 if cfg["shared"] else 0)
+    counts = np.bincount(ids.reshape(-1), minlength=E).astype(np.int64)
+    if cfg["shared"]:
+        counts[cfg["E"]] += cfg["T"]
+    return counts
+
+
+def class_of(c: int) -> int:
+    for i, bm in enumerate(CLASS_BM):
+        if c <= bm:
+            return i
+    return len(CLASS_BM) - 1
+
+
+def algorithmic(cfg, counts):
+    """Algorithmic HBM bytes and ops of the layer and of each GEMM stage class.
+
+    Layer bytes = active experts' weights + scales, x in, out, ids + weights;
+    ops = 2 * MACs = routed rows * 6 * H * I (int8 or bf16)."""
+    H, I = cfg["H"], cfg["I"]
+    eb = 1 if cfg["kind"] == "w8a8" else 2
+    sb = 4 if cfg["kind"] == "w8a8" else 0
+    active = counts > 0
+    rows = int(counts.sum())
+    T = cfg["T"]
+    layer_bytes = int(active.sum()) * (3 * H * I * eb + (2 * I + H) * sb) + T * H * 2 * 2 + T * cfg["k"] * 12
+    layer_ops = rows * 6 * H * I
+    stages = {}
+    for c in range(len(CLASS_BM)):
+        sel = (counts > 0) & (np.array([class_of(int(x)) for x in counts]) == c)
+        n_exp, r = int(sel.sum()), int(counts[sel].sum())
+        if n_exp == 0:
+            continue
+        stages[f"w13_bm{CLASS_BM[c]}"] = dict(
+            bytes=n_exp * (2 * I * H * eb + 2 * I * sb) + r * H * eb + r * I * 2, ops=r * 2 * (2 * I) * H,
+            experts=n_exp, rows=r)
+        stages[f"w2_bm{CLASS_BM[c]}"] = dict(
+            bytes=n_exp * (H * I * eb + H * sb) + r * I * eb + r * H * 4, ops=r * 2 * H * I, experts=n_exp, rows=r)
+    return layer_bytes, layer_ops, stages
+
+
+def run_gpu(cfg, steps: int, warmup: int, device, keep_host: bool):
+    import torch
+
+    from fused_cpp_amd import cabi
+    from fused_cpp_amd.moe import fused_moe_bf16_tiled_with_shared, fused_moe_tiled, fused_moe_w8a8_tiled_with_shared
+
+    ids, w, tau = make_routing(cfg)
+    rng = np.random.default_rng(7)
+    x = torch.from_numpy(rng.standard_normal((cfg["T"], cfg["H"])).astype(np.float32)).to(device).to(torch.bfloat16)
+    ids_d = torch.from_numpy(ids).to(device)
+    w_d = torch.from_numpy(w).to(device)
+    t0 = time.time()
+    host = None
+    if cfg["kind"] == "w8a8":
+        weights, host = build_layer(cfg, device, keep_host)
+        if cfg["shared"]:
+            def step(out):
+                return fused_moe_w8a8_tiled_with_shared(x, weights, w_d, ids_d, routed_scaling_factor=cfg["scale"],
+                                                        out=out)
+        else:
+            def step(out):
+                return fused_moe_tiled(x, weights, w_d, ids_d, swiglu_limit=10.0, out=out)
+    else:
+        weights = build_bf16_layer(cfg, device)
+        if cfg["shared"]:
+            def step(out):
+                return fused_moe_bf16_tiled_with_shared(x, weights, w_d, ids_d, routed_scaling_factor=cfg["scale"],
+                                                        out=out)
+        else:
+            def step(out):
+                return fused_moe_tiled(x, weights, w_d, ids_d, out=out)
+    log(f"[bench] weights ready in {time.time() - t0:.1f}s")
+    out = torch.empty_like(x)
+    for _ in range(max(warmup, 1)):
+        step(out)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    cabi.stage_timing_read()  # clear
+    start.record()
+    for _ in range(steps):
+        step(out)
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    # Per-stage kernel durations: a separate pass with event pairs around each launch.
+    cabi.stage_timing_enable(True)
+    for _ in range(steps):
+        step(out)
+    torch.cuda.synchronize()
+    stages = cabi.stage_timing_read()
+    cabi.stage_timing_enable(False)
+    return dict(ms=ms, stages=stages, ids=ids, w=w, tau=tau, x=x, out=out, host=host, weights=weights)
+
+
+def cpu_baseline(cfg, res, max_routes: int | None):
+    """Time the oracle's grouped per-expert W8A8 layer (OpenMP) on this host."""
+    import oracle
+
+    q13, s13, q2, s2 = res["host"]
+    x_bits = res["x"].cpu().view(__import__("torch").int16).numpy().view(np.uint16)
+    counts_routes = oracle.route_build(res["ids"], q13.shape[0], cfg["E"] if cfg["shared"] else -1)
+    counts, offsets, sorted_routes, _ = counts_routes
+    kt = cfg["k"] + (1 if cfg["shared"] else 0)
+    R = cfg["T"] * kt
+    # bounded sample: whole experts in sorted order until max_routes
+    e_end = len(counts)
+    if max_routes is not None:
+        csum = np.cumsum(counts)
+        e_end = int(np.searchsorted(csum, max_routes) + 1)
+        e_end = min(e_end, len(counts))
+    route_out = np.zeros((R, cfg["H"]), np.float32)
+    threads = os.cpu_count() or 1
+    oracle.w8a8_expert_range(x_bits, sorted_routes, offsets, kt, q13, s13, q2, s2, 0, min(e_end, 2), route_out)
+    times = []
+    done = 0
+    for _ in range(3):
+        t0 = time.perf_counter()
+        done = oracle.w8a8_expert_range(x_bits, sorted_routes, offsets, kt, q13, s13, q2, s2, 0, e_end, route_out)
+        times.append(time.perf_counter() - t0)
+    t = float(np.median(times))
+    routes_per_s = done / t
+    layer_s = R / routes_per_s
+    return {
+        "value": round(cfg["T"] / layer_s, 2),
+        "unit": "tokens/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"oracle grouped W8A8 layer (OpenMP, {threads} threads), experts 0..{e_end - 1} = {done} of {R} "
+                  f"routes, median of 3 = {t:.2f}s, scaled to the full layer ({layer_s:.2f}s/layer)",
+    }
+
+
+def parity_check(cfg, res) -> dict:
+    """Bit-exact check of a few tokens against the oracle (same routing, same weights)."""
+    import oracle
+
+    q13, s13, q2, s2 = res["host"]
+    n = min(4, cfg["T"])
+    x_bits = res["x"][:n].cpu().view(__import__("torch").int16).numpy().view(np.uint16)
+    sid = cfg["E"] if cfg["shared"] else -1
+    ref = oracle.w8a8_forward(x_bits, res["ids"][:n], res["w"][:n], q13, s13, q2, s2, shared_id=sid,
+                              routed_scale=cfg["scale"])
+    got = res["out"][:n].cpu().view(__import__("torch").int16).numpy().view(np.uint16)
+    return {"tokens_checked": n, "bit_exact": bool(np.array_equal(ref, got))}
+
+
+def measure(cfg, args, device, want_cpu: bool):
+    res = run_gpu(cfg, args.steps, args.warmup, device, keep_host=want_cpu or cfg["kind"] == "w8a8")
+    counts = expert_counts(cfg, res["ids"])
+    layer_bytes, layer_ops, st_alg = algorithmic(cfg, counts)
+    ms = res["ms"]
+    # dominant kernel: largest per-step GPU time among GEMM stages
+    best = None
+    for name, (tot, n) in res["stages"].items():
+        if name in st_alg and (best is None or tot > best[1]):
+            best = (name, tot, n)
+    name, tot, n = best
+    avg_ms = tot / n
+    a = st_alg[name]
+    peak_ops = INT8_PEAK_TOPS if cfg["kind"] == "w8a8" else BF16_PEAK_TFLOPS
+    t_bytes = a["bytes"] / (HBM_PEAK_GBPS * 1e9)
+    t_ops = a["ops"] / (peak_ops * 1e12)
+    if t_bytes >= t_ops:
+        achieved = a["bytes"] / (avg_ms * 1e-3) / 1e9
+        roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBPS, 4)}
+    else:
+        achieved = a["ops"] / (avg_ms * 1e-3) / 1e12
+        roof = {"bound": "mfma", "achieved": round(achieved, 1), "peak": peak_ops, "unit": "TFLOP/s",
+                "frac": round(achieved / peak_ops, 4)}
+    roof.update({"kernel": f"grouped_gemm {name}", "avg_launch_ms": round(avg_ms, 4), "traffic": None,
+                 "algorithmic_bytes": a["bytes"], "algorithmic_ops": a["ops"], "experts": a["experts"],
+                 "rows": a["rows"]})
+    layer_roof_s = max(layer_bytes / (HBM_PEAK_GBPS * 1e9), layer_ops / (peak_ops * 1e12))
+    layer = {
+        "bytes": layer_bytes, "ops": layer_ops, "active_experts": int((counts > 0).sum()),
+        "zero_token_experts": int((counts[: cfg["E"]] == 0).sum()),
+        "hbm_TBps": round(layer_bytes / (ms * 1e-3) / 1e12, 3),
+        "ops_TOPS": round(layer_ops / (ms * 1e-3) / 1e12, 2),
+        "roofline_ms": round(layer_roof_s * 1e3, 4),
+        "roofline_frac": round(layer_roof_s * 1e3 / ms, 4),
+        "stage_ms_per_step": {k: round(v[0] / args.steps, 4) for k, v in res["stages"].items()},
+    }
+    if res.get("tau") is not None:
+        layer["zipf_tau"] = res["tau"]
+    out = {"ms": ms, "tokens_per_s": cfg["T"] / (ms * 1e-3), "roofline": roof, "layer": layer}
+    if cfg["kind"] == "w8a8" and res["host"] is not None:
+        out["parity"] = parity_check(cfg, res)
+    if want_cpu and cfg["kind"] == "w8a8":
+        max_routes = None if cfg["T"] * (cfg["k"] + 1) <= 1024 else args.cpu_routes
+        out["cpu_baseline"] = cpu_baseline(cfg, res, max_routes)
+    return out
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
+    ap.add_argument("--prefill", action="store_true", help="also measure C3 prefill as 'secondary'")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-routes", type=int, default=2048, help="route sample of the CPU baseline at prefill")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU only: every box has one MI355X; "
+                                   "run with --gpus 1 (multi-GPU sharding is described in DESIGN.md)"}))
+        return 2
+    os.environ.setdefault("FUSED_CPP_AMD_VALIDATE_IDS", "0")  # no host read inside the timed loop
+    import torch
+
+    device = torch.device("cuda", 0)
+    cfg = CONFIGS[args.config]
+    res = measure(cfg, args, device, want_cpu=not args.no_cpu_baseline)
+    line = {
+        "metric": "W8A8 MoE-layer tokens/s" if cfg["kind"] == "w8a8" else "BF16 MoE-layer tokens/s",
+        "value": round(res["tokens_per_s"], 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(res["ms"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8" if cfg["kind"] == "w8a8" else "bf16",
+        "data": "synthetic (seeded random N(0,0.02) weights, N(0,1) activations and router logits)",
+        "config": {"workload": cfg["desc"], "tokens": cfg["T"], "hidden": cfg["H"], "intermediate": cfg["I"],
+                   "routed_experts": cfg["E"], "top_k": cfg["k"], "shared_experts": int(cfg["shared"]),
+                   "routed_scaling": cfg["scale"], "parallelism": "single GPU"},
+        "roofline": res["roofline"],
+        "layer": res["layer"],
+    }
+    if "parity" in res:
+        line["parity"] = res["parity"]
+    if "cpu_baseline" in res:
+        line["cpu_baseline"] = res["cpu_baseline"]
+    if args.prefill and args.config == "c2":
+        import gc
+
+        gc.collect()
+        torch.cuda.empty_cache()
+        sec = measure(CONFIGS["c3"], args, device, want_cpu=False)
+        line["secondary"] = {"workload": CONFIGS["c3"]["desc"], "tokens_per_s": round(sec["tokens_per_s"], 1),
+                             "ms_per_step": round(sec["ms"], 4), "roofline": sec["roofline"],
+                             "layer": sec["layer"], "parity": sec.get("parity")}
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

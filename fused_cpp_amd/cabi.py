@@ -74,7 +74,27 @@ SIGNATURES = {
     "fcmoe_grouped_gemm_i8_acc": (_I, [_P, _I64, _P, _P, _P, _I64, _I64, _P, _I64, _I64, _P, _P, _SZ, _P]),
     "fcmoe_grouped_gemm_workspace_bytes": (_SZ, [_I64, _I64]),
     "fcmoe_w8a8_stage_views": (_I, [ctypes.POINTER(MoeArgs), _P, _P, _P, _P, _P, _P, _P]),
+    "fcmoe_stage_timing_enable": (_I, [_I]),
+    "fcmoe_stage_timing_read": (_I, [_P, _P]),
 }
+
+FCMOE_STAGE_COUNT = 24
+STAGE_NAMES = {0: "route", 1: "quant", 2: "requant", 3: "act", 4: "combine",
+               **{8 + c: f"w13_bm{bm}" for c, bm in enumerate((16, 32, 64, 128, 256))},
+               **{16 + c: f"w2_bm{bm}" for c, bm in enumerate((16, 32, 64, 128, 256))}}
+
+
+def stage_timing_enable(on: bool = True) -> None:
+    check(lib().fcmoe_stage_timing_enable(1 if on else 0), "stage_timing_enable")
+
+
+def stage_timing_read() -> dict[str, tuple[float, int]]:
+    """{stage name: (total ms, launches)} since the last read; clears the records."""
+    ms = (ctypes.c_double * FCMOE_STAGE_COUNT)()
+    n = (ctypes.c_int64 * FCMOE_STAGE_COUNT)()
+    check(lib().fcmoe_stage_timing_read(ctypes.cast(ms, ctypes.c_void_p), ctypes.cast(n, ctypes.c_void_p)),
+          "stage_timing_read")
+    return {STAGE_NAMES[i]: (ms[i], n[i]) for i in range(FCMOE_STAGE_COUNT) if n[i] > 0}
 
 _lib = None
 

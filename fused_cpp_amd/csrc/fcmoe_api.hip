@@ -1,8 +1,11 @@
 // fcmoe_api.hip -- the C ABI (include/fcmoe.h): argument validation,
 // workspace layout and the launch sequence of each fused operator.
 #include <stdio.h>
+#include <stdlib.h>
 
+#include <mutex>
 #include <string>
+#include <vector>
 
 #include "fcmoe_device.h"
 #include "fcmoe_internal.h"
@@ -91,6 +94,58 @@ Bf16Layout bf16_layout(const fcmoe_moe_args* a, Arena& ar) {
   L.route_out = ar.take<float>(L.routes * a->hidden);
   return L;
 }
+
+// ---- stage timing: event pairs recorded around each stage launch ----
+struct TimerRec {
+  int stage;
+  hipEvent_t a, b;
+};
+struct StageTimer {
+  std::mutex mu;
+  bool on = false;
+  std::vector<TimerRec> recs;
+  std::vector<hipEvent_t> pool;
+  StageTimer() {
+    const char* v = getenv("FUSED_CPP_MOE_STAGE_TIMING");
+    on = v && v[0] && v[0] != '0';
+  }
+  hipEvent_t get() {
+    if (!pool.empty()) {
+      hipEvent_t e = pool.back();
+      pool.pop_back();
+      return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    return e;
+  }
+};
+StageTimer& timer() {
+  static StageTimer* t = new StageTimer();  // lives until process exit
+  return *t;
+}
+
+struct Stage {
+  int id;
+  hipStream_t stream;
+  hipEvent_t a = nullptr;
+  Stage(int stage, hipStream_t s) : id(stage), stream(s) {
+    StageTimer& t = timer();
+    if (!t.on) return;
+    std::lock_guard<std::mutex> g(t.mu);
+    a = t.get();
+    if (a) hipEventRecord(a, stream);
+  }
+  ~Stage() {
+    if (!a) return;
+    StageTimer& t = timer();
+    std::lock_guard<std::mutex> g(t.mu);
+    hipEvent_t b = t.get();
+    if (!b) return;
+    hipEventRecord(b, stream);
+    t.recs.push_back({id, a, b});
+  }
+};
 
 __global__ void pad_rows_kernel(const uint16_t* x, int64_t rows, int64_t cols, int64_t ld, uint16_t* dst) {
   const int64_t r = blockIdx.y;
@@ -197,12 +252,18 @@ extern "C" int fcmoe_w8a8_forward(const fcmoe_moe_args* a, hipStream_t stream) {
   if (!ar.ok()) return fail(FCMOE_ESPACE, "W8A8 workspace too small");
   const int64_t H = a->hidden, I = a->inter;
 
-  rc = route_launch(a->topk_ids, a->ids_is_i64, a->topk_weights, a->tokens, a->top_k, a->experts, a->valid_experts,
-                    a->shared_expert_id, a->routed_scaling, a->shared_expert_id >= 0, L.rb, L.tc, a->invalid_count,
-                    stream);
-  if (rc) return rc;
-  rc = quant_rows_launch(a->x, 0, a->tokens, H, 0, L.xq, L.hp, L.xs, stream);
-  if (rc) return rc;
+  {
+    Stage st(FCMOE_STAGE_ROUTE, stream);
+    rc = route_launch(a->topk_ids, a->ids_is_i64, a->topk_weights, a->tokens, a->top_k, a->experts,
+                      a->valid_experts, a->shared_expert_id, a->routed_scaling, a->shared_expert_id >= 0, L.rb, L.tc,
+                      a->invalid_count, stream);
+    if (rc) return rc;
+  }
+  {
+    Stage st(FCMOE_STAGE_QUANT, stream);
+    rc = quant_rows_launch(a->x, 0, a->tokens, H, 0, L.xq, L.hp, L.xs, stream);
+    if (rc) return rc;
+  }
 
   GemmParams g13{};
   g13.a = L.xq;
@@ -226,11 +287,15 @@ extern "C" int fcmoe_w8a8_forward(const fcmoe_moe_args* a, hipStream_t stream) {
     GemmParams p = g13;
     p.tiles = L.rb.tiles + 2 * tile_offset(L.tc, c);
     p.tile_count = L.rb.tile_count + c;
+    Stage st(FCMOE_STAGE_W13_CLASS0 + c, stream);
     rc = gemm_launch(kEpiW13SwigluI8, L.tc.bm[c], p, L.tc.bound[c], stream);
     if (rc) return rc;
   }
-  rc = requant_launch(L.y, L.ip, L.routes, I, L.rb.rowmax, L.q2, L.ip, L.s2row, stream);
-  if (rc) return rc;
+  {
+    Stage st(FCMOE_STAGE_REQUANT, stream);
+    rc = requant_launch(L.y, L.ip, L.routes, I, L.rb.rowmax, L.q2, L.ip, L.s2row, stream);
+    if (rc) return rc;
+  }
 
   GemmParams g2{};
   g2.a = L.q2;
@@ -254,9 +319,11 @@ extern "C" int fcmoe_w8a8_forward(const fcmoe_moe_args* a, hipStream_t stream) {
     GemmParams p = g2;
     p.tiles = L.rb.tiles + 2 * tile_offset(L.tc, c);
     p.tile_count = L.rb.tile_count + c;
+    Stage st(FCMOE_STAGE_W2_CLASS0 + c, stream);
     rc = gemm_launch(kEpiW2RouteI8, L.tc.bm[c], p, L.tc.bound[c], stream);
     if (rc) return rc;
   }
+  Stage st(FCMOE_STAGE_COMBINE, stream);
   return combine_launch(L.route_out, L.rb.route_weight, L.rb.route_pos, a->tokens, L.kt, H, 0, 0, a->out, stream);
 }
 
@@ -305,10 +372,13 @@ extern "C" int fcmoe_bf16_forward(const fcmoe_moe_args* a, hipStream_t stream) {
   if (!ar.ok()) return fail(FCMOE_ESPACE, "BF16 workspace too small");
   const int64_t H = a->hidden, I = a->inter;
 
-  rc = route_launch(a->topk_ids, a->ids_is_i64, a->topk_weights, a->tokens, a->top_k, a->experts, a->valid_experts,
-                    a->shared_expert_id, a->routed_scaling, a->shared_expert_id >= 0 && a->top_k > 0, L.rb, L.tc,
-                    a->invalid_count, stream);
-  if (rc) return rc;
+  {
+    Stage st(FCMOE_STAGE_ROUTE, stream);
+    rc = route_launch(a->topk_ids, a->ids_is_i64, a->topk_weights, a->tokens, a->top_k, a->experts,
+                      a->valid_experts, a->shared_expert_id, a->routed_scaling,
+                      a->shared_expert_id >= 0 && a->top_k > 0, L.rb, L.tc, a->invalid_count, stream);
+    if (rc) return rc;
+  }
   const uint16_t* xa = a->x;
   if (L.xpad) {
     hipLaunchKernelGGL(pad_rows_kernel, dim3((unsigned)ceil_div(L.hp, 256), (unsigned)a->tokens), dim3(256), 0,
@@ -343,10 +413,12 @@ extern "C" int fcmoe_bf16_forward(const fcmoe_moe_args* a, hipStream_t stream) {
     GemmParams p = g13;
     p.tiles = L.rb.tiles + 2 * tile_offset(L.tc, c);
     p.tile_count = L.rb.tile_count + c;
+    Stage st(FCMOE_STAGE_W13_CLASS0 + c, stream);
     rc = gemm_launch(fused ? kEpiW13ActBf16 : kEpiRawF32Bias, L.tc.bm[c], p, L.tc.bound[c], stream);
     if (rc) return rc;
   }
   if (!fused) {
+    Stage st(FCMOE_STAGE_ACT, stream);
     rc = act_bf16_launch(L.gate_up, L.gu_ld, L.routes, I, round_up(I, 16), a->activation, L.y, L.ip, stream);
     if (rc) return rc;
   }
@@ -370,10 +442,12 @@ extern "C" int fcmoe_bf16_forward(const fcmoe_moe_args* a, hipStream_t stream) {
     GemmParams p = g2;
     p.tiles = L.rb.tiles + 2 * tile_offset(L.tc, c);
     p.tile_count = L.rb.tile_count + c;
+    Stage st(FCMOE_STAGE_W2_CLASS0 + c, stream);
     rc = gemm_launch(kEpiW2RouteBf16, L.tc.bm[c], p, L.tc.bound[c], stream);
     if (rc) return rc;
   }
   const int tree = (kt == 2 || kt == 4 || kt == 6 || kt == 8) ? 1 : 0;
+  Stage st(FCMOE_STAGE_COMBINE, stream);
   return combine_launch(L.route_out, L.rb.route_weight, L.rb.route_pos, a->tokens, kt, H, tree, a->skip_weighted,
                         a->out, stream);
 }
@@ -509,4 +583,36 @@ extern "C" int fcmoe_grouped_gemm_i8_acc(const int8_t* a, int64_t lda, const int
     if (rc) return rc;
   }
   return FCMOE_OK;
+}
+
+// ----------------------------------------------------------- stage timing --
+
+extern "C" int fcmoe_stage_timing_enable(int enable) {
+  StageTimer& t = timer();
+  std::lock_guard<std::mutex> g(t.mu);
+  t.on = enable != 0;
+  return FCMOE_OK;
+}
+
+extern "C" int fcmoe_stage_timing_read(double* total_ms, int64_t* launches) {
+  StageTimer& t = timer();
+  std::lock_guard<std::mutex> g(t.mu);
+  for (int i = 0; i < FCMOE_STAGE_COUNT; ++i) {
+    if (total_ms) total_ms[i] = 0.0;
+    if (launches) launches[i] = 0;
+  }
+  int rc = FCMOE_OK;
+  for (const TimerRec& r : t.recs) {
+    float ms = 0.0f;
+    if (hipEventSynchronize(r.b) != hipSuccess || hipEventElapsedTime(&ms, r.a, r.b) != hipSuccess) {
+      rc = fail(FCMOE_EDEVICE, "stage timing: event query failed");
+    } else if (r.stage >= 0 && r.stage < FCMOE_STAGE_COUNT) {
+      if (total_ms) total_ms[r.stage] += ms;
+      if (launches) launches[r.stage] += 1;
+    }
+    t.pool.push_back(r.a);
+    t.pool.push_back(r.b);
+  }
+  t.recs.clear();
+  return rc;
 }

@@ -170,6 +170,30 @@ int fcmoe_w8a8_stage_views(const fcmoe_moe_args* args, const int32_t** sorted_ro
                            int64_t* ldy, const int8_t** q2, int64_t* ldq, const float** s2row,
                            const float** route_out);
 
+/* ---- stage timing ------------------------------------------------------ */
+
+/* Stage ids for fcmoe_stage_timing_read. W13 / W2 class stages are per tile
+ * class c (BM = 16, 32, 64, 128, 256 for c = 0..4). */
+#define FCMOE_STAGE_ROUTE 0
+#define FCMOE_STAGE_QUANT 1
+#define FCMOE_STAGE_REQUANT 2
+#define FCMOE_STAGE_ACT 3
+#define FCMOE_STAGE_COMBINE 4
+#define FCMOE_STAGE_W13_CLASS0 8
+#define FCMOE_STAGE_W2_CLASS0 16
+#define FCMOE_STAGE_COUNT 24
+
+/* Per-stage GPU timing with hipEvents recorded on the launch stream around
+ * each stage of fcmoe_w8a8_forward / fcmoe_bf16_forward: the device-side
+ * counterpart of the reference's FUSED_CPP_MOE_STAGE_TIMING stderr timers
+ * (csrc/moe/arm/common/fused_moe_bf16_tiled.cpp:6446, 7122-7131).
+ * enable != 0 starts recording (the environment variable
+ * FUSED_CPP_MOE_STAGE_TIMING=1 enables it at load). _read synchronises on the
+ * recorded events, writes total milliseconds and launch counts per stage id
+ * (arrays of FCMOE_STAGE_COUNT) and clears the records. */
+int fcmoe_stage_timing_enable(int enable);
+int fcmoe_stage_timing_read(double* total_ms, int64_t* launches);
+
 #ifdef __cplusplus
 }
 #endif

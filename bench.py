@@ -152,7 +152,10 @@ def expert_counts(cfg, ids):
     return counts
 
 
-def class_of(c: int) -> int:
+def class_of(c: int, decode: bool) -> int:
+    """Tile class the GPU selector assigns to an expert with c rows (fcmoe_api.hip select_classes)."""
+    if decode:
+        return 0
     for i, bm in enumerate(CLASS_BM):
         if c <= bm:
             return i
@@ -173,8 +176,9 @@ def algorithmic(cfg, counts):
     layer_bytes = int(active.sum()) * (3 * H * I * eb + (2 * I + H) * sb) + T * H * 2 * 2 + T * cfg["k"] * 12
     layer_ops = rows * 6 * H * I
     stages = {}
+    decode = rows <= 8 * len(counts)
     for c in range(len(CLASS_BM)):
-        sel = (counts > 0) & (np.array([class_of(int(x)) for x in counts]) == c)
+        sel = (counts > 0) & (np.array([class_of(int(x), decode) for x in counts]) == c)
         n_exp, r = int(sel.sum()), int(counts[sel].sum())
         if n_exp == 0:
             continue

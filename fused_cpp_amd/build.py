@@ -34,7 +34,7 @@ HIP_FLAGS = [
     f"--offload-arch={ARCH}",
     "-O3",
     "-fPIC",
-    "-std=c++17",
+    "-std=c++20",
     "-ffp-contract=off",
     "-Xclang",
     "-target-feature",

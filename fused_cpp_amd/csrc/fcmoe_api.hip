@@ -20,6 +20,17 @@ thread_local std::string g_error;
 // experts (the shared expert at prefill) are split into BM=256 tiles.
 constexpr int kClassBM[] = {16, 32, 64, 128, 256};
 constexpr int kNumClasses = 5;
+// Decode: when an expert averages at most this many routed rows, everything
+// (the shared expert too, in several 16-row tiles) runs in the single BM=16
+// class: one launch per GEMM stage, no empty class launches, and weight
+// streaming is the only cost (a multi-tile expert re-reads its weights from
+// L2 / Infinity Cache, not HBM, since its tiles run side by side).
+constexpr int kDecodeRowsPerExpert = 8;
+
+TileClasses select_classes(int64_t routes, int64_t experts) {
+  if (routes <= kDecodeRowsPerExpert * experts) return make_tile_classes(kClassBM, 1, routes, experts);
+  return make_tile_classes(kClassBM, kNumClasses, routes, experts);
+}
 
 struct W8A8Layout {
   int64_t kt, routes, hp, ip;
@@ -68,7 +79,7 @@ W8A8Layout w8a8_layout(const fcmoe_moe_args* a, Arena& ar) {
   L.routes = a->tokens * L.kt;
   L.hp = round_up(a->hidden, 64);
   L.ip = round_up(a->inter, 64);
-  L.tc = make_tile_classes(kClassBM, kNumClasses, L.routes, a->experts);
+  L.tc = select_classes(L.routes, a->experts);
   route_take(ar, L.rb, L.routes, a->experts, L.tc);
   L.xq = ar.take<int8_t>(a->tokens * L.hp);
   L.xs = ar.take<float>(a->tokens);
@@ -86,7 +97,7 @@ Bf16Layout bf16_layout(const fcmoe_moe_args* a, Arena& ar) {
   L.hp = round_up(a->hidden, 32);
   L.ip = round_up(a->inter, 32);
   L.gu_ld = 2 * round_up(a->inter, 16);
-  L.tc = make_tile_classes(kClassBM, kNumClasses, L.routes, a->experts);
+  L.tc = select_classes(L.routes, a->experts);
   route_take(ar, L.rb, L.routes, a->experts, L.tc);
   L.xpad = (a->hidden % 32) ? ar.take<uint16_t>(a->tokens * L.hp) : nullptr;
   L.y = ar.take<uint16_t>(L.routes * L.ip);

@@ -60,16 +60,22 @@ int64_t tile_offset(const TileClasses& tc, int c) {
   return off;
 }
 
-int check_common(const fcmoe_moe_args* a) {
+int check_shapes(const fcmoe_moe_args* a) {
   if (!a) return fail(FCMOE_EINVAL, "args is NULL");
   if (a->tokens < 0 || a->hidden <= 0 || a->inter <= 0) return fail(FCMOE_EINVAL, "bad tokens/hidden/inter");
   if (a->top_k < 0 || (a->top_k == 0 && a->shared_expert_id < 0)) return fail(FCMOE_EINVAL, "top_k must be positive");
   if (a->experts <= 0 || a->experts > 1024) return fail(FCMOE_EINVAL, "experts must be in [1, 1024]");
   if (a->valid_experts <= 0 || a->valid_experts > a->experts) return fail(FCMOE_EINVAL, "bad valid_experts");
   if (a->shared_expert_id >= a->experts) return fail(FCMOE_EINVAL, "shared_expert_id out of range");
+  if (a->tokens > 65535) return fail(FCMOE_EINVAL, "tokens must be <= 65535");
+  return FCMOE_OK;
+}
+
+int check_common(const fcmoe_moe_args* a) {
+  int rc = check_shapes(a);
+  if (rc) return rc;
   if (a->tokens > 0 && (!a->x || !a->out || !a->w13 || !a->w2)) return fail(FCMOE_EINVAL, "NULL tensor");
   if (a->tokens > 0 && a->top_k > 0 && (!a->topk_ids || !a->topk_weights)) return fail(FCMOE_EINVAL, "NULL topk");
-  if (a->tokens > 65535) return fail(FCMOE_EINVAL, "tokens must be <= 65535");
   return FCMOE_OK;
 }
 
@@ -240,19 +246,20 @@ extern "C" int fcmoe_route_build(const void* topk_ids, int ids_is_i64, int64_t t
 // ------------------------------------------------------------------ W8A8 --
 
 extern "C" size_t fcmoe_w8a8_workspace_bytes(const fcmoe_moe_args* a) {
-  if (check_common(a)) return 0;
+  if (check_shapes(a)) return 0;
   Arena ar;
   w8a8_layout(a, ar);
   return ar.used + 256;
 }
 
 extern "C" int fcmoe_w8a8_forward(const fcmoe_moe_args* a, hipStream_t stream) {
-  int rc = check_common(a);
+  int rc = check_shapes(a);
   if (rc) return rc;
   if (a->activation != FCMOE_ACT_SILU_CLAMP10)
     return fail(FCMOE_EINVAL, "W8A8 supports only clamped SwiGLU with limit 10.0");
   if (a->hidden % 16 || a->inter % 16) return fail(FCMOE_EINVAL, "W8A8 requires H and F to be multiples of 16");
   if (a->skip_weighted) return fail(FCMOE_EINVAL, "W8A8 requires weighted TopK merge");
+  if ((rc = check_common(a))) return rc;
   if (!a->w13_scale || !a->w2_scale) return fail(FCMOE_EINVAL, "W8A8 scales are NULL");
   if (a->tokens == 0) return FCMOE_OK;
   Arena ar;
@@ -361,19 +368,20 @@ extern "C" int fcmoe_w8a8_stage_views(const fcmoe_moe_args* a, const int32_t** s
 // ------------------------------------------------------------------ BF16 --
 
 extern "C" size_t fcmoe_bf16_workspace_bytes(const fcmoe_moe_args* a) {
-  if (check_common(a)) return 0;
+  if (check_shapes(a)) return 0;
   Arena ar;
   bf16_layout(a, ar);
   return ar.used + 256;
 }
 
 extern "C" int fcmoe_bf16_forward(const fcmoe_moe_args* a, hipStream_t stream) {
-  int rc = check_common(a);
+  int rc = check_shapes(a);
   if (rc) return rc;
   if (a->activation < FCMOE_ACT_SILU || a->activation > FCMOE_ACT_SILU_CLAMP10)
     return fail(FCMOE_EINVAL, "unsupported activation");
   const int64_t kt = a->top_k + (a->shared_expert_id >= 0 ? 1 : 0);
   if (a->skip_weighted && kt != 1) return fail(FCMOE_EINVAL, "skip_weighted is only valid when top_k == 1");
+  if ((rc = check_common(a))) return rc;
   if (a->tokens == 0) return FCMOE_OK;
   Arena ar;
   ar.base = (char*)a->workspace;

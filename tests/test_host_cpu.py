@@ -1,0 +1,234 @@
+"""Host-side checks that need no GPU: the C ABI library loads and exports every
+symbol declared in include/fcmoe.h, the Python surface mirrors the
+reference's, and the wrappers' routing/validation logic (monkeypatched native
+calls, as the reference's own tests do: tests/test_moe_w8a8.py:105-162)."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+REPO = Path(__file__).resolve().parent.parent
+
+# fused_cpp.moe.__all__ (src/fused_cpp/moe/__init__.py:67-126)
+REFERENCE_MOE_ALL = {
+    "ASYNC_MOE_EXECUTION_STRICT", "ASYNC_MOE_EXECUTION_TAIL_POOL", "ASYNC_MOE_FULL_EXPERT_RANGE",
+    "ASYNC_MOE_PLACEMENT_FIXED", "ASYNC_MOE_PLACEMENT_TAIL_POOL", "ASYNC_MOE_PLAN_VERSION",
+    "ASYNC_MOE_RESIZE_NONE", "ASYNC_MOE_STAGE_EXPERT", "AsyncMoEPlanV2", "DEFAULT_MOE_COST_CACHE_DIR",
+    "MoePlannerRuntime", "PreparedBF16TiledFusedMoEWeights", "PreparedBF16TiledRoutedSharedMoEWeights",
+    "PreparedW8A16TiledFusedMoEWeights", "PreparedW8A8TiledFusedMoEWeights",
+    "PreparedW8A16TiledRoutedSharedMoEWeights", "PreparedW8A8TiledRoutedSharedMoEWeights",
+    "_HAS_BF16_TILED_FUSED_MOE", "_HAS_W8A8_TILED_FUSED_MOE", "available_fused_moe_bf16_tiled_backends",
+    "calibrate_moe_planner_quick", "enable_moe_planner_quick", "fused_moe_bf16_tiled",
+    "fused_moe_bf16_tiled_with_shared", "fused_moe_bf16_tiled_scheduled", "fused_moe_bf16_tiled_async",
+    "fused_moe_bf16_tiled_async_plan", "fused_moe_bf16_tiled_planned_staged", "fused_moe_bf16_tiled_vllm_staged",
+    "fused_moe_tiled", "fused_moe_w8a16_tiled", "fused_moe_w8a16_tiled_async_plan", "fused_moe_w8a8_tiled",
+    "fused_moe_w8a8_tiled_async_plan", "fused_moe_w8a16_tiled_with_shared", "fused_moe_w8a8_tiled_with_shared",
+    "shared_mlp_bf16_tiled", "fused_moe_naive", "get_default_moe_planner_runtime", "bf16_tiled_fused_moe",
+    "bf16_tiled_fused_moe_scheduled", "bf16_tiled_fused_moe_async", "bf16_tiled_fused_moe_async_plan",
+    "bf16_tiled_fused_moe_planned_staged", "bf16_tiled_fused_moe_vllm_staged", "naive_fused_moe",
+    "prepare_fused_moe_bf16_tiled_weights", "prepare_fused_moe_w8a16_tiled_weights",
+    "prepare_fused_moe_w8a16_tiled_quantized_weights", "prepare_fused_moe_w8a8_tiled_weights",
+    "prepare_fused_moe_w8a8_tiled_quantized_weights", "prepare_routed_shared_moe_bf16_tiled_weights",
+    "prepare_routed_shared_moe_w8a16_tiled_quantized_weights",
+    "prepare_routed_shared_moe_w8a8_tiled_quantized_weights", "prepare_shared_mlp_bf16_tiled_weights",
+    "prepare_bf16_tiled_fused_moe_weights", "set_default_moe_planner_runtime", "upgrade_legacy_async_plan",
+}
+# the torch-op reference implementation is not part of the GPU operator surface
+NOT_MIRRORED = {"fused_moe_naive", "naive_fused_moe"}
+
+REFERENCE_I8GEMM_ALL = {"PreparedI8GEMMWeight", "_supports_i8gemm", "dynamic_scaled_mm", "dynamic_scaled_mm_pair",
+                        "mm", "prepare"}
+
+
+def _declared_symbols() -> set[str]:
+    text = (REPO / "include" / "fcmoe.h").read_text()
+    return set(re.findall(r"\b(fcmoe_[a-z0-9_]+)\s*\(", text))
+
+
+def test_cabi_library_exports_every_declared_symbol():
+    from fused_cpp_amd import cabi
+
+    lib = ctypes.CDLL(str(cabi.LIB_PATH))
+    declared = _declared_symbols()
+    assert len(declared) >= 19
+    missing = [name for name in sorted(declared) if not hasattr(lib, name)]
+    assert not missing, f"libfcmoe.so lacks {missing}"
+    assert set(cabi.SIGNATURES) == declared  # the ctypes binding covers the whole header
+
+
+def test_cabi_host_only_calls():
+    from fused_cpp_amd import cabi
+
+    L = cabi.lib()
+    assert L.fcmoe_abi_version() == 1
+    assert L.fcmoe_packed_expert_bytes(1, 4096, 7168, 2) == 4096 * 7168
+    assert L.fcmoe_packed_expert_bytes(2, 22, 13, 2) == 2 * 16 * 64
+    assert L.fcmoe_packed_expert_bytes(3, 16, 16, 1) == -1
+    assert L.fcmoe_route_workspace_bytes(64, 8, 257, 256) > 0
+    args = cabi.MoeArgs()
+    args.tokens, args.hidden, args.inter, args.top_k, args.experts, args.valid_experts = 64, 7168, 2048, 8, 257, 257
+    args.shared_expert_id = 256
+    assert L.fcmoe_w8a8_workspace_bytes(ctypes.byref(args)) > 64 * 9 * 7168 * 4
+    # argument validation happens before any device work
+    args.activation = cabi.FCMOE_ACT_SILU
+    assert L.fcmoe_w8a8_forward(ctypes.byref(args), None) == -1
+    assert b"limit 10" in L.fcmoe_last_error()
+    args.experts = 2000
+    assert L.fcmoe_bf16_forward(ctypes.byref(args), None) == -1
+    assert b"experts" in L.fcmoe_last_error()
+
+
+def test_extension_module_loads():
+    from fused_cpp_amd import _native
+
+    assert _native.moe_C is not None, _native.NATIVE_ERROR
+    for name in ("fused_moe_w8a8_forward", "fused_moe_bf16_forward", "fused_moe_w8a8_prepare_weights",
+                 "fused_moe_bf16_prepare_weights", "i8gemm_prepare", "i8gemm_dynamic_scaled_mm"):
+        assert hasattr(_native.moe_C, name)
+
+
+def test_python_surface_mirrors_reference():
+    import fused_cpp_amd.i8gemm as i8
+    import fused_cpp_amd.moe as moe
+
+    assert REFERENCE_MOE_ALL - NOT_MIRRORED <= set(moe.__all__)
+    assert REFERENCE_I8GEMM_ALL <= set(i8.__all__)
+    w = moe.PreparedW8A8TiledFusedMoEWeights(w13=(torch.empty(1), 16, 16, torch.empty(1)),
+                                             w2=(torch.empty(1), 16, 16, torch.empty(1)))
+    assert w.fused_silu and w.backend_n_tile == 16
+
+
+def test_plan_v2_schema_shims():
+    from fused_cpp_amd.moe import AsyncMoEPlanV2, upgrade_legacy_async_plan
+
+    raw = upgrade_legacy_async_plan({"num_threads": 4, "thread_cpu_ids": [0, 1, 2, 3], "task_expert_ids": [0, 1],
+                                     "task_core_begins": [0, 2], "task_threads": [2, 2],
+                                     "task_dep_offsets": [0, 0, 0], "task_deps": []})
+    plan = AsyncMoEPlanV2.from_dict(raw)
+    assert plan.plan_version == 2 and plan.native_execution_mode == 0 and plan.native_early_merge == -1
+    with pytest.raises(ValueError, match="plan_version"):
+        AsyncMoEPlanV2.from_dict({**raw, "plan_version": 1})
+    with pytest.raises(ValueError, match="missing"):
+        AsyncMoEPlanV2.from_dict({"plan_version": 2})
+
+
+def test_planner_runtime_shims():
+    from fused_cpp_amd.moe import (MoePlannerRuntime, enable_moe_planner_quick, get_default_moe_planner_runtime,
+                                   set_default_moe_planner_runtime)
+
+    rt = enable_moe_planner_quick(hidden_size=7168, intermediate_size=2048, global_experts=256, local_experts=256,
+                                  shared_experts=1)
+    assert get_default_moe_planner_runtime() is rt
+    assert rt.plan_for_dispatch(None, None) is None
+    assert set_default_moe_planner_runtime(None) is rt
+    with pytest.raises(TypeError):
+        set_default_moe_planner_runtime(object())
+    with pytest.raises(ValueError):
+        MoePlannerRuntime(None, hidden_size=1, intermediate_size=1, global_experts=1, local_experts=1,
+                          shared_experts=2)
+
+
+@pytest.fixture
+def fake_backend(monkeypatch):
+    """Make the wrappers believe a device exists and route native calls to a recorder."""
+    from fused_cpp_amd.moe import bf16_tiled as mod
+
+    calls = {}
+    monkeypatch.setattr(mod, "_require_backend", lambda: None)
+    monkeypatch.setattr(mod, "_check_device_tensor", lambda t, name: None)
+
+    class FakeC:
+        def fused_moe_w8a8_forward(self, *args):
+            calls["w8a8"] = args
+            return args[0]
+
+        def fused_moe_bf16_forward(self, *args):
+            calls["bf16"] = args
+            return args[0]
+
+    monkeypatch.setattr(mod._native, "moe_C", FakeC())
+    return mod, calls
+
+
+def test_w8a8_routed_shared_wrapper_passes_shared_slot(fake_backend):
+    mod, calls = fake_backend
+    packed = mod.PreparedW8A8TiledFusedMoEWeights(w13=(torch.empty((3, 8)), 16, 32, torch.ones(3, 32)),
+                                                  w2=(torch.empty((3, 8)), 16, 16, torch.ones(3, 16)))
+    weights = mod.PreparedW8A8TiledRoutedSharedMoEWeights(packed=packed, routed_experts=2, shared_expert_id=2)
+    x = torch.zeros((2, 16), dtype=torch.bfloat16)
+    ids = torch.tensor([[0, 1], [1, 0]], dtype=torch.int64)
+    w = torch.tensor([[0.7, 0.3], [0.4, 0.6]], dtype=torch.float32)
+    mod.fused_moe_w8a8_tiled_with_shared(x, weights, w, ids, num_threads=4, routed_scaling_factor=2.5,
+                                         swiglu_limit=10.0)
+    args = calls["w8a8"]
+    assert args[11] == 2 and args[12] == 2.5 and args[13] == 2  # shared id, scale, routed ids < 2
+    assert torch.equal(args[10], ids)
+
+
+def test_w8a8_wrappers_reject_reference_error_cases(fake_backend):
+    mod, _ = fake_backend
+    w = mod.PreparedW8A8TiledFusedMoEWeights(w13=(torch.empty((1, 8)), 16, 16, torch.ones(1, 16)),
+                                             w2=(torch.empty((1, 8)), 8, 16, torch.ones(1, 16)))
+    x = torch.zeros((1, 16), dtype=torch.bfloat16)
+    ids = torch.zeros((1, 1), dtype=torch.int64)
+    with pytest.raises(ValueError, match="swiglu_limit=10.0"):
+        mod.fused_moe_w8a8_tiled_async_plan(x, w, torch.ones((1, 1)), ids, {"plan_version": 2}, swiglu_limit=0.0)
+    with pytest.raises(TypeError):
+        mod.fused_moe_w8a8_tiled(x, "not weights", torch.ones((1, 1)), ids)
+    with pytest.raises(RuntimeError, match="global_num_experts"):
+        mod.fused_moe_w8a8_tiled(x, w, torch.ones((1, 1)), ids, global_num_experts=4)
+    with pytest.raises(TypeError, match="integer"):
+        mod.fused_moe_w8a8_tiled(x, w, torch.ones((1, 1)), torch.zeros((1, 1)))
+
+
+def test_bf16_wrapper_activation_and_limit_rules(fake_backend):
+    mod, calls = fake_backend
+    w = mod.PreparedBF16TiledFusedMoEWeights(w13=(torch.empty((1, 8)), 16, 16), w2=(torch.empty((1, 8)), 8, 16),
+                                             fused_silu=True)
+    x = torch.zeros((1, 16), dtype=torch.bfloat16)
+    ids = torch.zeros((1, 1), dtype=torch.int32)
+    mod.fused_moe_bf16_tiled(x, w, torch.ones((1, 1)), ids, swiglu_limit=10.0)
+    assert calls["bf16"][11] == "silu_clamp10"
+    mod.fused_moe_bf16_tiled(x, w, torch.ones((1, 1)), ids, swiglu_limit=0.0)
+    assert calls["bf16"][11] == "silu"
+    with pytest.raises(ValueError, match="swiglu_limit=10.0"):
+        mod.fused_moe_bf16_tiled(x, w, torch.ones((1, 1)), ids, swiglu_limit=7.0)
+    with pytest.raises(ValueError, match="Unsupported MoE activation"):
+        mod.fused_moe_bf16_tiled(x, w, torch.ones((1, 1)), ids, activation="relu")
+    with pytest.raises(ValueError, match="skip_weighted"):
+        mod.fused_moe_bf16_tiled(x, w, torch.ones((1, 2)), torch.zeros((1, 2), dtype=torch.int32),
+                                 skip_weighted=True)
+    nf = mod.PreparedBF16TiledFusedMoEWeights(w13=(torch.empty((1, 8)), 16, 16), w2=(torch.empty((1, 8)), 8, 16))
+    with pytest.raises(ValueError, match="fuse_silu"):
+        mod.fused_moe_bf16_tiled(x, nf, torch.ones((1, 1)), ids, swiglu_limit=10.0)
+    with pytest.raises(ValueError, match="out must have shape"):
+        mod.fused_moe_bf16_tiled(x, w, torch.ones((1, 1)), ids, out=torch.empty((2, 16), dtype=torch.bfloat16))
+
+
+def test_fused_moe_tiled_dispatches_on_weight_type(fake_backend, monkeypatch):
+    mod, _ = fake_backend
+    w8 = mod.PreparedW8A8TiledFusedMoEWeights(w13=(torch.empty(1), 16, 16, torch.empty(1)),
+                                              w2=(torch.empty(1), 16, 16, torch.empty(1)))
+    expected = torch.zeros((1, 16), dtype=torch.bfloat16)
+    monkeypatch.setattr(mod, "fused_moe_w8a8_tiled", lambda *a, **k: expected)
+    assert mod.fused_moe_tiled(expected, w8, torch.ones((1, 1)), torch.zeros((1, 1), dtype=torch.int64),
+                               swiglu_limit=10.0) is expected
+    with pytest.raises(ValueError, match="bias"):
+        mod.fused_moe_tiled(expected, w8, torch.ones((1, 1)), torch.zeros((1, 1), dtype=torch.int64),
+                            w13_bias=torch.zeros(1))
+    with pytest.raises(TypeError):
+        mod.fused_moe_tiled(expected, object(), torch.ones((1, 1)), torch.zeros((1, 1), dtype=torch.int64))
+
+
+def test_w8a16_entry_points_raise_unavailable():
+    from fused_cpp_amd import moe
+
+    with pytest.raises(RuntimeError, match="W8A16"):
+        moe.fused_moe_w8a16_tiled(None, None, None, None)
+    with pytest.raises(RuntimeError, match="W8A16"):
+        moe.prepare_fused_moe_w8a16_tiled_weights(None, None)

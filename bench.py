@@ -296,6 +296,19 @@ def parity_check(cfg, res) -> dict:
     return {"tokens_checked": n, "bit_exact": bool(np.array_equal(ref, got))}
 
 
+def measured_traffic(config: str, stage: str):
+    """HBM bytes per launch of `stage` from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE passes (calibrated against a plain copy), if that workload was profiled."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", f"w8a8_decode_{config}_traffic.json")
+    if not os.path.exists(path):
+        path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", f"w8a8_prefill_{config}_traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f)["kernels"][stage]["traffic_bytes"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def measure(cfg, args, device, want_cpu: bool):
     res = run_gpu(cfg, args.steps, args.warmup, device, keep_host=want_cpu or cfg["kind"] == "w8a8")
     counts = expert_counts(cfg, res["ids"])
@@ -320,7 +333,8 @@ def measure(cfg, args, device, want_cpu: bool):
         achieved = a["ops"] / (avg_ms * 1e-3) / 1e12
         roof = {"bound": "mfma", "achieved": round(achieved, 1), "peak": peak_ops, "unit": "TFLOP/s",
                 "frac": round(achieved / peak_ops, 4)}
-    roof.update({"kernel": f"grouped_gemm {name}", "avg_launch_ms": round(avg_ms, 4), "traffic": None,
+    traffic = measured_traffic(args.config, name)
+    roof.update({"kernel": f"grouped_gemm {name}", "avg_launch_ms": round(avg_ms, 4), "traffic": traffic,
                  "algorithmic_bytes": a["bytes"], "algorithmic_ops": a["ops"], "experts": a["experts"],
                  "rows": a["rows"]})
     layer_roof_s = max(layer_bytes / (HBM_PEAK_GBPS * 1e9), layer_ops / (peak_ops * 1e12))
@@ -353,7 +367,20 @@ def main() -> int:
     ap.add_argument("--prefill", action="store_true", help="also measure C3 prefill as 'secondary'")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-routes", type=int, default=2048, help="route sample of the CPU baseline at prefill")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a plain 256 MiB device copy 5 times (scale reference for rocprofv3 "
+                         "FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
+    if args.copy_calibration:
+        import torch
+
+        src = torch.ones(256 << 20, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes": 256 << 20, "launches": 5}))
+        return 0
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only: every box has one MI355X; "
                                    "run with --gpus 1 (multi-GPU sharding is described in DESIGN.md)"}))

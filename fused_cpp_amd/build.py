@@ -36,6 +36,10 @@ HIP_FLAGS = [
     "-fPIC",
     "-std=c++20",
     "-ffp-contract=off",
+    # MFMA accumulators in ordinary VGPRs: avoids AGPR<->VGPR copy storms and
+    # lets the 256-row tile run 2 waves/SIMD (234 VGPRs, no AGPRs)
+    "-mllvm",
+    "-amdgpu-mfma-vgpr-form=1",
     "-Xclang",
     "-target-feature",
     "-Xclang",

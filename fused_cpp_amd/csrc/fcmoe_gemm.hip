@@ -123,10 +123,10 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(GemmParams p, in
     }
   }
   const uint8_t* wbase = (const uint8_t*)p.w + (int64_t)expert * p.w_expert_bytes;
-  const uint4* bptr[FN];
+  const v4i* bptr[FN];
 #pragma unroll
   for (int j = 0; j < FN; ++j)
-    bptr[j] = (const uint4*)(wbase + (tvalid[j] ? gtile[j] : 0) * p.k_chunks * 1024) + lane;
+    bptr[j] = (const v4i*)(wbase + (tvalid[j] ? gtile[j] : 0) * p.k_chunks * 1024) + lane;
 
   const int64_t lda_bytes = p.lda * (I8 ? 1 : 2);
   const int64_t kc = p.k_chunks;
@@ -148,14 +148,12 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(GemmParams p, in
     for (int i = 0; i < FM; ++i) afrag[i] = row_ptr(i * 16 + lane % 16) + (lane / 16) * 16;
   } else {
     static_assert(UNITS % kThreads == 0, "LDS A tiles must split evenly over the workgroup");
-#pragma unroll
-    for (int u = 0; u < UPT; ++u) {
-      const int unit = tid + u * kThreads;
-      const int r = unit / 4;
-      const int c16 = unit % 4;
-      adst[u] = r * ROWB + c16 * 16;
-      asrc[u] = row_ptr(r) + c16 * 16;
-    }
+    // compile-time unit indices keep these arrays in registers
+    [&]<int... U>(std::integer_sequence<int, U...>) {
+      ((adst[U] = ((tid + U * kThreads) / 4) * ROWB + ((tid + U * kThreads) % 4) * 16,
+        asrc[U] = row_ptr((tid + U * kThreads) / 4) + ((tid + U * kThreads) % 4) * 16),
+       ...);
+    }(std::make_integer_sequence<int, UPT>{});
   }
 
   // Prefetch ring: stage slot b holds the weight (and direct A) fragments of
@@ -167,9 +165,9 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(GemmParams p, in
   // register sets, alternating by chunk parity) and stored to the LDS buffer
   // of the next chunk just before the barrier.
   static_assert(ADIRECT || NB % 2 == 0, "LDS path needs an even ring");
-  uint4 bq[NB][FN];
-  uint4 aq[ADIRECT ? NB : 1][ADIRECT ? FM : 1];
-  uint4 areg[ADIRECT ? 1 : 2][ADIRECT ? 1 : UPT];
+  v4i bq[NB][FN];
+  v4i aq[ADIRECT ? NB : 1][ADIRECT ? FM : 1];
+  v4i areg[ADIRECT ? 1 : 2][ADIRECT ? 1 : UPT];
 
   // Loads are branch-free (a conditional load splits the block and the
   // compiler then drains every outstanding load before the next MFMA). Chunks
@@ -182,30 +180,31 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(GemmParams p, in
       if constexpr (ADIRECT) {
         // Small tiles read each weight byte once: nontemporal loads stream it
         // past the caches (measured ~12% more read bandwidth on MI355X).
-        const v4i t = __builtin_nontemporal_load((const v4i*)(bptr[j] + cc * kWave));
-        bq[slot][j] = __builtin_bit_cast(uint4, t);
+        bq[slot][j] = __builtin_nontemporal_load(bptr[j] + cc * kWave);
       } else {
         bq[slot][j] = bptr[j][cc * kWave];
       }
     }
     if constexpr (ADIRECT) {
 #pragma unroll
-      for (int i = 0; i < FM; ++i) aq[slot][i] = *(const uint4*)(afrag[i] + cc * 64);
+      for (int i = 0; i < FM; ++i) aq[slot][i] = *(const v4i*)(afrag[i] + cc * 64);
     }
   };
   auto load_a_regs = [&](int64_t c, auto set_c) {
     if constexpr (!ADIRECT) {
       constexpr int set = decltype(set_c)::value;
       const int64_t cc = c < kc ? c : kc - 1;
-#pragma unroll
-      for (int u = 0; u < UPT; ++u) areg[set][u] = *(const uint4*)(asrc[u] + cc * 64);
+      [&]<int... U>(std::integer_sequence<int, U...>) {
+        ((areg[set][U] = *(const v4i*)(asrc[U] + cc * 64)), ...);
+      }(std::make_integer_sequence<int, UPT>{});
     }
   };
   auto store_a_lds = [&](int buf, auto set_c) {
     if constexpr (!ADIRECT) {
       constexpr int set = decltype(set_c)::value;
-#pragma unroll
-      for (int u = 0; u < UPT; ++u) *(uint4*)(&sA[buf][adst[u]]) = areg[set][u];
+      [&]<int... U>(std::integer_sequence<int, U...>) {
+        ((*(v4i*)(&sA[buf][adst[U]]) = areg[set][U]), ...);
+      }(std::make_integer_sequence<int, UPT>{});
     }
   };
 
@@ -219,17 +218,17 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(GemmParams p, in
     constexpr int slot = decltype(slot_c)::value;
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
-      uint4 av;
+      v4i av;
       if constexpr (ADIRECT) {
         av = aq[slot][i];
       } else {
         const int r = wm * FM * 16 + i * 16 + (lane % 16);
-        av = *(const uint4*)(&sA[c & 1][r * ROWB + (lane / 16) * 16]);
+        av = *(const v4i*)(&sA[c & 1][r * ROWB + (lane / 16) * 16]);
       }
 #pragma unroll
       for (int j = 0; j < FN; ++j) {
         if constexpr (I8) {
-          acc[i][j] = mfma(__builtin_bit_cast(v4i, av), __builtin_bit_cast(v4i, bq[slot][j]), acc[i][j]);
+          acc[i][j] = mfma(av, bq[slot][j], acc[i][j]);
         } else {
           acc[i][j] = mfma(__builtin_bit_cast(v8bf, av), __builtin_bit_cast(v8bf, bq[slot][j]), acc[i][j]);
         }

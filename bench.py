@@ -34,7 +34,7 @@ import numpy as np
 HBM_PEAK_GBPS = 8000.0
 INT8_PEAK_TOPS = 5000.0
 BF16_PEAK_TFLOPS = 2500.0
-CLASS_BM = (16, 32, 64, 128, 256)
+CLASS_BM = (16, 32, 64, 128, 192, 256)
 
 CONFIGS = {
     "c0": dict(kind="bf16", T=32, H=1024, I=512, E=8, k=2, shared=False, scale=1.0, skew=None,

@@ -80,8 +80,8 @@ SIGNATURES = {
 
 FCMOE_STAGE_COUNT = 24
 STAGE_NAMES = {0: "route", 1: "quant", 2: "requant", 3: "act", 4: "combine",
-               **{8 + c: f"w13_bm{bm}" for c, bm in enumerate((16, 32, 64, 128, 256))},
-               **{16 + c: f"w2_bm{bm}" for c, bm in enumerate((16, 32, 64, 128, 256))}}
+               **{8 + c: f"w13_bm{bm}" for c, bm in enumerate((16, 32, 64, 128, 192, 256))},
+               **{16 + c: f"w2_bm{bm}" for c, bm in enumerate((16, 32, 64, 128, 192, 256))}}
 
 
 def stage_timing_enable(on: bool = True) -> None:

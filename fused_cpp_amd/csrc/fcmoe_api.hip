@@ -18,8 +18,8 @@ thread_local std::string g_error;
 // Tile rows of the grouped GEMM classes (the tokens-per-expert selector): an
 // expert with c routed rows runs in the smallest class with BM >= c; larger
 // experts (the shared expert at prefill) are split into BM=256 tiles.
-constexpr int kClassBM[] = {16, 32, 64, 128, 256};
-constexpr int kNumClasses = 5;
+constexpr int kClassBM[] = {16, 32, 64, 128, 192, 256};
+constexpr int kNumClasses = 6;
 // Decode: when an expert averages at most this many routed rows, everything
 // (the shared expert too, in several 16-row tiles) runs in the single BM=16
 // class: one launch per GEMM stage, no empty class launches, and weight
@@ -164,6 +164,77 @@ struct Stage {
   }
 };
 
+// ---- tile-class concurrency: the class launches of one GEMM stage are
+// independent (disjoint experts), so at prefill they run on side streams
+// forked from the caller's stream with events and joined back: the HBM-bound
+// small-tile classes overlap the MFMA-bound 256-row class. Streams and events
+// are per host thread and device (created on first use, default priority,
+// kept until process exit); a stage with one class launches inline.
+struct SideStreams {
+  bool ready = false;
+  hipStream_t s[kNumClasses] = {};
+  hipEvent_t fork = nullptr;
+  hipEvent_t join[kNumClasses] = {};
+};
+constexpr int kMaxDevices = 64;
+thread_local SideStreams t_side[kMaxDevices];
+
+int side_streams(SideStreams** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return fail(FCMOE_EDEVICE, "hipGetDevice failed");
+  SideStreams& ss = t_side[dev];
+  if (!ss.ready) {
+    if (hipEventCreateWithFlags(&ss.fork, hipEventDisableTiming) != hipSuccess)
+      return fail(FCMOE_EDEVICE, "hipEventCreate failed");
+    for (int c = 0; c < kNumClasses; ++c) {
+      if (hipStreamCreateWithFlags(&ss.s[c], hipStreamNonBlocking) != hipSuccess ||
+          hipEventCreateWithFlags(&ss.join[c], hipEventDisableTiming) != hipSuccess)
+        return fail(FCMOE_EDEVICE, "side stream creation failed");
+    }
+    ss.ready = true;
+  }
+  *out = &ss;
+  return FCMOE_OK;
+}
+
+// Launch one GEMM stage: class c runs gemm(c, stream_c). With several
+// classes, the largest class (last) stays on the caller's stream and is
+// launched first; the others are forked.
+bool timing_on();
+
+template <typename F>
+int run_classes(const TileClasses& tc, hipStream_t stream, F&& gemm) {
+  // Stage timing brackets each launch with events on its stream, so it runs
+  // the classes one after another: each event pair then times one kernel.
+  if (tc.n <= 1 || timing_on()) {
+    for (int c = 0; c < tc.n; ++c) {
+      const int rc = gemm(c, stream);
+      if (rc) return rc;
+    }
+    return FCMOE_OK;
+  }
+  SideStreams* ss = nullptr;
+  int rc = side_streams(&ss);
+  if (rc) return rc;
+  if (hipEventRecord(ss->fork, stream) != hipSuccess) return fail(FCMOE_EDEVICE, "hipEventRecord failed");
+  if ((rc = gemm(tc.n - 1, stream))) return rc;
+  for (int c = tc.n - 2; c >= 0; --c) {
+    if (hipStreamWaitEvent(ss->s[c], ss->fork, 0) != hipSuccess) return fail(FCMOE_EDEVICE, "stream wait failed");
+    if ((rc = gemm(c, ss->s[c]))) return rc;
+    if (hipEventRecord(ss->join[c], ss->s[c]) != hipSuccess) return fail(FCMOE_EDEVICE, "hipEventRecord failed");
+  }
+  for (int c = tc.n - 2; c >= 0; --c)
+    if (hipStreamWaitEvent(stream, ss->join[c], 0) != hipSuccess) return fail(FCMOE_EDEVICE, "stream wait failed");
+  return FCMOE_OK;
+}
+
+bool timing_on() {
+  StageTimer& t = timer();
+  std::lock_guard<std::mutex> g(t.mu);
+  return t.on;
+}
+
 __global__ void pad_rows_kernel(const uint16_t* x, int64_t rows, int64_t cols, int64_t ld, uint16_t* dst) {
   const int64_t r = blockIdx.y;
   const int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -301,14 +372,14 @@ extern "C" int fcmoe_w8a8_forward(const fcmoe_moe_args* a, hipStream_t stream) {
   g13.scale_row = L.xs;
   g13.scale_col = a->w13_scale;
   g13.rowmax = L.rb.rowmax;
-  for (int c = 0; c < L.tc.n; ++c) {
+  rc = run_classes(L.tc, stream, [&](int c, hipStream_t s) {
     GemmParams p = g13;
     p.tiles = L.rb.tiles + 2 * tile_offset(L.tc, c);
     p.tile_count = L.rb.tile_count + c;
-    Stage st(FCMOE_STAGE_W13_CLASS0 + c, stream);
-    rc = gemm_launch(kEpiW13SwigluI8, L.tc.bm[c], p, L.tc.bound[c], stream);
-    if (rc) return rc;
-  }
+    Stage st(FCMOE_STAGE_W13_CLASS0 + c, s);
+    return gemm_launch(kEpiW13SwigluI8, L.tc.bm[c], p, L.tc.bound[c], s);
+  });
+  if (rc) return rc;
   {
     Stage st(FCMOE_STAGE_REQUANT, stream);
     rc = requant_launch(L.y, L.ip, L.routes, I, L.rb.rowmax, L.q2, L.ip, L.s2row, stream);
@@ -333,14 +404,14 @@ extern "C" int fcmoe_w8a8_forward(const fcmoe_moe_args* a, hipStream_t stream) {
   g2.scale_row = L.s2row;
   g2.scale_col = a->w2_scale;
   g2.sorted_routes = L.rb.sorted_routes;
-  for (int c = 0; c < L.tc.n; ++c) {
+  rc = run_classes(L.tc, stream, [&](int c, hipStream_t s) {
     GemmParams p = g2;
     p.tiles = L.rb.tiles + 2 * tile_offset(L.tc, c);
     p.tile_count = L.rb.tile_count + c;
-    Stage st(FCMOE_STAGE_W2_CLASS0 + c, stream);
-    rc = gemm_launch(kEpiW2RouteI8, L.tc.bm[c], p, L.tc.bound[c], stream);
-    if (rc) return rc;
-  }
+    Stage st(FCMOE_STAGE_W2_CLASS0 + c, s);
+    return gemm_launch(kEpiW2RouteI8, L.tc.bm[c], p, L.tc.bound[c], s);
+  });
+  if (rc) return rc;
   Stage st(FCMOE_STAGE_COMBINE, stream);
   return combine_launch(L.route_out, L.rb.route_weight, L.rb.route_pos, a->tokens, L.kt, H, 0, 0, a->out, stream);
 }
@@ -428,14 +499,14 @@ extern "C" int fcmoe_bf16_forward(const fcmoe_moe_args* a, hipStream_t stream) {
   g13.ldo = fused ? L.ip : L.gu_ld;
   g13.bias = a->w13_bias;
   g13.activation = a->activation;
-  for (int c = 0; c < L.tc.n; ++c) {
+  rc = run_classes(L.tc, stream, [&](int c, hipStream_t s) {
     GemmParams p = g13;
     p.tiles = L.rb.tiles + 2 * tile_offset(L.tc, c);
     p.tile_count = L.rb.tile_count + c;
-    Stage st(FCMOE_STAGE_W13_CLASS0 + c, stream);
-    rc = gemm_launch(fused ? kEpiW13ActBf16 : kEpiRawF32Bias, L.tc.bm[c], p, L.tc.bound[c], stream);
-    if (rc) return rc;
-  }
+    Stage st(FCMOE_STAGE_W13_CLASS0 + c, s);
+    return gemm_launch(fused ? kEpiW13ActBf16 : kEpiRawF32Bias, L.tc.bm[c], p, L.tc.bound[c], s);
+  });
+  if (rc) return rc;
   if (!fused) {
     Stage st(FCMOE_STAGE_ACT, stream);
     rc = act_bf16_launch(L.gate_up, L.gu_ld, L.routes, I, round_up(I, 16), a->activation, L.y, L.ip, stream);
@@ -457,14 +528,14 @@ extern "C" int fcmoe_bf16_forward(const fcmoe_moe_args* a, hipStream_t stream) {
   g2.ldo = H;
   g2.bias = a->w2_bias;
   g2.sorted_routes = L.rb.sorted_routes;
-  for (int c = 0; c < L.tc.n; ++c) {
+  rc = run_classes(L.tc, stream, [&](int c, hipStream_t s) {
     GemmParams p = g2;
     p.tiles = L.rb.tiles + 2 * tile_offset(L.tc, c);
     p.tile_count = L.rb.tile_count + c;
-    Stage st(FCMOE_STAGE_W2_CLASS0 + c, stream);
-    rc = gemm_launch(kEpiW2RouteBf16, L.tc.bm[c], p, L.tc.bound[c], stream);
-    if (rc) return rc;
-  }
+    Stage st(FCMOE_STAGE_W2_CLASS0 + c, s);
+    return gemm_launch(kEpiW2RouteBf16, L.tc.bm[c], p, L.tc.bound[c], s);
+  });
+  if (rc) return rc;
   const int tree = (kt == 2 || kt == 4 || kt == 6 || kt == 8) ? 1 : 0;
   Stage st(FCMOE_STAGE_COMBINE, stream);
   return combine_launch(L.route_out, L.rb.route_weight, L.rb.route_pos, a->tokens, kt, H, tree, a->skip_weighted,

@@ -42,39 +42,69 @@ __device__ __forceinline__ float tree_merge(const float* route_out, const float*
   return TreeSum<0, K>::run(v);
 }
 
+// VW output channels per thread (VW = 4 when hidden % 4 == 0: 16-byte route
+// loads, 8-byte bf16 stores; else 1). Each channel's arithmetic is identical
+// to the scalar form.
+template <int VW>
 __global__ __launch_bounds__(256) void combine_kernel(const float* route_out, const float* route_weight,
                                                        const int32_t* route_pos, int64_t tokens, int kt,
                                                        int64_t hidden, int tree, int skip_weighted, uint16_t* out) {
   const int64_t t = blockIdx.y;
-  const int64_t h = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (t >= tokens || h >= hidden) return;
+  const int64_t h0 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * VW;
+  if (t >= tokens || h0 >= hidden) return;
   const int64_t r0 = t * kt;
-  float acc = 0.0f;
+  float acc[VW];
+#pragma unroll
+  for (int v = 0; v < VW; ++v) acc[v] = 0.0f;
+  auto load = [&](int64_t r, float (&dst)[VW]) {
+    if constexpr (VW == 4) {
+      const float4 q = *(const float4*)(route_out + r * hidden + h0);
+      dst[0] = q.x;
+      dst[1] = q.y;
+      dst[2] = q.z;
+      dst[3] = q.w;
+    } else {
+      dst[0] = route_out[r * hidden + h0];
+    }
+  };
   if (skip_weighted) {
-    acc = route_pos[r0] >= 0 ? route_out[r0 * hidden + h] : 0.0f;
+    if (route_pos[r0] >= 0) load(r0, acc);
   } else if (tree) {
-    switch (kt) {
-      case 2:
-        acc = tree_merge<2>(route_out, route_weight, r0, hidden, h);
-        break;
-      case 4:
-        acc = tree_merge<4>(route_out, route_weight, r0, hidden, h);
-        break;
-      case 6:
-        acc = tree_merge<6>(route_out, route_weight, r0, hidden, h);
-        break;
-      default:
-        acc = tree_merge<8>(route_out, route_weight, r0, hidden, h);
-        break;
+#pragma unroll
+    for (int v = 0; v < VW; ++v) {
+      switch (kt) {
+        case 2:
+          acc[v] = tree_merge<2>(route_out, route_weight, r0, hidden, h0 + v);
+          break;
+        case 4:
+          acc[v] = tree_merge<4>(route_out, route_weight, r0, hidden, h0 + v);
+          break;
+        case 6:
+          acc[v] = tree_merge<6>(route_out, route_weight, r0, hidden, h0 + v);
+          break;
+        default:
+          acc[v] = tree_merge<8>(route_out, route_weight, r0, hidden, h0 + v);
+          break;
+      }
     }
   } else {
     for (int s = 0; s < kt; ++s) {
       const int64_t r = r0 + s;
       if (route_pos[r] < 0) continue;
-      acc = __builtin_fmaf(route_out[r * hidden + h], route_weight[r], acc);
+      const float w = route_weight[r];
+      float v4[VW];
+      load(r, v4);
+#pragma unroll
+      for (int v = 0; v < VW; ++v) acc[v] = __builtin_fmaf(v4[v], w, acc[v]);
     }
   }
-  out[t * hidden + h] = f32_to_bf16(acc);
+  if constexpr (VW == 4) {
+    const uint32_t lo = (uint32_t)f32_to_bf16(acc[0]) | ((uint32_t)f32_to_bf16(acc[1]) << 16);
+    const uint32_t hi = (uint32_t)f32_to_bf16(acc[2]) | ((uint32_t)f32_to_bf16(acc[3]) << 16);
+    *(uint2*)(out + t * hidden + h0) = make_uint2(lo, hi);
+  } else {
+    out[t * hidden + h0] = f32_to_bf16(acc[0]);
+  }
 }
 
 }  // namespace
@@ -83,8 +113,12 @@ int combine_launch(const float* route_out, const float* route_weight, const int3
                    int64_t kt, int64_t hidden, int tree, int skip_weighted, uint16_t* out, hipStream_t stream) {
   if (tokens <= 0) return FCMOE_OK;
   if (tokens > 65535) return fail(FCMOE_EINVAL, "too many tokens");
-  hipLaunchKernelGGL(combine_kernel, dim3((unsigned)ceil_div(hidden, 256), (unsigned)tokens), dim3(256), 0, stream,
-                     route_out, route_weight, route_pos, tokens, (int)kt, hidden, tree, skip_weighted, out);
+  if (hidden % 4 == 0)
+    hipLaunchKernelGGL(combine_kernel<4>, dim3((unsigned)ceil_div(hidden / 4, 256), (unsigned)tokens), dim3(256), 0,
+                       stream, route_out, route_weight, route_pos, tokens, (int)kt, hidden, tree, skip_weighted, out);
+  else
+    hipLaunchKernelGGL(combine_kernel<1>, dim3((unsigned)ceil_div(hidden, 256), (unsigned)tokens), dim3(256), 0,
+                       stream, route_out, route_weight, route_pos, tokens, (int)kt, hidden, tree, skip_weighted, out);
   return check_launch("combine");
 }
 

@@ -395,6 +395,8 @@ int launch_bm(int bm, const GemmParams& p, int64_t max_tiles, hipStream_t stream
       return launch_cfg<I8, EPI, 1, 4, 4, 4, 4, false>(p, max_tiles, stream);
     case 128:
       return launch_cfg<I8, EPI, 2, 2, 4, 4, 4, false>(p, max_tiles, stream);
+    case 192:
+      return launch_cfg<I8, EPI, 2, 2, 6, 4, 2, false>(p, max_tiles, stream);
     case 256:
       return launch_cfg<I8, EPI, 2, 2, 8, 4, 2, false>(p, max_tiles, stream);
     default:

@@ -173,7 +173,7 @@ int fcmoe_w8a8_stage_views(const fcmoe_moe_args* args, const int32_t** sorted_ro
 /* ---- stage timing ------------------------------------------------------ */
 
 /* Stage ids for fcmoe_stage_timing_read. W13 / W2 class stages are per tile
- * class c (BM = 16, 32, 64, 128, 256 for c = 0..4). */
+ * class c (BM = 16, 32, 64, 128, 192, 256 for c = 0..5). */
 #define FCMOE_STAGE_ROUTE 0
 #define FCMOE_STAGE_QUANT 1
 #define FCMOE_STAGE_REQUANT 2

@@ -87,7 +87,8 @@ def test_quant_rows_ties_to_even_matches_oracle(gpu, oracle_lib, f32):
     [
         ([1, 0, 3, 16, 17], 64, 48),            # BM 16 / 32 classes, N not a multiple of 64
         ([33, 64, 65, 128], 128, 64),           # BM 64 / 128
-        ([129, 256, 600, 0, 2], 192, 80),       # BM 256 and a multi-tile expert
+        ([129, 256, 600, 0, 2], 192, 80),       # BM 192 / 256 and a multi-tile expert
+        ([150, 193, 7, 0, 64], 128, 48),        # BM 192 edges
         ([5, 2, 300], 7168, 64),                # DSv3 hidden as K
     ],
 )

@@ -17,6 +17,7 @@ disabled.
 from __future__ import annotations
 
 import os
+import re
 import subprocess
 import sys
 import sysconfig
@@ -29,7 +30,7 @@ CSRC = PKG / "csrc"
 ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 ARCH = os.environ.get("FCMOE_OFFLOAD_ARCH", "gfx950")
 
-HIP_SOURCES = ["fcmoe_api.hip", "fcmoe_route.hip", "fcmoe_quant.hip", "fcmoe_gemm.hip", "fcmoe_combine.hip"]
+HIP_SOURCES = ["fcmoe_api.hip", "fcmoe_route.hip", "fcmoe_quant.hip", "fcmoe_gemm.hip", "fcmoe_combine.hip", "fcmoe_router.hip"]
 HIP_FLAGS = [
     f"--offload-arch={ARCH}",
     "-O3",
@@ -51,11 +52,24 @@ EXT = PKG / ("_moe_C" + sysconfig.get_config_var("EXT_SUFFIX"))
 BUILD_DIR = PKG / "_build"
 
 
-def _run(cmd: list[str]) -> None:
+def _run(cmd: list[str]) -> str:
     proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
     if proc.returncode != 0:
         sys.stderr.write(proc.stdout)
         raise RuntimeError(f"build step failed ({proc.returncode}): {' '.join(cmd[:3])} ...")
+    return proc.stdout
+
+
+_SCRATCH_RE = re.compile(r"Function Name: (\S+).*?ScratchSize \[bytes/lane\]: (\d+)", re.S)
+
+
+def _check_no_scratch(src: str, remarks: str) -> None:
+    """Refuse kernels that spill to scratch: every kernel here is sized to keep
+    its working set in registers, and a spill means a tile configuration
+    exceeds the register budget it was designed for."""
+    spilled = [(name, int(n)) for name, n in _SCRATCH_RE.findall(remarks) if int(n) > 0]
+    if spilled:
+        raise RuntimeError(f"{src}: kernels use scratch (register spills): {spilled[:4]}")
 
 
 def build_lib() -> Path:
@@ -65,7 +79,9 @@ def build_lib() -> Path:
 
     def compile_one(src: str) -> str:
         obj = BUILD_DIR / (src + ".o")
-        _run([hipcc, *HIP_FLAGS, "-c", str(CSRC / src), "-o", str(obj)])
+        remarks = _run([hipcc, *HIP_FLAGS, "-Rpass-analysis=kernel-resource-usage", "-c", str(CSRC / src), "-o",
+                        str(obj)])
+        _check_no_scratch(src, remarks)
         return str(obj)
 
     with ThreadPoolExecutor(max_workers=min(len(HIP_SOURCES), os.cpu_count() or 1)) as ex:

@@ -65,6 +65,7 @@ SIGNATURES = {
     "fcmoe_route_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64]),
     "fcmoe_route_build": (_I, [_P, _I, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _SZ, _P]),
     "fcmoe_quantize_rows": (_I, [_P, _I, _I64, _I64, _I, _P, _I64, _P, _P]),
+    "fcmoe_router_topk": (_I, [_P, _I64, _I64, _I64, _I, ctypes.c_float, _P, _I, _P, _P]),
     "fcmoe_w8a8_workspace_bytes": (_SZ, [ctypes.POINTER(MoeArgs)]),
     "fcmoe_w8a8_forward": (_I, [ctypes.POINTER(MoeArgs), _P]),
     "fcmoe_bf16_workspace_bytes": (_SZ, [ctypes.POINTER(MoeArgs)]),

@@ -71,6 +71,12 @@ __device__ __forceinline__ int wave_sum(int v) {
   return v;
 }
 
+// Butterfly sum: every lane ends with the same value (same pairing order).
+__device__ __forceinline__ float wave_sum(float v) {
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
 __host__ __device__ __forceinline__ int64_t round_up(int64_t v, int64_t q) { return (v + q - 1) / q * q; }
 __host__ __device__ __forceinline__ int64_t ceil_div(int64_t v, int64_t q) { return (v + q - 1) / q; }
 

@@ -31,7 +31,6 @@ namespace fcmoe {
 
 namespace {
 
-constexpr int kThreads = 256;
 
 template <bool I8>
 struct Acc;
@@ -65,13 +64,18 @@ __device__ __forceinline__ float act_bf16_mode(float g, float u, int mode) {
 // Barrier for the LDS A buffers: waits only for this wave's LDS traffic
 // (lgkmcnt), not for the weight loads still in flight (a __syncthreads fence
 // would also drain vmcnt and empty the prefetch ring).
+// The builtin (not inline asm) lets the compiler's wait-count pass see the
+// wait, so it does not wait again for LDS reads this one already covered.
+// gfx9 s_waitcnt immediate: vmcnt [3:0]+[15:14], expcnt [6:4], lgkmcnt
+// [11:8]; 0xC07F = lgkmcnt(0), the other counters unconstrained.
 __device__ __forceinline__ void lds_barrier() {
-  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xC07F);
   __builtin_amdgcn_s_barrier();
 }
 
 template <bool I8, int EPI, int WM, int WN, int FM, int FN, int NB, bool ADIRECT>
-__global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(GemmParams p, int n_blocks) {
+__global__ __launch_bounds__(WM * WN * kWave) void grouped_gemm_kernel(GemmParams p, int n_blocks) {
+  constexpr int kThreads = WM * WN * kWave;
   constexpr int BM = WM * FM * 16;
   constexpr int ROWB = 64 + 16;                    // LDS row stride (bytes): 16 rows hit distinct banks
   constexpr int UNITS = BM * 4;                    // 16-byte A units per 64-byte K chunk
@@ -80,7 +84,7 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(GemmParams p, in
   static_assert(!ADIRECT || WM == 1, "direct A fragments assume one wave row");
   typedef typename Acc<I8>::type AccT;
 
-  __shared__ __attribute__((aligned(16))) uint8_t sA[ADIRECT ? 1 : 2][ADIRECT ? 16 : BM * ROWB];
+  __shared__ __attribute__((aligned(16))) uint8_t sA[ADIRECT ? 1 : 3][ADIRECT ? 16 : BM * ROWB];
 
   // Tiles run last-first: the route kernel lists experts in id order and the
   // appended shared expert (the largest) is last, so it starts first.
@@ -156,18 +160,25 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(GemmParams p, in
     }(std::make_integer_sequence<int, UPT>{});
   }
 
-  // Prefetch ring: stage slot b holds the weight (and direct A) fragments of
-  // one 64-byte K chunk; chunk c+NB-1 is issued before chunk c is consumed, so
+  // Prefetch ring: slot s holds the weight (and direct A) fragments of one
+  // 64-byte K chunk; chunk c+NB-1 is issued before chunk c is consumed, so
   // NB-1 chunks of loads stay in flight per wave. Slots are compile-time
-  // indices (the loop body is unrolled NB times), letting the compiler wait
-  // only for the slot being consumed.
-  // LDS path: A chunks are loaded to registers two chunks ahead (two
-  // register sets, alternating by chunk parity) and stored to the LDS buffer
-  // of the next chunk just before the barrier.
-  static_assert(ADIRECT || NB % 2 == 0, "LDS path needs an even ring");
+  // indices (the loop body is unrolled), letting the compiler wait only for
+  // the slot being consumed.
+  //
+  // LDS path (three A buffers, chunk c in buffer c % 3): A(c) is loaded to
+  // registers in iteration c-3 (two register sets, by chunk parity), stored
+  // to its buffer at the start of iteration c-2 and made visible by the
+  // barrier that ends iteration c-2. Iteration c reads buffer c % 3 with the
+  // fragment reads running two fragments ahead of the MFMAs, and ends by
+  // reading the first two fragments of chunk c+1, so the next iteration's
+  // MFMAs start right after its barrier.
+  constexpr int U = (ADIRECT || NB % 2 == 0) ? NB : 2 * NB;  // unroll: slot and set are constants
+  static_assert(ADIRECT || FM >= 3, "the fragment ring runs two fragments ahead");
   v4i bq[NB][FN];
   v4i aq[ADIRECT ? NB : 1][ADIRECT ? FM : 1];
   v4i areg[ADIRECT ? 1 : 2][ADIRECT ? 1 : UPT];
+  v4i af[ADIRECT ? 1 : FM];  // LDS fragments of the current chunk
 
   // Loads are branch-free (a conditional load splits the block and the
   // compiler then drains every outstanding load before the next MFMA). Chunks
@@ -194,19 +205,21 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(GemmParams p, in
     if constexpr (!ADIRECT) {
       constexpr int set = decltype(set_c)::value;
       const int64_t cc = c < kc ? c : kc - 1;
-      [&]<int... U>(std::integer_sequence<int, U...>) {
-        ((areg[set][U] = *(const v4i*)(asrc[U] + cc * 64)), ...);
+      [&]<int... Q>(std::integer_sequence<int, Q...>) {
+        ((areg[set][Q] = *(const v4i*)(asrc[Q] + cc * 64)), ...);
       }(std::make_integer_sequence<int, UPT>{});
     }
   };
   auto store_a_lds = [&](int buf, auto set_c) {
     if constexpr (!ADIRECT) {
       constexpr int set = decltype(set_c)::value;
-      [&]<int... U>(std::integer_sequence<int, U...>) {
-        ((*(v4i*)(&sA[buf][adst[U]]) = areg[set][U]), ...);
+      [&]<int... Q>(std::integer_sequence<int, Q...>) {
+        ((*(v4i*)(&sA[buf][adst[Q]]) = areg[set][Q]), ...);
       }(std::make_integer_sequence<int, UPT>{});
     }
   };
+  const int frag_off = (wm * FM * 16 + (lane % 16)) * ROWB + (lane / 16) * 16;
+  auto read_frag = [&](int buf, int i) -> v4i { return *(const v4i*)(&sA[buf][frag_off + i * 16 * ROWB]); };
 
   AccT acc[FM][FN];
 #pragma unroll
@@ -214,24 +227,14 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(GemmParams p, in
 #pragma unroll
     for (int j = 0; j < FN; ++j) acc[i][j] = AccT{0, 0, 0, 0};
 
-  auto compute = [&](int64_t c, auto slot_c) {
+  auto mfma_row = [&](v4i av, int i, auto slot_c) {
     constexpr int slot = decltype(slot_c)::value;
 #pragma unroll
-    for (int i = 0; i < FM; ++i) {
-      v4i av;
-      if constexpr (ADIRECT) {
-        av = aq[slot][i];
+    for (int j = 0; j < FN; ++j) {
+      if constexpr (I8) {
+        acc[i][j] = mfma(av, bq[slot][j], acc[i][j]);
       } else {
-        const int r = wm * FM * 16 + i * 16 + (lane % 16);
-        av = *(const v4i*)(&sA[c & 1][r * ROWB + (lane / 16) * 16]);
-      }
-#pragma unroll
-      for (int j = 0; j < FN; ++j) {
-        if constexpr (I8) {
-          acc[i][j] = mfma(av, bq[slot][j], acc[i][j]);
-        } else {
-          acc[i][j] = mfma(__builtin_bit_cast(v8bf, av), __builtin_bit_cast(v8bf, bq[slot][j]), acc[i][j]);
-        }
+        acc[i][j] = mfma(__builtin_bit_cast(v8bf, av), __builtin_bit_cast(v8bf, bq[slot][j]), acc[i][j]);
       }
     }
   };
@@ -244,33 +247,57 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(GemmParams p, in
     load_a_regs(0, std::integral_constant<int, 0>{});
     load_a_regs(1, std::integral_constant<int, 1>{});
     store_a_lds(0, std::integral_constant<int, 0>{});
+    store_a_lds(1, std::integral_constant<int, 1>{});
+    load_a_regs(2, std::integral_constant<int, 0>{});
     lds_barrier();
+    af[0] = read_frag(0, 0);
+    if constexpr (FM > 1) af[1] = read_frag(0, 1);
   }
 
+  int buf = 0;  // c % 3
   auto body = [&](int64_t c, auto b_c) {
     constexpr int b = decltype(b_c)::value;
-    load_a_regs(c + 2, std::integral_constant<int, b % 2>{});
-    issue(c + NB - 1, std::integral_constant<int, (b + NB - 1) % NB>{});
-    // keep the prefetch ahead of this chunk's MFMAs (the scheduler would
-    // otherwise sink the loads below them and drain the ring)
-    __builtin_amdgcn_sched_barrier(0);
-    compute(c, b_c);
-    __builtin_amdgcn_sched_barrier(0);
-    if constexpr (!ADIRECT) {
-      store_a_lds((int)((c + 1) & 1), std::integral_constant<int, (b + 1) % 2>{});
+    if constexpr (ADIRECT) {
+      issue(c + NB - 1, std::integral_constant<int, (b + NB - 1) % NB>{});
+      // keep the prefetch ahead of this chunk's MFMAs (the scheduler would
+      // otherwise sink the loads below them and drain the ring)
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < FM; ++i) mfma_row(aq[b % NB][i], i, std::integral_constant<int, b % NB>{});
+      __builtin_amdgcn_sched_barrier(0);
+    } else {
+      const int buf2 = buf == 0 ? 2 : buf - 1;  // (c + 2) % 3
+      const int buf1 = buf == 2 ? 0 : buf + 1;  // (c + 1) % 3
+      store_a_lds(buf2, std::integral_constant<int, b % 2>{});
+      load_a_regs(c + 3, std::integral_constant<int, (b + 1) % 2>{});
+      issue(c + NB - 1, std::integral_constant<int, (b + NB - 1) % NB>{});
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        // fragment i+2 of this chunk, or the first two of the next chunk
+        if (i + 2 < FM)
+          af[(i + 2) % FM] = read_frag(buf, i + 2);
+        else
+          af[(i + 2) % FM] = read_frag(buf1, i + 2 - FM);
+        mfma_row(af[i], i, std::integral_constant<int, b % NB>{});
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+        __builtin_amdgcn_sched_group_barrier(0x008, FN, 0); // then FN MFMAs
+      }
+      __builtin_amdgcn_sched_barrier(0);
       lds_barrier();
+      buf = buf1;
     }
   };
   int64_t c0 = 0;
-  for (; c0 + NB <= kc; c0 += NB) {
+  for (; c0 + U <= kc; c0 += U) {
     [&]<int... S>(std::integer_sequence<int, S...>) {
       (body(c0 + S, std::integral_constant<int, S>{}), ...);
-    }(std::make_integer_sequence<int, NB>{});
+    }(std::make_integer_sequence<int, U>{});
   }
-  // tail (< NB chunks): ring slots continue from 0
+  // tail (< U chunks): slots continue from 0
   [&]<int... S>(std::integer_sequence<int, S...>) {
     ((c0 + S < kc ? body(c0 + S, std::integral_constant<int, S>{}) : void()), ...);
-  }(std::make_integer_sequence<int, NB - 1>{});
+  }(std::make_integer_sequence<int, U - 1>{});
 
   // ---- epilogues
   const int col = lane % 16;
@@ -374,7 +401,7 @@ int launch_cfg(const GemmParams& p, int64_t max_tiles, hipStream_t stream) {
   const int64_t grid = max_tiles * n_blocks;
   if (grid <= 0) return FCMOE_OK;
   if (grid > INT32_MAX) return fail(FCMOE_EINVAL, "grouped gemm grid too large");
-  hipLaunchKernelGGL((grouped_gemm_kernel<I8, EPI, WM, WN, FM, FN, NB, ADIRECT>), dim3((unsigned)grid), dim3(kThreads), 0,
+  hipLaunchKernelGGL((grouped_gemm_kernel<I8, EPI, WM, WN, FM, FN, NB, ADIRECT>), dim3((unsigned)grid), dim3(WM * WN * kWave), 0,
                      stream, p, (int)n_blocks);
   return check_launch("grouped_gemm");
 }

@@ -86,6 +86,16 @@ int fcmoe_route_build(const void* topk_ids, int ids_is_i64, int64_t tokens, int6
 int fcmoe_quantize_rows(const void* x, int x_is_f32, int64_t rows, int64_t cols, int rounding, int8_t* q,
                         int64_t ldq, float* scales, hipStream_t stream);
 
+/* Top-k softmax router (the caller step before the MoE op; the reference
+ * receives ids/weights from vLLM: src/fused_cpp/moe/bf16_tiled.py:676-681,
+ * docs/vllm_bf16_tiled_moe_integration.md:75-87). logits [tokens, experts]
+ * fp32 -> topk_ids [tokens, top_k] (int64 if ids_is_i64 else int32, in
+ * descending logit order, lower id first on ties) and topk_weights
+ * [tokens, top_k] fp32 = softmax prob (/ sum of the selected probs if
+ * renormalize) * scale. experts <= 1024, top_k <= min(experts, 64). */
+int fcmoe_router_topk(const float* logits, int64_t tokens, int64_t experts, int64_t top_k, int renormalize,
+                      float scale, void* topk_ids, int ids_is_i64, float* topk_weights, hipStream_t stream);
+
 /* ---- fused MoE forward -------------------------------------------------- */
 
 typedef struct fcmoe_moe_args {

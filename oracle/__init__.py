@@ -10,6 +10,8 @@ Two parts:
   W8A8 pipeline, routing, activation/weight quantisation and i8gemm, restated
   from the reference one binary32 operation at a time (see the citations in the
   C file). Wrapped here with ctypes + numpy.
+* ``router_topk``: numpy restatement of the caller-side router (softmax ->
+  top-k -> renormalise -> scale) that produces the MoE op's ids and weights.
 * ``bf16_moe_reference``: an fp32 numpy restatement of the BF16 fused MoE
   semantics of ``src/fused_cpp/moe/naive.py:309-422`` (grouped per-expert
   linear, activation, weighted top-k sum) used as the tolerance reference.
@@ -134,6 +136,21 @@ def quant_weight_rows(w_bits: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
     s = np.empty(shape[:-1], np.float32)
     lib().orc_quant_weight_rows(_ptr(w_bits), rows, shape[-1], _ptr(q), _ptr(s))
     return q, s
+
+
+def router_topk(logits: np.ndarray, k: int, *, renormalize: bool = True, scale: float = 1.0):
+    """Caller-side router (docs/vllm_bf16_tiled_moe_integration.md:75-87; the reference
+    itself receives ids/weights, src/fused_cpp/moe/bf16_tiled.py:676-681), in fp32:
+    p = exp(x - max) / sum(exp(x - max)); ids = the k largest logits in descending order,
+    the lower expert id first on ties; w = p[ids] (/ sum p[ids]) * scale."""
+    x = np.asarray(logits, np.float32)
+    z = np.exp(x - x.max(axis=1, keepdims=True))
+    p = z / z.sum(axis=1, keepdims=True, dtype=np.float32)
+    ids = np.argsort(-x, axis=1, kind="stable")[:, :k]
+    w = np.take_along_axis(p, ids, axis=1)
+    if renormalize:
+        w = w / w.sum(axis=1, keepdims=True, dtype=np.float32)
+    return ids.astype(np.int64), (w * np.float32(scale)).astype(np.float32)
 
 
 def route_build(ids: np.ndarray, experts: int, shared_id: int = -1):

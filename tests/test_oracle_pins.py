@@ -116,6 +116,32 @@ def test_weight_quant_matches_reference_test(oracle_lib):
 
 # -------------------------------------------------------------- routing --
 
+@pytest.mark.parametrize("tokens,experts,k,renorm,scale", [(5, 8, 2, True, 1.0), (64, 256, 8, True, 2.5),
+                                                            (33, 384, 8, False, 1.0), (7, 1024, 64, True, 1.0)])
+def test_router_oracle_matches_torch_float64_and_brute_force(oracle_lib, tokens, experts, k, renorm, scale):
+    rng = np.random.default_rng(experts + k)
+    x = rng.standard_normal((tokens, experts)).astype(np.float32)
+    ids, w = oracle_lib.router_topk(x, k, renormalize=renorm, scale=scale)
+    # torch float64: softmax -> topk (sorted) -> renormalise -> scale
+    p = torch.softmax(torch.from_numpy(x).double(), dim=1)
+    tw, ti = torch.topk(p, k, dim=1, sorted=True)
+    if renorm:
+        tw = tw / tw.sum(dim=1, keepdim=True)
+    np.testing.assert_array_equal(ids, ti.numpy())
+    np.testing.assert_allclose(w, (tw * scale).numpy(), rtol=2e-6, atol=1e-9)
+    # brute force selection order on the first rows
+    for t in range(min(tokens, 3)):
+        expect = sorted(range(experts), key=lambda e: (-float(x[t, e]), e))[:k]
+        assert list(ids[t]) == expect
+
+
+def test_router_oracle_ties_take_lower_id(oracle_lib):
+    x = np.array([[1.0, 3.0, 3.0, 2.0], [0.0, 0.0, 0.0, 0.0]], np.float32)
+    ids, w = oracle_lib.router_topk(x, 2, scale=2.0)
+    assert ids.tolist() == [[1, 2], [0, 1]]
+    np.testing.assert_allclose(w, [[1.0, 1.0], [1.0, 1.0]], rtol=1e-7)
+
+
 @pytest.mark.parametrize("tokens,top_k,experts,shared", [(1, 1, 1, -1), (37, 2, 4, -1), (50, 8, 17, 16),
                                                           (300, 6, 9, 8)])
 def test_route_build_matches_stable_argsort_and_brute_force(oracle_lib, tokens, top_k, experts, shared):

@@ -22,56 +22,15 @@
 // since A and B use the same lane->K mapping, the products pair the same k
 // whatever the hardware's internal K order. D lane l, register i holds row
 // 4*(l/16)+i, column l%16.
+#include <cstdlib>
 #include <utility>
 
-#include "fcmoe_device.h"
-#include "fcmoe_internal.h"
+#include "fcmoe_gemm_common.h"
 
 namespace fcmoe {
 
 namespace {
 
-
-template <bool I8>
-struct Acc;
-template <>
-struct Acc<true> {
-  typedef v4i type;
-};
-template <>
-struct Acc<false> {
-  typedef v4f type;
-};
-
-__device__ __forceinline__ v4i mfma(v4i a, v4i b, v4i c) {
-  return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
-}
-__device__ __forceinline__ v4f mfma(v8bf a, v8bf b, v4f c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-}
-
-__device__ __forceinline__ float silu_f(float g) { return g / (1.0f + expf(-g)); }
-
-__device__ __forceinline__ float act_bf16_mode(float g, float u, int mode) {
-  if (mode == FCMOE_ACT_SILU_CLAMP10) {
-    g = fminf(g, 10.0f);
-    u = fmaxf(fminf(u, 10.0f), -10.0f);
-  }
-  if (mode == FCMOE_ACT_GELU) return 0.5f * g * (1.0f + erff(g * 0.70710678118654752440f)) * u;
-  return silu_f(g) * u;
-}
-
-// Barrier for the LDS A buffers: waits only for this wave's LDS traffic
-// (lgkmcnt), not for the weight loads still in flight (a __syncthreads fence
-// would also drain vmcnt and empty the prefetch ring).
-// The builtin (not inline asm) lets the compiler's wait-count pass see the
-// wait, so it does not wait again for LDS reads this one already covered.
-// gfx9 s_waitcnt immediate: vmcnt [3:0]+[15:14], expcnt [6:4], lgkmcnt
-// [11:8]; 0xC07F = lgkmcnt(0), the other counters unconstrained.
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_s_waitcnt(0xC07F);
-  __builtin_amdgcn_s_barrier();
-}
 
 template <bool I8, int EPI, int WM, int WN, int FM, int FN, int NB, bool ADIRECT>
 __global__ __launch_bounds__(WM * WN * kWave) void grouped_gemm_kernel(GemmParams p, int n_blocks) {
@@ -299,97 +258,7 @@ __global__ __launch_bounds__(WM * WN * kWave) void grouped_gemm_kernel(GemmParam
     ((c0 + S < kc ? body(c0 + S, std::integral_constant<int, S>{}) : void()), ...);
   }(std::make_integer_sequence<int, U - 1>{});
 
-  // ---- epilogues
-  const int col = lane % 16;
-  if constexpr (EPI == kEpiW13SwigluI8 || EPI == kEpiW13ActBf16) {
-    const int64_t n = p.n;  // 2F logical
-#pragma unroll
-    for (int i = 0; i < FM; ++i) {
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int r = wm * FM * 16 + i * 16 + (lane / 16) * 4 + q;
-        const bool rok = r < rows;
-        const int pos = pos0 + r;
-        float amax = 0.0f;
-#pragma unroll
-        for (int j = 0; j < FN / 2; ++j) {
-          const int64_t f = (gtile[j]) * 16 + col;  // gate channel (group 0)
-          if (!(rok && tvalid[j] && f < p.n_half)) continue;
-          float y;
-          if constexpr (EPI == kEpiW13SwigluI8) {
-            // w13_epilogue, csrc/moe/arm/i8mm_w8a8/kernels.cpp:230-246.
-            const float xs = p.scale_row[p.row_map ? p.row_map[pos] : pos];
-            const float* sc = p.scale_col + (int64_t)expert * n;
-            float gate = (float)acc[i][j][q] * (xs * sc[f]);
-            float up = (float)acc[i][j + FN / 2][q] * (xs * sc[p.n_half + f]);
-            gate = fminf(gate, 10.0f);
-            up = fmaxf(fminf(up, 10.0f), -10.0f);
-            const float ex = fexpa_exp_neg(gate);
-            y = (gate * up) / (ex + 1.0f);
-          } else {
-            float gate = acc[i][j][q];
-            float up = acc[i][j + FN / 2][q];
-            if (p.bias) {
-              gate = gate + p.bias[(int64_t)expert * n + f];
-              up = up + p.bias[(int64_t)expert * n + p.n_half + f];
-            }
-            y = act_bf16_mode(gate, up, p.activation);
-          }
-          const uint16_t yb = f32_to_bf16(y);
-          ((uint16_t*)p.out)[(int64_t)pos * p.ldo + f] = yb;
-          amax = fmaxf(amax, fabsf(bf16_to_f32(yb)));
-        }
-        if constexpr (EPI == kEpiW13SwigluI8) {
-          amax = max16(amax);
-          if (rok && col == 0) atomicMax(p.rowmax + pos, __float_as_uint(amax));
-        }
-      }
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < FM; ++i) {
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int r = wm * FM * 16 + i * 16 + (lane / 16) * 4 + q;
-        if (r >= rows) continue;
-        const int pos = pos0 + r;
-#pragma unroll
-        for (int j = 0; j < FN; ++j) {
-          if (!tvalid[j]) continue;
-          const int64_t g = gtile[j] / p.n_tiles;
-          const int64_t t = gtile[j] - g * p.n_tiles;
-          const int64_t cin = t * 16 + col;
-          if (cin >= p.n_half) continue;
-          const int64_t ch = g * p.n_half + cin;  // logical channel
-          if constexpr (EPI == kEpiRawI32) {
-            ((int32_t*)p.out)[(int64_t)pos * p.ldo + ch] = (int32_t)acc[i][j][q];
-          } else if constexpr (EPI == kEpiW2RouteI8) {
-            // store_w2, csrc/moe/arm/i8mm_w8a8/kernels.cpp:248-257.
-            const int64_t route = p.sorted_routes[pos];
-            const float v = (float)acc[i][j][q] * (p.scale_row[pos] * p.scale_col[(int64_t)expert * p.n + ch]);
-            ((float*)p.out)[route * p.ldo + ch] = v;
-          } else if constexpr (EPI == kEpiI8Gemm) {
-            // write_scaled_output, csrc/i8gemm.cpp:148-164 (left to right).
-            float v = (float)acc[i][j][q] * p.scale_row[pos] * p.scale_col[ch];
-            if (p.bias) v = v + p.bias[ch];
-            if (p.out_bf16)
-              ((uint16_t*)p.out)[(int64_t)pos * p.ldo + ch] = f32_to_bf16(v);
-            else
-              ((float*)p.out)[(int64_t)pos * p.ldo + ch] = v;
-          } else if constexpr (EPI == kEpiRawF32Bias) {
-            float v = acc[i][j][q];
-            if (p.bias) v = v + p.bias[(int64_t)expert * p.n + ch];
-            ((float*)p.out)[(int64_t)pos * p.ldo + gtile[j] * 16 + col] = v;  // packed channel order
-          } else if constexpr (EPI == kEpiW2RouteBf16) {
-            float v = acc[i][j][q];
-            if (p.bias) v = v + p.bias[(int64_t)expert * p.n + ch];
-            const int64_t route = p.sorted_routes[pos];
-            ((float*)p.out)[route * p.ldo + ch] = v;
-          }
-        }
-      }
-    }
-  }
+  gemm_epilogue<I8, EPI, FM, FN>(p, acc, gtile, tvalid, wm * FM * 16, rows, pos0, expert, lane);
 }
 
 template <bool I8, int EPI, int WM, int WN, int FM, int FN, int NB, bool ADIRECT>
@@ -434,6 +303,11 @@ int launch_bm(int bm, const GemmParams& p, int64_t max_tiles, hipStream_t stream
 }  // namespace
 
 int gemm_launch(int epi, int bm, const GemmParams& p, int64_t max_tiles, hipStream_t stream) {
+  static const bool use_lds = [] {
+    const char* v = getenv("FCMOE_GEMM_LDS");
+    return !(v && v[0] == '0');
+  }();
+  if (use_lds && bm >= 128) return gemm_lds_launch(epi, bm, p, max_tiles, stream);
   switch (epi) {
     case kEpiRawI32:
       return launch_bm<true, kEpiRawI32>(bm, p, max_tiles, stream);

@@ -1,0 +1,207 @@
+// fcmoe_gemm_common.h -- pieces shared by the grouped-GEMM kernels
+// (fcmoe_gemm.hip: register-ring kernels; fcmoe_gemm_lds.hip: LDS-staged
+// prefill kernel): MFMA wrappers, bf16-path activations, the LDS barrier and
+// the fused epilogues.
+//
+// Accumulator layout (both kernels): acc[i][j] is the 16x16 block of row
+// fragment i and channel tile j; lane l, register q holds row
+// row_base + 16 i + 4 (l / 16) + q and column l % 16 of tile gtile[j].
+#pragma once
+
+#include "fcmoe_device.h"
+#include "fcmoe_internal.h"
+
+namespace fcmoe {
+namespace {
+
+template <bool I8>
+struct Acc;
+template <>
+struct Acc<true> {
+  typedef v4i type;
+};
+template <>
+struct Acc<false> {
+  typedef v4f type;
+};
+
+__device__ __forceinline__ v4i mfma(v4i a, v4i b, v4i c) {
+  return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ v4f mfma(v8bf a, v8bf b, v4f c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float silu_f(float g) { return g / (1.0f + expf(-g)); }
+
+__device__ __forceinline__ float act_bf16_mode(float g, float u, int mode) {
+  if (mode == FCMOE_ACT_SILU_CLAMP10) {
+    g = fminf(g, 10.0f);
+    u = fmaxf(fminf(u, 10.0f), -10.0f);
+  }
+  if (mode == FCMOE_ACT_GELU) return 0.5f * g * (1.0f + erff(g * 0.70710678118654752440f)) * u;
+  return silu_f(g) * u;
+}
+
+// Barrier for the LDS A buffers: waits only for this wave's LDS traffic
+// (lgkmcnt), not for the weight loads still in flight (a __syncthreads fence
+// would also drain vmcnt and empty the prefetch ring).
+// The builtin (not inline asm) lets the compiler's wait-count pass see the
+// wait, so it does not wait again for LDS reads this one already covered.
+// gfx9 s_waitcnt immediate: vmcnt [3:0]+[15:14], expcnt [6:4], lgkmcnt
+// [11:8]; 0xC07F = lgkmcnt(0), the other counters unconstrained.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  __builtin_amdgcn_s_barrier();
+}
+
+// Fused epilogues. W13 pairs: tiles j < FN/2 are gate tiles and tile
+// j + FN/2 is the matching up tile (same channels of the other group).
+//
+// Per-column values (channels, scales, biases) are loaded once and per-row
+// values (positions, routes, row scales) once per 16-row fragment, ahead of
+// that fragment's stores: the output may alias those arrays as far as the
+// compiler knows, so a load left between stores would wait for each store.
+// Channels, positions and routes fit in 32 bits (checked by the launchers).
+template <bool I8, int EPI, int FM, int FN>
+__device__ __forceinline__ void gemm_epilogue(const GemmParams& p, const typename Acc<I8>::type (&acc)[FM][FN],
+                                              const int64_t (&gtile)[FN], const bool (&tvalid)[FN], int row_base,
+                                              int rows, int pos0, int expert, int lane) {
+  const int col = lane % 16;
+  auto row_of = [&](int i, int q, bool* ok) -> int {
+    const int r = row_base + i * 16 + (lane / 16) * 4 + q;
+    *ok = r < rows;
+    return pos0 + (r < rows ? r : rows - 1);  // clamped: loads stay in range
+  };
+  if constexpr (EPI == kEpiW13SwigluI8 || EPI == kEpiW13ActBf16) {
+    constexpr int HP = FN / 2;
+    const int64_t n = p.n;  // 2F logical
+    int f[HP];
+    bool fv[HP];
+    float cg[HP], cu[HP];  // W13 int8: gate / up channel scales; bf16: biases
+#pragma unroll
+    for (int j = 0; j < HP; ++j) {
+      f[j] = (int)(gtile[j] * 16 + col);  // gate channel (group 0)
+      fv[j] = tvalid[j] && f[j] < p.n_half;
+      const int64_t fc = fv[j] ? f[j] : 0;
+      if constexpr (EPI == kEpiW13SwigluI8) {
+        cg[j] = p.scale_col[(int64_t)expert * n + fc];
+        cu[j] = p.scale_col[(int64_t)expert * n + p.n_half + fc];
+      } else {
+        cg[j] = p.bias ? p.bias[(int64_t)expert * n + fc] : 0.0f;
+        cu[j] = p.bias ? p.bias[(int64_t)expert * n + p.n_half + fc] : 0.0f;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      int pos[4];
+      bool rok[4];
+      float xs[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        pos[q] = row_of(i, q, &rok[q]);
+        if constexpr (EPI == kEpiW13SwigluI8) xs[q] = p.scale_row[p.row_map ? p.row_map[pos[q]] : pos[q]];
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        float amax = 0.0f;
+#pragma unroll
+        for (int j = 0; j < HP; ++j) {
+          if (!(rok[q] && fv[j])) continue;
+          float y;
+          if constexpr (EPI == kEpiW13SwigluI8) {
+            // w13_epilogue, csrc/moe/arm/i8mm_w8a8/kernels.cpp:230-246.
+            float gate = (float)acc[i][j][q] * (xs[q] * cg[j]);
+            float up = (float)acc[i][j + HP][q] * (xs[q] * cu[j]);
+            gate = fminf(gate, 10.0f);
+            up = fmaxf(fminf(up, 10.0f), -10.0f);
+            const float ex = fexpa_exp_neg(gate);
+            y = (gate * up) / (ex + 1.0f);
+          } else {
+            float gate = acc[i][j][q];
+            float up = acc[i][j + HP][q];
+            if (p.bias) {
+              gate = gate + cg[j];
+              up = up + cu[j];
+            }
+            y = act_bf16_mode(gate, up, p.activation);
+          }
+          const uint16_t yb = f32_to_bf16(y);
+          ((uint16_t*)p.out)[(int64_t)pos[q] * p.ldo + f[j]] = yb;
+          amax = fmaxf(amax, fabsf(bf16_to_f32(yb)));
+        }
+        if constexpr (EPI == kEpiW13SwigluI8) {
+          amax = max16(amax);
+          if (rok[q] && col == 0) atomicMax(p.rowmax + pos[q], __float_as_uint(amax));
+        }
+      }
+    }
+  } else {
+    constexpr bool ROUTE = EPI == kEpiW2RouteI8 || EPI == kEpiW2RouteBf16;
+    constexpr bool ROWSCALE = EPI == kEpiW2RouteI8 || EPI == kEpiI8Gemm;
+    int ch[FN], dch[FN];
+    bool cv[FN];
+    float cs[FN], cb[FN];  // column scale, column bias
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const int64_t g = gtile[j] / p.n_tiles;
+      const int64_t t = gtile[j] - g * p.n_tiles;
+      const int64_t cin = t * 16 + col;
+      cv[j] = tvalid[j] && cin < p.n_half;
+      ch[j] = cv[j] ? (int)(g * p.n_half + cin) : 0;          // logical channel
+      dch[j] = EPI == kEpiRawF32Bias ? (int)(gtile[j] * 16 + col) : ch[j];  // RawF32Bias: packed order
+      cs[j] = 0.0f;
+      cb[j] = 0.0f;
+      if constexpr (EPI == kEpiW2RouteI8) cs[j] = p.scale_col[(int64_t)expert * p.n + ch[j]];
+      if constexpr (EPI == kEpiI8Gemm) {
+        cs[j] = p.scale_col[ch[j]];
+        if (p.bias) cb[j] = p.bias[ch[j]];
+      }
+      if constexpr (EPI == kEpiRawF32Bias || EPI == kEpiW2RouteBf16) {
+        if (p.bias) cb[j] = p.bias[(int64_t)expert * p.n + ch[j]];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      int orow[4];  // output row: sorted position or flat route
+      bool rok[4];
+      float rs[4];  // row scale
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int pos = row_of(i, q, &rok[q]);
+        orow[q] = ROUTE ? p.sorted_routes[pos] : pos;
+        rs[q] = ROWSCALE ? p.scale_row[pos] : 0.0f;
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        if (!rok[q]) continue;
+        const int64_t obase = (int64_t)orow[q] * p.ldo;
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+          if (!cv[j]) continue;
+          if constexpr (EPI == kEpiRawI32) {
+            ((int32_t*)p.out)[obase + ch[j]] = (int32_t)acc[i][j][q];
+          } else if constexpr (EPI == kEpiW2RouteI8) {
+            // store_w2, csrc/moe/arm/i8mm_w8a8/kernels.cpp:248-257.
+            ((float*)p.out)[obase + ch[j]] = (float)acc[i][j][q] * (rs[q] * cs[j]);
+          } else if constexpr (EPI == kEpiI8Gemm) {
+            // write_scaled_output, csrc/i8gemm.cpp:148-164 (left to right).
+            float v = (float)acc[i][j][q] * rs[q] * cs[j];
+            if (p.bias) v = v + cb[j];
+            if (p.out_bf16)
+              ((uint16_t*)p.out)[obase + ch[j]] = f32_to_bf16(v);
+            else
+              ((float*)p.out)[obase + ch[j]] = v;
+          } else {  // kEpiRawF32Bias, kEpiW2RouteBf16
+            float v = acc[i][j][q];
+            if (p.bias) v = v + cb[j];
+            ((float*)p.out)[obase + dch[j]] = v;
+          }
+        }
+      }
+    }
+  }
+}
+
+}  // namespace
+}  // namespace fcmoe

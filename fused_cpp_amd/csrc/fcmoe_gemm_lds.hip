@@ -1,0 +1,250 @@
+// fcmoe_gemm_lds.hip -- LDS-staged grouped GEMM for large row tiles
+// (prefill: BM = 128 / 192 / 256 rows of one expert).
+//
+// Why a second kernel: at large M the MFMA pipe, not HBM, is the limit, and
+// on CDNA4 every instruction that moves a 1 KB operand block through VGPRs
+// (global load, LDS write, LDS read) costs MFMA issue time. This kernel
+//   * stages both operands with buffer_load ... lds (global -> LDS without
+//     VGPRs, issued at almost no MFMA cost),
+//   * gives each wave a large 16 FM x 16 FN tile (96x128 / 128x96 / 64x128)
+//     so each LDS fragment read feeds FN or FM MFMAs,
+//   * keeps the accumulators in VGPRs at 2 waves per SIMD (8 waves per
+//     workgroup, one workgroup per CU).
+//
+// Work decomposition: grid.x = tiles * n_blocks; a workgroup computes rows
+// [m0, m0 + BM) of one expert against 4 * FN consecutive 16-channel tiles
+// (W13: 4 * FN/2 gate tiles and the matching up tiles). Waves are 2 (rows) x
+// 4 (channel tiles); the epilogues are the shared gemm_epilogue.
+//
+// Pipeline: a ring of three LDS stages, each one 64-byte K chunk of the
+// A tile (BM rows) and of the workgroup's B tiles. Iteration c waits for its
+// own stage-c loads (vmcnt), meets the other waves at one barrier (their
+// stage-c loads have landed; everyone is done reading stage c-1), issues
+// chunk c+2 into stage (c+2) % 3 and computes chunk c.
+//
+// LDS layouts (per stage): A rows packed 64 bytes apart, the four 16-byte
+// units of row r stored at slot (unit ^ ((r >> 2) & 3)) so the 16 rows of a
+// fragment read fall on distinct banks; B tiles in their packed MFMA operand
+// order (1 KB per tile chunk, lane l's 16 bytes at 16 l).
+#include <utility>
+
+#include "fcmoe_gemm_common.h"
+
+namespace fcmoe {
+
+namespace {
+
+constexpr int kWM = 2;
+constexpr int kWN = 4;
+constexpr int kWaves = kWM * kWN;
+constexpr int kThreadsLds = kWaves * kWave;
+constexpr int kStages = 3;
+// Raw buffer resource word 3 for gfx9: 32-bit data format, no swizzle.
+constexpr int kBufWord3 = 0x00020000;
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// s_waitcnt vmcnt(N) with the other counters unconstrained (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+template <bool I8, int EPI, int FM, int FN>
+__global__ __launch_bounds__(kThreadsLds) void grouped_gemm_lds_kernel(GemmParams p, int n_blocks) {
+  // The body is device-only: the buffer-resource type does not exist for the
+  // host target, and the host pass needs only the kernel's signature.
+#if __HIP_DEVICE_COMPILE__
+  constexpr int BM = kWM * FM * 16;
+  constexpr int NT = kWN * FN;            // channel tiles per workgroup
+  constexpr int A_BYTES = BM * 64;
+  constexpr int STAGE = A_BYTES + NT * 1024;
+  constexpr int LA = BM / 16;             // A loads (16 rows x 64 bytes) per stage
+  constexpr int L = LA + NT;              // loads per stage
+  constexpr int LPW = (L + kWaves - 1) / kWaves;  // loads per wave per stage
+  constexpr bool PAIR = (EPI == kEpiW13SwigluI8 || EPI == kEpiW13ActBf16);
+  constexpr int HP = FN / 2;
+  static_assert(L >= kWaves, "every wave issues at least one load per stage");
+  static_assert(FM >= 3, "the fragment ring runs two fragments ahead");
+  typedef typename Acc<I8>::type AccT;
+
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[kStages * STAGE];
+
+  const int count = *p.tile_count;
+  const int tile = count - 1 - (int)(blockIdx.x / n_blocks);  // last-first, as the register kernel
+  if (tile < 0) return;
+  const int nb = blockIdx.x % n_blocks;
+  const int expert = p.tiles[2 * tile];
+  const int m0 = p.tiles[2 * tile + 1];
+  const int rows_left = p.counts[expert] - m0;
+  const int rows = rows_left < BM ? rows_left : BM;
+  const int pos0 = p.offsets[expert] + m0;
+
+  const int lane = threadIdx.x % kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int wm = wave / kWN;
+  const int wn = wave % kWN;
+  const int64_t kc = p.k_chunks;
+  const int64_t total_tiles = (int64_t)p.n_groups * p.n_tiles;
+
+  // channel tile (index within the expert) of wave column wn_, slot j
+  auto tile_of = [&](int wn_, int j, bool* valid) -> int64_t {
+    if constexpr (PAIR) {
+      const int64_t pr = ((int64_t)nb * kWN + wn_) * HP + (j % HP);
+      *valid = pr < p.n_tiles;
+      return (j < HP ? 0 : p.n_tiles) + pr;
+    } else {
+      const int64_t t = ((int64_t)nb * kWN + wn_) * FN + j;
+      *valid = t < total_tiles;
+      return t;
+    }
+  };
+
+  // ---- buffer resources and this wave's LPW loads per stage. Load index g:
+  // g < LA -> A rows [16 g, 16 g + 16); else B tile g - LA. Waves take
+  // g = wave, wave + 8, ...; indices past L repeat load g - L (same bytes to
+  // the same place) so every wave issues exactly LPW loads.
+  const int64_t lda_bytes = p.lda * (I8 ? 1 : 2);
+  const __amdgpu_buffer_rsrc_t rsrc_a =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p.a), (short)0, 0x7ffffff0, kBufWord3);
+  const __amdgpu_buffer_rsrc_t rsrc_b = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)((const uint8_t*)p.w + (int64_t)expert * p.w_expert_bytes), (short)0,
+      (int)(p.w_expert_bytes < 0x7ffffff0 ? p.w_expert_bytes : 0x7ffffff0), kBufWord3);
+  uint32_t voff[LPW];
+  bool is_a[LPW];
+  int lds_off[LPW];
+#pragma unroll
+  for (int u = 0; u < LPW; ++u) {
+    int g = wave + kWaves * u;
+    if (g >= L) g -= L;
+    is_a[u] = g < LA;
+    if (g < LA) {
+      const int r = g * 16 + lane / 4;
+      const int unit = (lane % 4) ^ ((lane >> 4) & 3);
+      const int pos = pos0 + (r < rows ? r : rows - 1);  // rows past the tile re-read the last row
+      const int64_t arow = p.row_map ? (int64_t)p.row_map[pos] : (int64_t)pos;
+      voff[u] = (uint32_t)(arow * lda_bytes + unit * 16);
+      lds_off[u] = g * 1024;
+    } else {
+      const int t = g - LA;
+      bool valid;
+      const int64_t gt = tile_of(t / FN, t % FN, &valid);
+      voff[u] = (uint32_t)((valid ? gt : 0) * kc * 1024 + lane * 16);
+      lds_off[u] = A_BYTES + t * 1024;
+    }
+  }
+  auto issue = [&](int64_t c, int stage) {
+    const int64_t cc = c < kc ? c : kc - 1;  // past the end: re-load the last chunk (never read)
+    const int soff_a = (int)(cc * 64);
+    const int soff_b = (int)(cc * 1024);
+#pragma unroll
+    for (int u = 0; u < LPW; ++u) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(is_a[u] ? rsrc_a : rsrc_b,
+                                               (lds_ptr_t)(smem + stage * STAGE + lds_off[u]), 16, voff[u],
+                                               is_a[u] ? soff_a : soff_b, 0, 0);
+    }
+  };
+
+  // ---- fragment addresses (bytes within a stage)
+  const int a_frag = (wm * FM * 16 + lane % 16) * 64 + (((lane / 16) ^ ((lane % 16) >> 2)) * 16);
+  const int b_frag = A_BYTES + wn * FN * 1024 + lane * 16;
+
+  AccT acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = AccT{0, 0, 0, 0};
+
+  issue(0, 0);
+  issue(1, 1);
+  int stage = 0;
+  for (int64_t c = 0; c < kc; ++c) {
+    wait_vmcnt<LPW>();  // this wave's chunk-c loads have landed (chunk c+1's may still fly)
+    __builtin_amdgcn_s_barrier();
+    issue(c + 2, stage == 0 ? 2 : stage - 1);
+    const uint8_t* st = smem + stage * STAGE;
+    v4i bf[FN];
+    v4i af[FM];
+#pragma unroll
+    for (int j = 0; j < FN; ++j) bf[j] = *(const v4i*)(st + b_frag + j * 1024);
+    af[0] = *(const v4i*)(st + a_frag);
+    af[1] = *(const v4i*)(st + a_frag + 1024);
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      if (i + 2 < FM) af[i + 2] = *(const v4i*)(st + a_frag + (i + 2) * 1024);
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        if constexpr (I8) {
+          acc[i][j] = mfma(af[i], bf[j], acc[i][j]);
+        } else {
+          acc[i][j] = mfma(__builtin_bit_cast(v8bf, af[i]), __builtin_bit_cast(v8bf, bf[j]), acc[i][j]);
+        }
+      }
+    }
+    stage = stage == 2 ? 0 : stage + 1;
+  }
+  wait_vmcnt<0>();  // the two trailing (unused) stage loads
+
+  int64_t gtile[FN];
+  bool tvalid[FN];
+#pragma unroll
+  for (int j = 0; j < FN; ++j) gtile[j] = tile_of(wn, j, &tvalid[j]);
+  gemm_epilogue<I8, EPI, FM, FN>(p, acc, gtile, tvalid, wm * FM * 16, rows, pos0, expert, lane);
+#endif
+}
+
+template <bool I8, int EPI, int FM, int FN>
+int launch_lds_cfg(const GemmParams& p, int64_t max_tiles, hipStream_t stream) {
+  constexpr bool PAIR = (EPI == kEpiW13SwigluI8 || EPI == kEpiW13ActBf16);
+  const int64_t per_block = PAIR ? (int64_t)kWN * (FN / 2) : (int64_t)kWN * FN;
+  const int64_t units = PAIR ? p.n_tiles : (int64_t)p.n_groups * p.n_tiles;
+  const int64_t n_blocks = ceil_div(units, per_block);
+  const int64_t grid = max_tiles * n_blocks;
+  if (grid <= 0) return FCMOE_OK;
+  if (grid > INT32_MAX) return fail(FCMOE_EINVAL, "grouped gemm grid too large");
+  // 32-bit buffer offsets: A rows and one expert's packed weights
+  if (p.w_expert_bytes >= 0x7ffffff0) return fail(FCMOE_EINVAL, "expert weights exceed 2 GiB");
+  hipLaunchKernelGGL((grouped_gemm_lds_kernel<I8, EPI, FM, FN>), dim3((unsigned)grid), dim3(kThreadsLds), 0, stream,
+                     p, (int)n_blocks);
+  return check_launch("grouped_gemm_lds");
+}
+
+template <bool I8, int EPI>
+int launch_lds_bm(int bm, const GemmParams& p, int64_t max_tiles, hipStream_t stream) {
+  switch (bm) {
+    case 128:
+      return launch_lds_cfg<I8, EPI, 4, 8>(p, max_tiles, stream);
+    case 192:
+      return launch_lds_cfg<I8, EPI, 6, 8>(p, max_tiles, stream);
+    case 256:
+      return launch_lds_cfg<I8, EPI, 8, 6>(p, max_tiles, stream);
+    default:
+      return fail(FCMOE_EINVAL, "unsupported LDS tile rows");
+  }
+}
+
+}  // namespace
+
+int gemm_lds_launch(int epi, int bm, const GemmParams& p, int64_t max_tiles, hipStream_t stream) {
+  switch (epi) {
+    case kEpiRawI32:
+      return launch_lds_bm<true, kEpiRawI32>(bm, p, max_tiles, stream);
+    case kEpiW13SwigluI8:
+      return launch_lds_bm<true, kEpiW13SwigluI8>(bm, p, max_tiles, stream);
+    case kEpiW2RouteI8:
+      return launch_lds_bm<true, kEpiW2RouteI8>(bm, p, max_tiles, stream);
+    case kEpiI8Gemm:
+      return launch_lds_bm<true, kEpiI8Gemm>(bm, p, max_tiles, stream);
+    case kEpiW13ActBf16:
+      return launch_lds_bm<false, kEpiW13ActBf16>(bm, p, max_tiles, stream);
+    case kEpiRawF32Bias:
+      return launch_lds_bm<false, kEpiRawF32Bias>(bm, p, max_tiles, stream);
+    case kEpiW2RouteBf16:
+      return launch_lds_bm<false, kEpiW2RouteBf16>(bm, p, max_tiles, stream);
+    default:
+      return fail(FCMOE_EINVAL, "unknown epilogue");
+  }
+}
+
+}  // namespace fcmoe

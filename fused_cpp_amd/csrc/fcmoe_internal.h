@@ -111,6 +111,9 @@ struct GemmParams {
 };
 
 int gemm_launch(int epi, int bm, const GemmParams& p, int64_t max_tiles, hipStream_t stream);
+// LDS-staged kernel for bm in {128, 192, 256} (fcmoe_gemm_lds.hip); gemm_launch
+// dispatches to it unless FCMOE_GEMM_LDS=0.
+int gemm_lds_launch(int epi, int bm, const GemmParams& p, int64_t max_tiles, hipStream_t stream);
 
 // ---- combine (fcmoe_combine.hip) ----
 int combine_launch(const float* route_out, const float* route_weight, const int32_t* route_pos, int64_t tokens,

@@ -47,6 +47,9 @@ CONFIGS = {
                desc="C3 W8A8 DSv3 prefill: T=4096 Zipf(1.2) routing, +1 shared"),
     "c4": dict(kind="w8a8", T=8192, H=7168, I=2048, E=384, k=8, shared=True, scale=2.5, skew=None,
                desc="C4 W8A8 prefill: T=8192 H=7168 I=2048 E=384 top-8 +1 shared"),
+    # not a BASELINE config: the C1 decode shape on the W8A16 path (int8 weights, bf16 activations)
+    "c1w8": dict(kind="w8a16", T=32, H=7168, I=2048, E=256, k=8, shared=True, scale=2.5, skew=None,
+                 desc="C1 shape on W8A16: T=32 H=7168 I=2048 E=256 top-8 +1 shared, int8 weights"),
 }
 
 
@@ -168,8 +171,8 @@ def algorithmic(cfg, counts):
     Layer bytes = active experts' weights + scales, x in, out, ids + weights;
     ops = 2 * MACs = routed rows * 6 * H * I (int8 or bf16)."""
     H, I = cfg["H"], cfg["I"]
-    eb = 1 if cfg["kind"] == "w8a8" else 2
-    sb = 4 if cfg["kind"] == "w8a8" else 0
+    eb = 1 if cfg["kind"] in ("w8a8", "w8a16") else 2
+    sb = 4 if cfg["kind"] in ("w8a8", "w8a16") else 0
     active = counts > 0
     rows = int(counts.sum())
     T = cfg["T"]
@@ -194,6 +197,7 @@ def run_gpu(cfg, steps: int, warmup: int, device, keep_host: bool):
     import torch
 
     from fused_cpp_amd import cabi
+    from fused_cpp_amd import moe
     from fused_cpp_amd.moe import fused_moe_bf16_tiled_with_shared, fused_moe_tiled, fused_moe_w8a8_tiled_with_shared
 
     ids, w, tau = make_routing(cfg)
@@ -212,6 +216,16 @@ def run_gpu(cfg, steps: int, warmup: int, device, keep_host: bool):
         else:
             def step(out):
                 return fused_moe_tiled(x, weights, w_d, ids_d, swiglu_limit=10.0, out=out)
+    elif cfg["kind"] == "w8a16":
+        w8, _ = build_layer(cfg, device, False)
+        p = w8.packed
+        weights = moe.PreparedW8A16TiledRoutedSharedMoEWeights(
+            packed=moe.PreparedW8A16TiledFusedMoEWeights(w13=p.w13, w2=p.w2), routed_experts=w8.routed_experts,
+            shared_expert_id=w8.shared_expert_id)
+
+        def step(out):
+            return moe.fused_moe_w8a16_tiled_with_shared(x, weights, w_d, ids_d, routed_scaling_factor=cfg["scale"],
+                                                         out=out)
     else:
         weights = build_bf16_layer(cfg, device)
         if cfg["shared"]:
@@ -392,7 +406,7 @@ def main() -> int:
     cfg = CONFIGS[args.config]
     res = measure(cfg, args, device, want_cpu=not args.no_cpu_baseline)
     line = {
-        "metric": "W8A8 MoE-layer tokens/s" if cfg["kind"] == "w8a8" else "BF16 MoE-layer tokens/s",
+        "metric": {"w8a8": "W8A8", "w8a16": "W8A16", "bf16": "BF16"}[cfg["kind"]] + " MoE-layer tokens/s",
         "value": round(res["tokens_per_s"], 1),
         "unit": "tokens/s",
         "n_gpus": 1,

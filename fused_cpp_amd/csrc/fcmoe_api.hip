@@ -96,16 +96,23 @@ W8A8Layout w8a8_layout(const fcmoe_moe_args* a, Arena& ar) {
   return L;
 }
 
-Bf16Layout bf16_layout(const fcmoe_moe_args* a, Arena& ar) {
+// BF16 and W8A16 share this layout. K is padded to the GEMM's K chunk: 32
+// bf16 elements (64 bytes) for bf16 weights, 64 elements for int8 weights.
+// W8A16 streams weights on the direct-A kernel only: tile classes 16 / 32.
+Bf16Layout bf16_layout(const fcmoe_moe_args* a, Arena& ar, bool w8 = false) {
   Bf16Layout L;
+  const int64_t kmul = w8 ? 64 : 32;
   L.kt = a->top_k + (a->shared_expert_id >= 0 ? 1 : 0);
   L.routes = a->tokens * L.kt;
-  L.hp = round_up(a->hidden, 32);
-  L.ip = round_up(a->inter, 32);
+  L.hp = round_up(a->hidden, kmul);
+  L.ip = round_up(a->inter, kmul);
   L.gu_ld = 2 * round_up(a->inter, 16);
-  L.tc = select_classes(L.routes, a->experts);
+  if (w8)
+    L.tc = make_tile_classes(kClassBM, L.routes <= kDecodeRowsPerExpert * a->experts ? 1 : 2, L.routes, a->experts);
+  else
+    L.tc = select_classes(L.routes, a->experts);
   route_take(ar, L.rb, L.routes, a->experts, L.tc);
-  L.xpad = (a->hidden % 32) ? ar.take<uint16_t>(a->tokens * L.hp) : nullptr;
+  L.xpad = (a->hidden % kmul) ? ar.take<uint16_t>(a->tokens * L.hp) : nullptr;
   L.y = ar.take<uint16_t>(L.routes * L.ip);
   L.gate_up = a->activation == FCMOE_ACT_SWIGLUOAI ? ar.take<float>(L.routes * L.gu_ld) : nullptr;
   L.route_out = ar.take<float>(L.routes * a->hidden);
@@ -438,18 +445,21 @@ extern "C" int fcmoe_w8a8_stage_views(const fcmoe_moe_args* a, const int32_t** s
 
 // ------------------------------------------------------------------ BF16 --
 
-extern "C" size_t fcmoe_bf16_workspace_bytes(const fcmoe_moe_args* a) {
-  if (check_shapes(a)) return 0;
-  Arena ar;
-  bf16_layout(a, ar);
-  return ar.used + 256;
-}
+namespace {
 
-extern "C" int fcmoe_bf16_forward(const fcmoe_moe_args* a, hipStream_t stream) {
+// BF16 weights (w8 = false) or W8A16: int8 per-channel weights with fp32
+// scales against bf16 activations (w8 = true). Same routing, activation and
+// combine; the GEMMs differ in operand type and epilogue.
+int bf16_family_forward(const fcmoe_moe_args* a, hipStream_t stream, bool w8) {
   int rc = check_shapes(a);
   if (rc) return rc;
   if (a->activation < FCMOE_ACT_SILU || a->activation > FCMOE_ACT_SILU_CLAMP10)
     return fail(FCMOE_EINVAL, "unsupported activation");
+  if (w8) {
+    if (a->activation == FCMOE_ACT_SWIGLUOAI) return fail(FCMOE_EINVAL, "W8A16 supports silu, gelu and silu_clamp10");
+    if (a->w13_bias || a->w2_bias) return fail(FCMOE_EINVAL, "W8A16 fused MoE does not support biases");
+    if (!a->w13_scale || !a->w2_scale) return fail(FCMOE_EINVAL, "W8A16 needs w13_scale and w2_scale");
+  }
   const int64_t kt = a->top_k + (a->shared_expert_id >= 0 ? 1 : 0);
   if (a->skip_weighted && kt != 1) return fail(FCMOE_EINVAL, "skip_weighted is only valid when top_k == 1");
   if ((rc = check_common(a))) return rc;
@@ -458,8 +468,9 @@ extern "C" int fcmoe_bf16_forward(const fcmoe_moe_args* a, hipStream_t stream) {
   ar.base = (char*)a->workspace;
   ar.cap = a->workspace_bytes;
   if (!ar.base) return fail(FCMOE_ESPACE, "workspace is NULL");
-  Bf16Layout L = bf16_layout(a, ar);
+  Bf16Layout L = bf16_layout(a, ar, w8);
   if (!ar.ok()) return fail(FCMOE_ESPACE, "BF16 workspace too small");
+  const int64_t kmul = w8 ? 64 : 32;
   const int64_t H = a->hidden, I = a->inter;
 
   {
@@ -477,7 +488,7 @@ extern "C" int fcmoe_bf16_forward(const fcmoe_moe_args* a, hipStream_t stream) {
     xa = L.xpad;
   }
   // y columns [F, ip) feed W2's zero-padded K and must be finite zeros.
-  if (I % 32) {
+  if (I % kmul) {
     rc = fill_u32_launch((uint32_t*)L.y, L.routes * L.ip / 2, 0u, stream);
     if (rc) return rc;
   }
@@ -489,22 +500,24 @@ extern "C" int fcmoe_bf16_forward(const fcmoe_moe_args* a, hipStream_t stream) {
   g13.offsets = L.rb.offsets;
   g13.counts = L.rb.counts;
   g13.w = a->w13;
-  g13.w_expert_bytes = fcmoe_packed_expert_bytes(2, 2 * I, H, 2);
+  g13.w_expert_bytes = fcmoe_packed_expert_bytes(w8 ? 1 : 2, 2 * I, H, 2);
   g13.n = 2 * I;
   g13.n_half = I;
   g13.n_tiles = ceil_div(I, 16);
-  g13.k_chunks = ceil_div(H * 2, 64);
+  g13.k_chunks = w8 ? ceil_div(H, 64) : ceil_div(H * 2, 64);
   g13.n_groups = 2;
   g13.out = fused ? (void*)L.y : (void*)L.gate_up;
   g13.ldo = fused ? L.ip : L.gu_ld;
   g13.bias = a->w13_bias;
+  g13.scale_col = w8 ? a->w13_scale : nullptr;
   g13.activation = a->activation;
+  const int epi13 = w8 ? kEpiW13ActW8 : (fused ? kEpiW13ActBf16 : kEpiRawF32Bias);
   rc = run_classes(L.tc, stream, [&](int c, hipStream_t s) {
     GemmParams p = g13;
     p.tiles = L.rb.tiles + 2 * tile_offset(L.tc, c);
     p.tile_count = L.rb.tile_count + c;
     Stage st(FCMOE_STAGE_W13_CLASS0 + c, s);
-    return gemm_launch(fused ? kEpiW13ActBf16 : kEpiRawF32Bias, L.tc.bm[c], p, L.tc.bound[c], s);
+    return gemm_launch(epi13, L.tc.bm[c], p, L.tc.bound[c], s);
   });
   if (rc) return rc;
   if (!fused) {
@@ -518,28 +531,53 @@ extern "C" int fcmoe_bf16_forward(const fcmoe_moe_args* a, hipStream_t stream) {
   g2.offsets = L.rb.offsets;
   g2.counts = L.rb.counts;
   g2.w = a->w2;
-  g2.w_expert_bytes = fcmoe_packed_expert_bytes(2, H, I, 1);
+  g2.w_expert_bytes = fcmoe_packed_expert_bytes(w8 ? 1 : 2, H, I, 1);
   g2.n = H;
   g2.n_half = H;
   g2.n_tiles = ceil_div(H, 16);
-  g2.k_chunks = ceil_div(I * 2, 64);
+  g2.k_chunks = w8 ? ceil_div(I, 64) : ceil_div(I * 2, 64);
   g2.n_groups = 1;
   g2.out = L.route_out;
   g2.ldo = H;
   g2.bias = a->w2_bias;
+  g2.scale_col = w8 ? a->w2_scale : nullptr;
   g2.sorted_routes = L.rb.sorted_routes;
   rc = run_classes(L.tc, stream, [&](int c, hipStream_t s) {
     GemmParams p = g2;
     p.tiles = L.rb.tiles + 2 * tile_offset(L.tc, c);
     p.tile_count = L.rb.tile_count + c;
     Stage st(FCMOE_STAGE_W2_CLASS0 + c, s);
-    return gemm_launch(kEpiW2RouteBf16, L.tc.bm[c], p, L.tc.bound[c], s);
+    return gemm_launch(w8 ? kEpiW2RouteW8 : kEpiW2RouteBf16, L.tc.bm[c], p, L.tc.bound[c], s);
   });
   if (rc) return rc;
   const int tree = (kt == 2 || kt == 4 || kt == 6 || kt == 8) ? 1 : 0;
   Stage st(FCMOE_STAGE_COMBINE, stream);
   return combine_launch(L.route_out, L.rb.route_weight, L.rb.route_pos, a->tokens, kt, H, tree, a->skip_weighted,
                         a->out, stream);
+}
+
+}  // namespace
+
+extern "C" size_t fcmoe_bf16_workspace_bytes(const fcmoe_moe_args* a) {
+  if (check_shapes(a)) return 0;
+  Arena ar;
+  bf16_layout(a, ar);
+  return ar.used + 256;
+}
+
+extern "C" int fcmoe_bf16_forward(const fcmoe_moe_args* a, hipStream_t stream) {
+  return bf16_family_forward(a, stream, false);
+}
+
+extern "C" size_t fcmoe_w8a16_workspace_bytes(const fcmoe_moe_args* a) {
+  if (check_shapes(a)) return 0;
+  Arena ar;
+  bf16_layout(a, ar, true);
+  return ar.used + 256;
+}
+
+extern "C" int fcmoe_w8a16_forward(const fcmoe_moe_args* a, hipStream_t stream) {
+  return bf16_family_forward(a, stream, true);
 }
 
 // ---------------------------------------------------------------- i8gemm --

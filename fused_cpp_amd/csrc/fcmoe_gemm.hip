@@ -39,8 +39,13 @@ __global__ __launch_bounds__(WM * WN * kWave) void grouped_gemm_kernel(GemmParam
   constexpr int ROWB = 64 + 16;                    // LDS row stride (bytes): 16 rows hit distinct banks
   constexpr int UNITS = BM * 4;                    // 16-byte A units per 64-byte K chunk
   constexpr int UPT = (UNITS + kThreads - 1) / kThreads;
-  constexpr bool PAIR = (EPI == kEpiW13SwigluI8 || EPI == kEpiW13ActBf16);
+  constexpr bool PAIR = epi_pair(EPI);
+  // W8A16: bf16 A, int8 B. A K chunk is 64 elements = 128 bytes (two 16-byte
+  // fragments per lane); each chunk runs two bf16 MFMAs per tile pair.
+  constexpr bool W8 = epi_w8(EPI);
+  constexpr int AW = W8 ? 2 : 1;
   static_assert(!ADIRECT || WM == 1, "direct A fragments assume one wave row");
+  static_assert(!W8 || (ADIRECT && !I8), "W8A16 runs on the direct-A path with fp32 accumulators");
   typedef typename Acc<I8>::type AccT;
 
   __shared__ __attribute__((aligned(16))) uint8_t sA[ADIRECT ? 1 : 3][ADIRECT ? 16 : BM * ROWB];
@@ -91,7 +96,7 @@ __global__ __launch_bounds__(WM * WN * kWave) void grouped_gemm_kernel(GemmParam
   for (int j = 0; j < FN; ++j)
     bptr[j] = (const v4i*)(wbase + (tvalid[j] ? gtile[j] : 0) * p.k_chunks * 1024) + lane;
 
-  const int64_t lda_bytes = p.lda * (I8 ? 1 : 2);
+  const int64_t lda_bytes = p.lda * (I8 ? 1 : 2);  // bf16 rows for the bf16 and W8A16 paths
   const int64_t kc = p.k_chunks;
 
   // ---- A sources. Direct: lane l reads row l%16 of each fragment, bytes
@@ -108,7 +113,7 @@ __global__ __launch_bounds__(WM * WN * kWave) void grouped_gemm_kernel(GemmParam
   };
   if constexpr (ADIRECT) {
 #pragma unroll
-    for (int i = 0; i < FM; ++i) afrag[i] = row_ptr(i * 16 + lane % 16) + (lane / 16) * 16;
+    for (int i = 0; i < FM; ++i) afrag[i] = row_ptr(i * 16 + lane % 16) + (lane / 16) * 16 * AW;
   } else {
     static_assert(UNITS % kThreads == 0, "LDS A tiles must split evenly over the workgroup");
     // compile-time unit indices keep these arrays in registers
@@ -135,7 +140,7 @@ __global__ __launch_bounds__(WM * WN * kWave) void grouped_gemm_kernel(GemmParam
   constexpr int U = (ADIRECT || NB % 2 == 0) ? NB : 2 * NB;  // unroll: slot and set are constants
   static_assert(ADIRECT || FM >= 3, "the fragment ring runs two fragments ahead");
   v4i bq[NB][FN];
-  v4i aq[ADIRECT ? NB : 1][ADIRECT ? FM : 1];
+  v4i aq[ADIRECT ? NB : 1][ADIRECT ? FM : 1][AW];
   v4i areg[ADIRECT ? 1 : 2][ADIRECT ? 1 : UPT];
   v4i af[ADIRECT ? 1 : FM];  // LDS fragments of the current chunk
 
@@ -157,7 +162,9 @@ __global__ __launch_bounds__(WM * WN * kWave) void grouped_gemm_kernel(GemmParam
     }
     if constexpr (ADIRECT) {
 #pragma unroll
-      for (int i = 0; i < FM; ++i) aq[slot][i] = *(const v4i*)(afrag[i] + cc * 64);
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int h = 0; h < AW; ++h) aq[slot][i][h] = *(const v4i*)(afrag[i] + cc * 64 * AW + h * 16);
     }
   };
   auto load_a_regs = [&](int64_t c, auto set_c) {
@@ -221,8 +228,22 @@ __global__ __launch_bounds__(WM * WN * kWave) void grouped_gemm_kernel(GemmParam
       // keep the prefetch ahead of this chunk's MFMAs (the scheduler would
       // otherwise sink the loads below them and drain the ring)
       __builtin_amdgcn_sched_barrier(0);
+      if constexpr (W8) {
+        // int8 weights -> bf16 once per tile, reused by every row fragment
 #pragma unroll
-      for (int i = 0; i < FM; ++i) mfma_row(aq[b % NB][i], i, std::integral_constant<int, b % NB>{});
+        for (int j = 0; j < FN; ++j) {
+          v4i lo, hi;
+          i8x16_to_bf16(bq[b % NB][j], lo, hi);
+#pragma unroll
+          for (int i = 0; i < FM; ++i) {
+            acc[i][j] = mfma(__builtin_bit_cast(v8bf, aq[b % NB][i][0]), __builtin_bit_cast(v8bf, lo), acc[i][j]);
+            acc[i][j] = mfma(__builtin_bit_cast(v8bf, aq[b % NB][i][1]), __builtin_bit_cast(v8bf, hi), acc[i][j]);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < FM; ++i) mfma_row(aq[b % NB][i][0], i, std::integral_constant<int, b % NB>{});
+      }
       __builtin_amdgcn_sched_barrier(0);
     } else {
       const int buf2 = buf == 0 ? 2 : buf - 1;  // (c + 2) % 3
@@ -263,7 +284,7 @@ __global__ __launch_bounds__(WM * WN * kWave) void grouped_gemm_kernel(GemmParam
 
 template <bool I8, int EPI, int WM, int WN, int FM, int FN, int NB, bool ADIRECT>
 int launch_cfg(const GemmParams& p, int64_t max_tiles, hipStream_t stream) {
-  constexpr bool PAIR = (EPI == kEpiW13SwigluI8 || EPI == kEpiW13ActBf16);
+  constexpr bool PAIR = epi_pair(EPI);
   const int64_t per_block = PAIR ? FN / 2 * WN : FN * WN;
   const int64_t units = PAIR ? p.n_tiles : (int64_t)p.n_groups * p.n_tiles;
   const int64_t n_blocks = ceil_div(units, per_block);
@@ -281,7 +302,7 @@ int launch_bm(int bm, const GemmParams& p, int64_t max_tiles, hipStream_t stream
     case 16:
       // decode: W13 pairs 2 gate + 2 up tiles per wave; W2 (short K) runs
       // 2 tiles per wave with a deeper ring, giving twice the waves
-      if constexpr (EPI == kEpiW13SwigluI8 || EPI == kEpiW13ActBf16)
+      if constexpr (epi_pair(EPI))
         return launch_cfg<I8, EPI, 1, 4, 1, 4, 4, true>(p, max_tiles, stream);
       else
         return launch_cfg<I8, EPI, 1, 4, 1, 2, 8, true>(p, max_tiles, stream);
@@ -300,9 +321,27 @@ int launch_bm(int bm, const GemmParams& p, int64_t max_tiles, hipStream_t stream
   }
 }
 
+// W8A16 is a weight-streaming (decode) path: direct-A tiles of 16 or 32 rows.
+template <int EPI>
+int launch_bm_w8(int bm, const GemmParams& p, int64_t max_tiles, hipStream_t stream) {
+  switch (bm) {
+    case 16:
+      if constexpr (epi_pair(EPI))
+        return launch_cfg<false, EPI, 1, 4, 1, 4, 4, true>(p, max_tiles, stream);
+      else
+        return launch_cfg<false, EPI, 1, 4, 1, 2, 8, true>(p, max_tiles, stream);
+    case 32:
+      return launch_cfg<false, EPI, 1, 4, 2, 4, 4, true>(p, max_tiles, stream);
+    default:
+      return fail(FCMOE_EINVAL, "W8A16 tiles are 16 or 32 rows");
+  }
+}
+
 }  // namespace
 
 int gemm_launch(int epi, int bm, const GemmParams& p, int64_t max_tiles, hipStream_t stream) {
+  if (epi == kEpiW13ActW8) return launch_bm_w8<kEpiW13ActW8>(bm, p, max_tiles, stream);
+  if (epi == kEpiW2RouteW8) return launch_bm_w8<kEpiW2RouteW8>(bm, p, max_tiles, stream);
   static const bool use_lds = [] {
     const char* v = getenv("FCMOE_GEMM_LDS");
     return !(v && v[0] == '0');

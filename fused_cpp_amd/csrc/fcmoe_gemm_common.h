@@ -55,6 +55,40 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_s_barrier();
 }
 
+// W13 epilogues pair gate and up tiles; W8A16 epilogues stream int8 weights
+// against bf16 activations.
+__host__ __device__ constexpr bool epi_pair(int epi) {
+  return epi == kEpiW13SwigluI8 || epi == kEpiW13ActBf16 || epi == kEpiW13ActW8;
+}
+__host__ __device__ constexpr bool epi_w8(int epi) { return epi == kEpiW13ActW8 || epi == kEpiW2RouteW8; }
+
+// 16 int8 weights -> two bf16 MFMA operands (bytes 0-7, bytes 8-15), as
+// packed bf16 pairs in 32-bit words. Exact: the bytes are biased to unsigned
+// (x ^ 0x80), converted with v_cvt_f32_ubyteN, un-biased by an exact
+// subtraction of 128, and |q| <= 127 has at most 7 significant bits, so the
+// high 16 bits of the fp32 value are its bf16 value (v_perm packs two).
+__device__ __forceinline__ uint32_t bf16_pair(float lo, float hi) {
+  return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
+}
+__device__ __forceinline__ void i8x16_to_bf16(v4i b, v4i& lo, v4i& hi) {
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const uint32_t u = (uint32_t)b[w] ^ 0x80808080u;
+    const float f0 = (float)(u & 0xffu) - 128.0f;
+    const float f1 = (float)((u >> 8) & 0xffu) - 128.0f;
+    const float f2 = (float)((u >> 16) & 0xffu) - 128.0f;
+    const float f3 = (float)(u >> 24) - 128.0f;
+    const int p0 = (int)bf16_pair(f0, f1), p1 = (int)bf16_pair(f2, f3);
+    if (w < 2) {
+      lo[2 * w] = p0;
+      lo[2 * w + 1] = p1;
+    } else {
+      hi[2 * (w - 2)] = p0;
+      hi[2 * (w - 2) + 1] = p1;
+    }
+  }
+}
+
 // Fused epilogues. W13 pairs: tiles j < FN/2 are gate tiles and tile
 // j + FN/2 is the matching up tile (same channels of the other group).
 //
@@ -73,18 +107,18 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, const typenam
     *ok = r < rows;
     return pos0 + (r < rows ? r : rows - 1);  // clamped: loads stay in range
   };
-  if constexpr (EPI == kEpiW13SwigluI8 || EPI == kEpiW13ActBf16) {
+  if constexpr (epi_pair(EPI)) {
     constexpr int HP = FN / 2;
     const int64_t n = p.n;  // 2F logical
     int f[HP];
     bool fv[HP];
-    float cg[HP], cu[HP];  // W13 int8: gate / up channel scales; bf16: biases
+    float cg[HP], cu[HP];  // W13 int8 / W8A16: gate / up channel scales; bf16: biases
 #pragma unroll
     for (int j = 0; j < HP; ++j) {
       f[j] = (int)(gtile[j] * 16 + col);  // gate channel (group 0)
       fv[j] = tvalid[j] && f[j] < p.n_half;
       const int64_t fc = fv[j] ? f[j] : 0;
-      if constexpr (EPI == kEpiW13SwigluI8) {
+      if constexpr (EPI == kEpiW13SwigluI8 || EPI == kEpiW13ActW8) {
         cg[j] = p.scale_col[(int64_t)expert * n + fc];
         cu[j] = p.scale_col[(int64_t)expert * n + p.n_half + fc];
       } else {
@@ -117,6 +151,9 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, const typenam
             up = fmaxf(fminf(up, 10.0f), -10.0f);
             const float ex = fexpa_exp_neg(gate);
             y = (gate * up) / (ex + 1.0f);
+          } else if constexpr (EPI == kEpiW13ActW8) {
+            // x . (q * s) accumulated as (x . q) * s in fp32
+            y = act_bf16_mode(acc[i][j][q] * cg[j], acc[i][j + HP][q] * cu[j], p.activation);
           } else {
             float gate = acc[i][j][q];
             float up = acc[i][j + HP][q];
@@ -137,7 +174,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, const typenam
       }
     }
   } else {
-    constexpr bool ROUTE = EPI == kEpiW2RouteI8 || EPI == kEpiW2RouteBf16;
+    constexpr bool ROUTE = EPI == kEpiW2RouteI8 || EPI == kEpiW2RouteBf16 || EPI == kEpiW2RouteW8;
     constexpr bool ROWSCALE = EPI == kEpiW2RouteI8 || EPI == kEpiI8Gemm;
     int ch[FN], dch[FN];
     bool cv[FN];
@@ -152,7 +189,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, const typenam
       dch[j] = EPI == kEpiRawF32Bias ? (int)(gtile[j] * 16 + col) : ch[j];  // RawF32Bias: packed order
       cs[j] = 0.0f;
       cb[j] = 0.0f;
-      if constexpr (EPI == kEpiW2RouteI8) cs[j] = p.scale_col[(int64_t)expert * p.n + ch[j]];
+      if constexpr (EPI == kEpiW2RouteI8 || EPI == kEpiW2RouteW8) cs[j] = p.scale_col[(int64_t)expert * p.n + ch[j]];
       if constexpr (EPI == kEpiI8Gemm) {
         cs[j] = p.scale_col[ch[j]];
         if (p.bias) cb[j] = p.bias[ch[j]];
@@ -192,6 +229,8 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, const typenam
               ((uint16_t*)p.out)[obase + ch[j]] = f32_to_bf16(v);
             else
               ((float*)p.out)[obase + ch[j]] = v;
+          } else if constexpr (EPI == kEpiW2RouteW8) {
+            ((float*)p.out)[obase + ch[j]] = acc[i][j][q] * cs[j];
           } else {  // kEpiRawF32Bias, kEpiW2RouteBf16
             float v = acc[i][j][q];
             if (p.bias) v = v + cb[j];

@@ -63,7 +63,7 @@ __global__ __launch_bounds__(kThreadsLds) void grouped_gemm_lds_kernel(GemmParam
   constexpr int LA = BM / 16;             // A loads (16 rows x 64 bytes) per stage
   constexpr int L = LA + NT;              // loads per stage
   constexpr int LPW = (L + kWaves - 1) / kWaves;  // loads per wave per stage
-  constexpr bool PAIR = (EPI == kEpiW13SwigluI8 || EPI == kEpiW13ActBf16);
+  constexpr bool PAIR = epi_pair(EPI);
   constexpr int HP = FN / 2;
   static_assert(L >= kWaves, "every wave issues at least one load per stage");
   static_assert(FM >= 3, "the fragment ring runs two fragments ahead");
@@ -196,7 +196,7 @@ __global__ __launch_bounds__(kThreadsLds) void grouped_gemm_lds_kernel(GemmParam
 
 template <bool I8, int EPI, int FM, int FN>
 int launch_lds_cfg(const GemmParams& p, int64_t max_tiles, hipStream_t stream) {
-  constexpr bool PAIR = (EPI == kEpiW13SwigluI8 || EPI == kEpiW13ActBf16);
+  constexpr bool PAIR = epi_pair(EPI);
   const int64_t per_block = PAIR ? (int64_t)kWN * (FN / 2) : (int64_t)kWN * FN;
   const int64_t units = PAIR ? p.n_tiles : (int64_t)p.n_groups * p.n_tiles;
   const int64_t n_blocks = ceil_div(units, per_block);

@@ -81,6 +81,8 @@ enum Epilogue : int {
   kEpiW13ActBf16,     // bf16: acc (+bias) -> activation -> bf16 y
   kEpiRawF32Bias,     // bf16: acc (+bias) -> fp32 gate_up (natural channel order)
   kEpiW2RouteBf16,    // bf16: acc (+bias) -> fp32 route rows
+  kEpiW13ActW8,       // W8A16 (bf16 A, int8 B): acc * s_w -> activation -> bf16 y
+  kEpiW2RouteW8,      // W8A16: acc * s_w -> fp32 route rows
 };
 
 struct GemmParams {

@@ -56,25 +56,43 @@ at::Tensor pack(const at::Tensor& w, int n_groups) {
 using W8A8Tuple =
     std::tuple<at::Tensor, int64_t, int64_t, at::Tensor, at::Tensor, int64_t, int64_t, at::Tensor, int64_t, int64_t>;
 
-// Packs checkpoint int8 experts (csrc/moe/arm/i8mm_w8a8/kernels.cpp:424-444).
-W8A8Tuple w8a8_prepare_quantized(at::Tensor w13, at::Tensor s13, at::Tensor w2, at::Tensor s2) {
+// Packs per-channel int8 experts plus fp32 scales. `what` names the path in
+// errors; W8A8 requires H, F % 16 (csrc/moe/arm/i8mm_w8a8/kernels.cpp:55),
+// W8A16 requires F % 8 (fused_moe_bf16_tiled.cpp:5035).
+W8A8Tuple pack_int8_experts(at::Tensor w13, at::Tensor s13, at::Tensor w2, at::Tensor s2, const char* what,
+                            bool w8a16) {
   check_device(w13, "w13_weight");
   check_device(w2, "w2_weight");
-  TORCH_CHECK(w13.scalar_type() == at::kChar && w2.scalar_type() == at::kChar,
-              "W8A8 weights must have dtype torch.int8");
-  TORCH_CHECK(w13.dim() == 3 && w2.dim() == 3, "W8A8 weights must be [E, 2F, H] and [E, H, F]");
-  TORCH_CHECK(w13.size(0) > 0 && w13.size(0) == w2.size(0), "W8A8 expert counts must match and be positive");
-  TORCH_CHECK(w13.size(1) % 2 == 0, "W8A8 W13 output dimension must be even");
+  TORCH_CHECK(w13.scalar_type() == at::kChar && w2.scalar_type() == at::kChar, what,
+              " weights must have dtype torch.int8");
+  TORCH_CHECK(w13.dim() == 3 && w2.dim() == 3, what, " weights must be [E, 2F, H] and [E, H, F]");
+  TORCH_CHECK(w13.size(0) > 0 && w13.size(0) == w2.size(0), what, " expert counts must match and be positive");
+  TORCH_CHECK(w13.size(1) % 2 == 0, what, " W13 output dimension must be even");
   const int64_t e = w13.size(0), f = w13.size(1) / 2, h = w13.size(2);
-  TORCH_CHECK(w2.size(1) == h && w2.size(2) == f, "W8A8 W2 shape mismatch");
-  TORCH_CHECK(h % 16 == 0 && f % 16 == 0, "W8A8 requires H and F to be multiples of 16");
-  TORCH_CHECK(s13.scalar_type() == at::kFloat && s2.scalar_type() == at::kFloat, "W8A8 scales must be float32");
-  TORCH_CHECK(s13.numel() == e * 2 * f, "W8A8 W13 scales must contain one value per output channel");
-  TORCH_CHECK(s2.numel() == e * h, "W8A8 W2 scales must contain one value per output channel");
+  TORCH_CHECK(w2.size(1) == h && w2.size(2) == f, what, " W2 shape mismatch");
+  if (w8a16) {
+    TORCH_CHECK(f % 8 == 0, "W8A16 fused W13 requires F % 8 == 0, got ", f);
+  } else {
+    TORCH_CHECK(h % 16 == 0 && f % 16 == 0, what, " requires H and F to be multiples of 16");
+  }
+  TORCH_CHECK(s13.scalar_type() == at::kFloat && s2.scalar_type() == at::kFloat, what, " scales must be float32");
+  TORCH_CHECK(s13.numel() == e * 2 * f, what, " W13 scales must contain one value per output channel");
+  TORCH_CHECK(s2.numel() == e * h, what, " W2 scales must contain one value per output channel");
   at::Tensor p13 = pack(w13.contiguous(), 2);
   at::Tensor p2 = pack(w2.contiguous(), 1);
   return {p13, h, 2 * f, s13.to(w13.device()).reshape({e, 2 * f}).contiguous(), p2, f, h,
           s2.to(w13.device()).reshape({e, h}).contiguous(), kBackendId, 16};
+}
+
+// Packs checkpoint int8 experts (csrc/moe/arm/i8mm_w8a8/kernels.cpp:424-444).
+W8A8Tuple w8a8_prepare_quantized(at::Tensor w13, at::Tensor s13, at::Tensor w2, at::Tensor s2) {
+  return pack_int8_experts(w13, s13, w2, s2, "W8A8", false);
+}
+
+// W8A16 checkpoint packing (fused_moe_bf16_tiled.cpp:5012-5112): the same
+// per-channel int8 + fp32 scale layout as W8A8.
+W8A8Tuple w8a16_prepare_quantized(at::Tensor w13, at::Tensor s13, at::Tensor w2, at::Tensor s2) {
+  return pack_int8_experts(w13, s13, w2, s2, "W8A16", true);
 }
 
 // Quantise bf16 experts per output channel on the GPU, then pack
@@ -99,6 +117,32 @@ W8A8Tuple w8a8_prepare(at::Tensor w13, at::Tensor w2) {
   auto [q13, s13] = quant(w13);
   auto [q2, s2] = quant(w2);
   return w8a8_prepare_quantized(q13, s13, q2, s2);
+}
+
+// W8A16 prepare from bf16 (fused_moe_bf16_tiled.cpp:6211-6266,
+// quantize_pack_expert_weight_per_channel :4947-4976): the same per-channel
+// quantisation as W8A8 (scale = max|w| / 127, or 1; q = nearbyint(w / scale)
+// clamped to +-127).
+W8A8Tuple w8a16_prepare(at::Tensor w13, at::Tensor w2) {
+  check_device(w13, "w13_weight");
+  check_device(w2, "w2_weight");
+  TORCH_CHECK(w13.scalar_type() == at::kBFloat16 && w2.scalar_type() == at::kBFloat16,
+              "W8A16 source weights must be torch.bfloat16");
+  TORCH_CHECK(w13.dim() == 3 && w2.dim() == 3, "W8A16 weights must be [E, 2F, H] and [E, H, F]");
+  auto quant = [](const at::Tensor& src) {
+    at::Tensor s = src.contiguous();
+    const int64_t cols = s.size(-1);
+    const int64_t rows = s.numel() / cols;
+    at::Tensor q = at::empty(s.sizes(), s.options().dtype(at::kChar));
+    at::Tensor sc = at::empty({s.size(0), s.size(1)}, s.options().dtype(at::kFloat));
+    check_rc(fcmoe_quantize_weight_rows((const uint16_t*)s.data_ptr(), rows, cols, (int8_t*)q.data_ptr(),
+                                        sc.data_ptr<float>(), current_stream()),
+             "quantize_weight_rows");
+    return std::make_pair(q, sc);
+  };
+  auto [q13, s13] = quant(w13);
+  auto [q2, s2] = quant(w2);
+  return w8a16_prepare_quantized(q13, s13, q2, s2);
 }
 
 fcmoe_moe_args base_args(const at::Tensor& input, const at::Tensor& topk_weights, const at::Tensor& topk_ids,
@@ -252,6 +296,44 @@ at::Tensor bf16_forward(at::Tensor input, at::Tensor w13, int64_t w13_k, int64_t
   return output;
 }
 
+// W8A16 forward (bf16_tiled.py:1309-1373; native fused_moe_bf16_tiled.cpp
+// W8A16 executor): int8 per-channel weights, bf16 activations, fp32 accumulate
+// with the channel scale applied to the accumulator, bf16 intermediate.
+at::Tensor w8a16_forward(at::Tensor input, at::Tensor w13, int64_t w13_k, int64_t w13_n, at::Tensor s13,
+                         at::Tensor w2, int64_t w2_k, int64_t w2_n, at::Tensor s2, at::Tensor topk_weights,
+                         at::Tensor topk_ids, std::string activation, int64_t global_num_experts, bool skip_weighted,
+                         int64_t shared_id, double routed_scale, c10::optional<at::Tensor> out, bool validate_ids) {
+  check_routing(input, topk_weights, topk_ids);
+  check_device(w13, "w13_packed");
+  TORCH_CHECK(input.size(1) == w13_k && w13_n == 2 * w2_k && w2_n == w13_k, "W8A16 expert dimensions mismatch");
+  const int64_t e = w13.size(0);
+  TORCH_CHECK(w2.size(0) == e && s13.sizes() == at::IntArrayRef({e, w13_n}) && s2.sizes() == at::IntArrayRef({e, w2_n}),
+              "W8A16 packed weights/scales are invalid");
+  TORCH_CHECK(w13.size(1) == fcmoe_packed_expert_bytes(1, w13_n, w13_k, 2) &&
+                  w2.size(1) == fcmoe_packed_expert_bytes(1, w2_n, w2_k, 1),
+              "W8A16 packed weight strides are invalid");
+  at::Tensor output = output_for(input, out);
+  at::Tensor invalid = at::zeros({1}, input.options().dtype(at::kInt));
+  fcmoe_moe_args a = base_args(input, topk_weights, topk_ids, e, shared_id, routed_scale, global_num_experts, output);
+  a.inter = w2_k;
+  a.w13 = w13.data_ptr();
+  a.w2 = w2.data_ptr();
+  a.w13_scale = s13.data_ptr<float>();
+  a.w2_scale = s2.data_ptr<float>();
+  a.activation = activation_code(activation);
+  a.skip_weighted = skip_weighted ? 1 : 0;
+  a.invalid_count = invalid.data_ptr<int32_t>();
+  at::Tensor ws = workspace(fcmoe_w8a16_workspace_bytes(&a), input);
+  a.workspace = ws.data_ptr();
+  a.workspace_bytes = ws.numel();
+  {
+    pybind11::gil_scoped_release release;
+    check_rc(fcmoe_w8a16_forward(&a, current_stream()), "fused_moe_w8a16");
+  }
+  maybe_check_invalid(invalid, validate_ids);
+  return output;
+}
+
 // i8gemm prepare (csrc/i8gemm.cpp:280-316): packed weight, fp32 [N] scales,
 // K, N, Kp, Np, backend name.
 std::tuple<at::Tensor, at::Tensor, int64_t, int64_t, int64_t, int64_t, std::string> i8gemm_prepare(
@@ -311,6 +393,9 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("fused_moe_w8a8_prepare_weights", &w8a8_prepare);
   m.def("fused_moe_w8a8_prepare_quantized_weights", &w8a8_prepare_quantized);
   m.def("fused_moe_w8a8_forward", &w8a8_forward);
+  m.def("fused_moe_w8a16_prepare_weights", &w8a16_prepare);
+  m.def("fused_moe_w8a16_prepare_quantized_weights", &w8a16_prepare_quantized);
+  m.def("fused_moe_w8a16_forward", &w8a16_forward);
   m.def("fused_moe_bf16_prepare_weights", &bf16_prepare);
   m.def("fused_moe_bf16_forward", &bf16_forward);
   m.def("i8gemm_prepare", &i8gemm_prepare);

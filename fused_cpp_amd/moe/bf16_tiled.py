@@ -51,7 +51,7 @@ class PreparedBF16TiledFusedMoEWeights:
 
 @dataclass(frozen=True)
 class PreparedW8A16TiledFusedMoEWeights:
-    """Per-output-channel INT8 weights for the W8A16 path (not in this build)."""
+    """Per-output-channel INT8 weights (packed, fp32 scales) against BF16 activations."""
 
     w13: tuple[torch.Tensor, int, int, torch.Tensor]
     w2: tuple[torch.Tensor, int, int, torch.Tensor]
@@ -339,16 +339,67 @@ def prepare_routed_shared_moe_bf16_tiled_weights(
     return PreparedBF16TiledRoutedSharedMoEWeights(packed=combined, routed_experts=e, shared_expert_id=e)
 
 
-def prepare_fused_moe_w8a16_tiled_weights(w13_weight: torch.Tensor, w2_weight: torch.Tensor):
-    raise RuntimeError("W8A16 fused MoE packing is unavailable in this build")
+def _prepared_w8a16(packed: tuple) -> PreparedW8A16TiledFusedMoEWeights:
+    return PreparedW8A16TiledFusedMoEWeights(
+        w13=(packed[0], int(packed[1]), int(packed[2]), packed[3]),
+        w2=(packed[4], int(packed[5]), int(packed[6]), packed[7]),
+        gemm_backend=int(packed[8]),
+        backend_n_tile=int(packed[9]),
+    )
 
 
-def prepare_fused_moe_w8a16_tiled_quantized_weights(w13_weight, w13_scale, w2_weight, w2_scale):
-    raise RuntimeError("pre-quantized W8A16 fused MoE packing is unavailable in this build")
+def prepare_fused_moe_w8a16_tiled_weights(
+    w13_weight: torch.Tensor,
+    w2_weight: torch.Tensor,
+) -> PreparedW8A16TiledFusedMoEWeights:
+    """Quantize BF16 expert weights to symmetric per-output-channel INT8 (bf16_tiled.py:453-472).
+
+    scale = max|w|/127 (1 if zero), q = nearbyint(w/scale) clamped to +-127
+    (fused_moe_bf16_tiled.cpp:4947-4976), computed on the GPU. The packed layout
+    is the W8A8 one: the weights stream through the same MFMA operand tiles.
+    """
+    _require_backend()
+    if w13_weight.dtype != torch.bfloat16 or w2_weight.dtype != torch.bfloat16:
+        raise TypeError("W8A16 source weights must be torch.bfloat16")
+    return _prepared_w8a16(_native.moe_C.fused_moe_w8a16_prepare_weights(_to_device(w13_weight),
+                                                                         _to_device(w2_weight)))
 
 
-def prepare_routed_shared_moe_w8a16_tiled_quantized_weights(*args: Any, **kwargs: Any):
-    raise RuntimeError("pre-quantized routed+shared W8A16 packing is unavailable in this build")
+def prepare_fused_moe_w8a16_tiled_quantized_weights(
+    w13_weight: torch.Tensor,
+    w13_scale: torch.Tensor,
+    w2_weight: torch.Tensor,
+    w2_scale: torch.Tensor,
+) -> PreparedW8A16TiledFusedMoEWeights:
+    """Pack checkpoint INT8 expert weights without dequantizing or requantizing (bf16_tiled.py:484-499)."""
+    _require_backend()
+    return _prepared_w8a16(_native.moe_C.fused_moe_w8a16_prepare_quantized_weights(
+        _to_device(w13_weight), _to_device(w13_scale.float()), _to_device(w2_weight), _to_device(w2_scale.float())))
+
+
+def prepare_routed_shared_moe_w8a16_tiled_quantized_weights(
+    routed_w13_weight: torch.Tensor,
+    routed_w13_scale: torch.Tensor,
+    routed_w2_weight: torch.Tensor,
+    routed_w2_scale: torch.Tensor,
+    shared_w13_weight: torch.Tensor,
+    shared_w13_scale: torch.Tensor,
+    shared_w2_weight: torch.Tensor,
+    shared_w2_scale: torch.Tensor,
+) -> PreparedW8A16TiledRoutedSharedMoEWeights:
+    """Routed checkpoint INT8 experts plus one same-shape shared expert appended as expert E
+    (bf16_tiled.py:541-570; native fused_moe_bf16_tiled.cpp:6276-6288)."""
+    if shared_w13_weight.dim() != 2 or shared_w2_weight.dim() != 2:
+        raise ValueError("shared W8A16 weights must be [2F, H] and [H, F]")
+    e = int(routed_w13_weight.shape[0])
+    dev = lambda t: _to_device(t)  # noqa: E731
+    packed = prepare_fused_moe_w8a16_tiled_quantized_weights(
+        torch.cat((dev(routed_w13_weight), dev(shared_w13_weight).unsqueeze(0)), dim=0),
+        torch.cat((dev(routed_w13_scale).reshape(e, -1), dev(shared_w13_scale).reshape(1, -1)), dim=0),
+        torch.cat((dev(routed_w2_weight), dev(shared_w2_weight).unsqueeze(0)), dim=0),
+        torch.cat((dev(routed_w2_scale).reshape(e, -1), dev(shared_w2_scale).reshape(1, -1)), dim=0),
+    )
+    return PreparedW8A16TiledRoutedSharedMoEWeights(packed=packed, routed_experts=e, shared_expert_id=e)
 
 
 # ---------------------------------------------------------------- BF16 ops --
@@ -664,16 +715,147 @@ def fused_moe_w8a8_tiled_with_shared(
 
 # --------------------------------------------------------------- W8A16 ops --
 
-def fused_moe_w8a16_tiled_async_plan(*args: Any, **kwargs: Any) -> torch.Tensor:
-    raise RuntimeError("W8A16 Plan V2 execution is unavailable in this build")
+def _w8a16_call(input, weights, topk_weights, topk_ids, *, activation, global_num_experts, skip_weighted, shared_id,
+                scaling, out):
+    w13, w2 = weights.w13, weights.w2
+    return _native.moe_C.fused_moe_w8a16_forward(
+        input.contiguous(), w13[0], int(w13[1]), int(w13[2]), w13[3], w2[0], int(w2[1]), int(w2[2]), w2[3],
+        topk_weights, topk_ids, activation, int(global_num_experts), bool(skip_weighted), int(shared_id),
+        float(scaling), out, _native.validate_ids_default())
 
 
-def fused_moe_w8a16_tiled(*args: Any, **kwargs: Any) -> torch.Tensor:
-    raise RuntimeError("W8A16 fused MoE is unavailable in this build")
+def _w8a16_activation(activation: Any, weights: PreparedW8A16TiledFusedMoEWeights, swiglu_limit) -> str:
+    native = _native_activation_name(activation, weights, swiglu_limit)
+    if native not in ("silu", "silu_clamp10", "gelu"):
+        raise ValueError(f"W8A16 fused MoE supports silu (optionally clamped) and gelu, got {native!r}")
+    return native
 
 
-def fused_moe_w8a16_tiled_with_shared(*args: Any, **kwargs: Any) -> torch.Tensor:
-    raise RuntimeError("routed+shared W8A16 fused MoE is unavailable in this build")
+def _check_w8a16_call(input, weights, topk_weights, topk_ids, num_threads, global_num_experts, skip_weighted,
+                      silu_poly_degree, out):
+    if not isinstance(weights, PreparedW8A16TiledFusedMoEWeights):
+        raise TypeError("weights must be PreparedW8A16TiledFusedMoEWeights")
+    if input.dtype != torch.bfloat16:
+        raise TypeError("W8A16 input must be a torch.bfloat16 tensor")
+    if topk_ids.dtype not in _INTEGER_DTYPES:
+        raise TypeError(f"topk_ids must use an integer dtype, got {topk_ids.dtype}")
+    if not topk_weights.dtype.is_floating_point:
+        raise TypeError(f"topk_weights must use a floating dtype, got {topk_weights.dtype}")
+    _check_routing(input, topk_weights, topk_ids)
+    if int(num_threads) <= 0:
+        raise ValueError(f"num_threads must be positive, got {num_threads}")
+    if int(silu_poly_degree) not in (4, 5, 6):
+        raise ValueError("silu_poly_degree must be 4, 5 or 6")
+    if bool(skip_weighted) and int(topk_ids.shape[1]) != 1:
+        raise ValueError("skip_weighted is only valid when top_k == 1")
+    experts = int(weights.w13[0].shape[0])
+    if global_num_experts != -1 and not (0 < int(global_num_experts) <= experts):
+        raise RuntimeError(f"global_num_experts must be positive and <= {experts}, got {global_num_experts}")
+    _validate_output_buffer(input, out)
+
+
+def fused_moe_w8a16_tiled_async_plan(
+    input: torch.Tensor,
+    weights: PreparedW8A16TiledFusedMoEWeights,
+    topk_weights: torch.Tensor,
+    topk_ids: torch.Tensor,
+    plan: AsyncMoEPlanV2 | Mapping[str, object],
+    *,
+    activation: Any = "silu",
+    global_num_experts: int = -1,
+    skip_weighted: bool = False,
+    silu_poly_degree: int = 5,
+    swiglu_limit: float | None = None,
+    cache_dequant: bool = False,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Per-channel W8A16 experts (bf16_tiled.py:1309-1373); the plan is schema-checked only."""
+    _require_backend()
+    materialize_plan(plan)
+    return fused_moe_w8a16_tiled(input, weights, topk_weights, topk_ids, activation=activation,
+                                 global_num_experts=global_num_experts, skip_weighted=skip_weighted,
+                                 silu_poly_degree=silu_poly_degree, swiglu_limit=swiglu_limit,
+                                 cache_dequant=cache_dequant, out=out)
+
+
+def fused_moe_w8a16_tiled(
+    input: torch.Tensor,
+    weights: PreparedW8A16TiledFusedMoEWeights,
+    topk_weights: torch.Tensor,
+    topk_ids: torch.Tensor,
+    *,
+    num_threads: int = 1,
+    activation: Any = "silu",
+    global_num_experts: int = -1,
+    skip_weighted: bool = False,
+    silu_poly_degree: int = 5,
+    swiglu_limit: float | None = None,
+    cache_dequant: bool = False,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """W8A16 fused MoE (bf16_tiled.py:1376-1447) on bf16 MFMA.
+
+    INT8 weights are widened to bf16 in registers (exact) and accumulate against
+    the bf16 activations in fp32; each output channel's scale multiplies its
+    accumulator. ``cache_dequant`` selects a CPU dequantised-window cache in the
+    reference and changes nothing here (weights are never dequantised to memory).
+    No planner runtime is required on the GPU.
+    """
+    _require_backend()
+    _check_w8a16_call(input, weights, topk_weights, topk_ids, num_threads, global_num_experts, skip_weighted,
+                      silu_poly_degree, out)
+    native_act = _w8a16_activation(activation, weights, swiglu_limit)
+    if int(input.shape[0]) == 0:
+        return out if out is not None else torch.empty_like(input)
+    w, _ = _weights_f32(topk_weights)
+    return _w8a16_call(input, weights, w, _ids(topk_ids), activation=native_act,
+                       global_num_experts=global_num_experts, skip_weighted=skip_weighted, shared_id=-1, scaling=1.0,
+                       out=out)
+
+
+def fused_moe_w8a16_tiled_with_shared(
+    input: torch.Tensor,
+    weights: PreparedW8A16TiledRoutedSharedMoEWeights,
+    topk_weights: torch.Tensor,
+    topk_ids: torch.Tensor,
+    *,
+    num_threads: int = 1,
+    routed_scaling_factor: float = 1.0,
+    activation: Any = "silu",
+    silu_poly_degree: int = 5,
+    swiglu_limit: float | None = None,
+    cache_dequant: bool = False,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Checkpoint W8A16 routed experts with one all-token shared expert (bf16_tiled.py:881-961).
+
+    The shared expert is slot k of every token with weight 1.0; routed weights
+    are multiplied by ``routed_scaling_factor`` inside the route kernel.
+    """
+    _require_backend()
+    if not isinstance(weights, PreparedW8A16TiledRoutedSharedMoEWeights):
+        raise TypeError("weights must be PreparedW8A16TiledRoutedSharedMoEWeights")
+    if input.dtype != torch.bfloat16:
+        raise TypeError("input must be a torch.bfloat16 tensor")
+    _check_routing(input, topk_weights, topk_ids)
+    if int(topk_ids.shape[1]) <= 0:
+        raise ValueError("topk tensors must match input tokens and have positive top_k")
+    if int(num_threads) <= 0:
+        raise ValueError(f"num_threads must be positive, got {num_threads}")
+    scaling = float(routed_scaling_factor)
+    if not math.isfinite(scaling):
+        raise ValueError("routed_scaling_factor must be finite")
+    native_act = _w8a16_activation(activation, weights.packed, swiglu_limit)
+    if _activation_name(activation) != "silu":
+        raise ValueError("routed+shared W8A16 scheduling currently requires activation='silu'")
+    _validate_output_buffer(input, out)
+    _check_routed_range(topk_ids, weights.routed_experts)
+    if int(input.shape[0]) == 0:
+        return out if out is not None else torch.empty_like(input)
+    w, scale = _weights_f32(topk_weights, scaling)
+    return _w8a16_call(input, weights.packed, w, _ids(topk_ids), activation=native_act,
+                       global_num_experts=weights.routed_experts, skip_weighted=False,
+                       shared_id=weights.shared_expert_id, scaling=scale, out=out)
 
 
 # ------------------------------------------------------------- dispatcher --

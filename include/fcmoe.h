@@ -146,6 +146,17 @@ int fcmoe_w8a8_forward(const fcmoe_moe_args* args, hipStream_t stream);
 size_t fcmoe_bf16_workspace_bytes(const fcmoe_moe_args* args);
 int fcmoe_bf16_forward(const fcmoe_moe_args* args, hipStream_t stream);
 
+/* W8A16 fused MoE (src/fused_cpp/moe/bf16_tiled.py:1309-1447; native W8A16
+ * executor csrc/moe/arm/common/fused_moe_bf16_tiled.cpp:6211-6288): bf16
+ * activations, int8 weights packed by fcmoe_pack_experts (elem_bytes 1,
+ * the W8A8 layout) with fp32 per-output-channel scales w13_scale [E, 2F] and
+ * w2_scale [E, H]. Products accumulate in fp32 on bf16 MFMA (int8 weights are
+ * exact in bf16); the channel scale multiplies the accumulator. Activation
+ * SILU, GELU or SILU_CLAMP10; no biases. Routing, intermediate (bf16) and
+ * combine as fcmoe_bf16_forward. Weight streaming runs 16/32-row tiles. */
+size_t fcmoe_w8a16_workspace_bytes(const fcmoe_moe_args* args);
+int fcmoe_w8a16_forward(const fcmoe_moe_args* args, hipStream_t stream);
+
 /* ---- i8gemm ------------------------------------------------------------- */
 
 /* Dynamic per-row W8A8 linear: quantise x [m, k] (bf16 or fp32) per row

@@ -225,10 +225,13 @@ def test_fused_moe_tiled_dispatches_on_weight_type(fake_backend, monkeypatch):
         mod.fused_moe_tiled(expected, object(), torch.ones((1, 1)), torch.zeros((1, 1), dtype=torch.int64))
 
 
-def test_w8a16_entry_points_raise_unavailable():
+def test_w8a16_entry_points_fail_loudly_without_a_gpu():
+    """No CPU fallback: on a host without a ROCm device every W8A16 entry raises."""
     from fused_cpp_amd import moe
 
-    with pytest.raises(RuntimeError, match="W8A16"):
-        moe.fused_moe_w8a16_tiled(None, None, None, None)
-    with pytest.raises(RuntimeError, match="W8A16"):
-        moe.prepare_fused_moe_w8a16_tiled_weights(None, None)
+    for fn, args in ((moe.fused_moe_w8a16_tiled, (None, None, None, None)),
+                     (moe.fused_moe_w8a16_tiled_with_shared, (None, None, None, None)),
+                     (moe.prepare_fused_moe_w8a16_tiled_weights, (None, None)),
+                     (moe.prepare_fused_moe_w8a16_tiled_quantized_weights, (None, None, None, None))):
+        with pytest.raises(RuntimeError, match="ROCm device"):
+            fn(*args)

@@ -615,23 +615,11 @@ extern "C" size_t fcmoe_i8gemm_workspace_bytes(int64_t m, int64_t k) {
   return ar.used + 256;
 }
 
-extern "C" int fcmoe_i8gemm(const void* x, int x_is_f32, int64_t m, int64_t k, const void* w_packed,
-                            const float* w_scale, int64_t n, const float* bias, void* out, int out_is_bf16,
-                            void* workspace, size_t workspace_bytes, hipStream_t stream) {
-  if (m < 0 || k <= 0 || n <= 0 || !w_packed || !w_scale) return fail(FCMOE_EINVAL, "i8gemm: bad args");
-  if (m == 0) return FCMOE_OK;
-  if (m > INT32_MAX / 2) return fail(FCMOE_EINVAL, "i8gemm: too many rows");
-  Arena ar;
-  ar.base = (char*)workspace;
-  ar.cap = workspace_bytes;
-  I8Layout L = i8_layout(m, k, ar);
-  if (!ar.base || !ar.ok()) return fail(FCMOE_ESPACE, "i8gemm: workspace too small");
-  int rc = quant_rows_launch(x, x_is_f32, m, k, 1, L.xq, L.kp, L.xs, stream);
-  if (rc) return rc;
-  hipLaunchKernelGGL(single_expert_counts_kernel, dim3(1), dim3(1), 0, stream, L.counts, L.offsets, (int32_t)m);
-  if ((rc = check_launch("i8gemm counts"))) return rc;
-  rc = tiles_from_counts_launch(L.counts, 1, L.tc, L.tiles, L.tile_count, stream);
-  if (rc) return rc;
+namespace {
+
+// One int8 GEMM of the quantised rows in L against a packed [n, k] weight.
+int i8gemm_run(const I8Layout& L, int64_t k, const void* w_packed, const float* w_scale, int64_t n, const float* bias,
+               void* out, int out_is_bf16, hipStream_t stream) {
   GemmParams g{};
   g.a = L.xq;
   g.lda = L.kp;
@@ -654,10 +642,54 @@ extern "C" int fcmoe_i8gemm(const void* x, int x_is_f32, int64_t m, int64_t k, c
     GemmParams p = g;
     p.tiles = L.tiles + 2 * tile_offset(L.tc, c);
     p.tile_count = L.tile_count + c;
-    rc = gemm_launch(kEpiI8Gemm, L.tc.bm[c], p, L.tc.bound[c], stream);
+    const int rc = gemm_launch(kEpiI8Gemm, L.tc.bm[c], p, L.tc.bound[c], stream);
     if (rc) return rc;
   }
   return FCMOE_OK;
+}
+
+// Row quantisation (ties to even) and the single-expert tile list.
+int i8gemm_prologue(const void* x, int x_is_f32, int64_t m, int64_t k, void* workspace, size_t workspace_bytes,
+                    I8Layout* L, hipStream_t stream) {
+  Arena ar;
+  ar.base = (char*)workspace;
+  ar.cap = workspace_bytes;
+  *L = i8_layout(m, k, ar);
+  if (!ar.base || !ar.ok()) return fail(FCMOE_ESPACE, "i8gemm: workspace too small");
+  int rc = quant_rows_launch(x, x_is_f32, m, k, 1, L->xq, L->kp, L->xs, stream);
+  if (rc) return rc;
+  hipLaunchKernelGGL(single_expert_counts_kernel, dim3(1), dim3(1), 0, stream, L->counts, L->offsets, (int32_t)m);
+  if ((rc = check_launch("i8gemm counts"))) return rc;
+  return tiles_from_counts_launch(L->counts, 1, L->tc, L->tiles, L->tile_count, stream);
+}
+
+}  // namespace
+
+extern "C" int fcmoe_i8gemm(const void* x, int x_is_f32, int64_t m, int64_t k, const void* w_packed,
+                            const float* w_scale, int64_t n, const float* bias, void* out, int out_is_bf16,
+                            void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  if (m < 0 || k <= 0 || n <= 0 || !w_packed || !w_scale) return fail(FCMOE_EINVAL, "i8gemm: bad args");
+  if (m == 0) return FCMOE_OK;
+  if (m > INT32_MAX / 2) return fail(FCMOE_EINVAL, "i8gemm: too many rows");
+  I8Layout L;
+  int rc = i8gemm_prologue(x, x_is_f32, m, k, workspace, workspace_bytes, &L, stream);
+  if (rc) return rc;
+  return i8gemm_run(L, k, w_packed, w_scale, n, bias, out, out_is_bf16, stream);
+}
+
+extern "C" int fcmoe_i8gemm_pair(const uint16_t* x, int64_t m, int64_t k, const void* w1_packed, const float* w1_scale,
+                                 int64_t n1, const void* w2_packed, const float* w2_scale, int64_t n2, uint16_t* out1,
+                                 uint16_t* out2, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  if (m < 0 || k <= 0 || n1 <= 0 || n2 <= 0 || !w1_packed || !w1_scale || !w2_packed || !w2_scale)
+    return fail(FCMOE_EINVAL, "i8gemm_pair: bad args");
+  if (m == 0) return FCMOE_OK;
+  if (m > INT32_MAX / 2) return fail(FCMOE_EINVAL, "i8gemm_pair: too many rows");
+  if (!x || !out1 || !out2) return fail(FCMOE_EINVAL, "i8gemm_pair: NULL tensor");
+  I8Layout L;
+  int rc = i8gemm_prologue(x, 0, m, k, workspace, workspace_bytes, &L, stream);
+  if (rc) return rc;
+  if ((rc = i8gemm_run(L, k, w1_packed, w1_scale, n1, nullptr, out1, 1, stream))) return rc;
+  return i8gemm_run(L, k, w2_packed, w2_scale, n2, nullptr, out2, 1, stream);
 }
 
 // ------------------------------------------------------------ diagnostics --

@@ -382,6 +382,33 @@ void i8gemm_dynamic_scaled_mm(at::Tensor output, at::Tensor input, at::Tensor pa
            "i8gemm");
 }
 
+// i8gemm_dynamic_scaled_mm_pair (csrc/i8gemm.cpp:453-570): one activation
+// quantisation shared by two bf16-output GEMMs.
+void i8gemm_dynamic_scaled_mm_pair(at::Tensor out1, at::Tensor out2, at::Tensor input, at::Tensor w1,
+                                   at::Tensor s1, int64_t k, int64_t n1, at::Tensor w2, at::Tensor s2, int64_t n2) {
+  check_device(input, "input");
+  TORCH_CHECK(input.dim() == 2 && input.is_contiguous() && input.scalar_type() == at::kBFloat16 && input.size(1) == k,
+              "i8gemm.dynamic_scaled_mm_pair: input must be contiguous BF16 [M, K]");
+  const int64_t m = input.size(0);
+  for (auto [o, w, sc, n, name] : {std::tuple<at::Tensor&, at::Tensor&, at::Tensor&, int64_t, const char*>{
+                                       out1, w1, s1, n1, "first"},
+                                   std::tuple<at::Tensor&, at::Tensor&, at::Tensor&, int64_t, const char*>{
+                                       out2, w2, s2, n2, "second"}}) {
+    TORCH_CHECK(o.scalar_type() == at::kBFloat16 && o.is_contiguous() && o.sizes() == at::IntArrayRef({m, n}), name,
+                " output must be contiguous BF16 [M, N]");
+    TORCH_CHECK(w.numel() == fcmoe_packed_expert_bytes(1, n, k, 1), name, " packed weight is invalid");
+    TORCH_CHECK(sc.numel() == n && sc.scalar_type() == at::kFloat && sc.is_contiguous(), name,
+                " scale must be contiguous float32 [N]");
+  }
+  if (m == 0) return;
+  at::Tensor ws = workspace(fcmoe_i8gemm_workspace_bytes(m, k), input);
+  pybind11::gil_scoped_release release;
+  check_rc(fcmoe_i8gemm_pair((const uint16_t*)input.data_ptr(), m, k, w1.data_ptr(), s1.data_ptr<float>(), n1,
+                             w2.data_ptr(), s2.data_ptr<float>(), n2, (uint16_t*)out1.data_ptr(),
+                             (uint16_t*)out2.data_ptr(), ws.data_ptr(), ws.numel(), current_stream()),
+           "i8gemm_pair");
+}
+
 std::vector<std::string> available_backends() { return {kBackendName}; }
 
 }  // namespace
@@ -400,4 +427,5 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("fused_moe_bf16_forward", &bf16_forward);
   m.def("i8gemm_prepare", &i8gemm_prepare);
   m.def("i8gemm_dynamic_scaled_mm", &i8gemm_dynamic_scaled_mm);
+  m.def("i8gemm_dynamic_scaled_mm_pair", &i8gemm_dynamic_scaled_mm_pair);
 }

@@ -21,7 +21,7 @@ import torch
 from fused_cpp_amd import _native
 
 _supports_i8gemm = _native.moe_C is not None and _native.gpu_available()
-_i8gemm_dynamic_scaled_mm_pair = None
+_i8gemm_dynamic_scaled_mm_pair = getattr(_native.moe_C, "i8gemm_dynamic_scaled_mm_pair", None)
 
 
 def _require_backend() -> None:
@@ -107,18 +107,29 @@ def mm(x: torch.Tensor, packed: PreparedI8GEMMWeight, *, bias: Optional[torch.Te
 
 def dynamic_scaled_mm_pair(x: torch.Tensor, first: PreparedI8GEMMWeight, second: PreparedI8GEMMWeight, *,
                            nthreads: int = 0) -> tuple[torch.Tensor, torch.Tensor]:
-    """Two BF16-output GEMMs sharing one activation quantisation (i8gemm.py:151-189)."""
+    """Two BF16-output GEMMs sharing one dynamic per-row activation quantisation (i8gemm.py:151-189).
+
+    The input rows are quantised once (scale = max|x|/127, ties-to-even rounding,
+    csrc/i8gemm.cpp:486-505) and both GEMMs read the same int8 rows.
+    """
     _require_backend()
+    if _i8gemm_dynamic_scaled_mm_pair is None:
+        raise RuntimeError("i8gemm dynamic pair kernel is unavailable in this build")
     if not isinstance(first, PreparedI8GEMMWeight) or not isinstance(second, PreparedI8GEMMWeight):
         raise TypeError("first and second must be PreparedI8GEMMWeight")
     if x.dtype != torch.bfloat16 or x.dim() != 2:
         raise TypeError("i8gemm.dynamic_scaled_mm_pair input must be BF16 [M, K]")
-    if first.k != second.k or x.shape[1] != first.k:
+    if first.k != second.k or first.k_padded != second.k_padded or x.shape[1] != first.k:
         raise ValueError("paired i8gemm weights and input must share K and Kp")
     if int(nthreads) < 0:
         raise ValueError("nthreads must be non-negative; zero selects the backend default")
-    return (dynamic_scaled_mm(x, first, out_dtype=torch.bfloat16),
-            dynamic_scaled_mm(x, second, out_dtype=torch.bfloat16))
+    x = x.to(first.packed_weight.device).contiguous()
+    first_output = torch.empty((x.shape[0], first.n), dtype=torch.bfloat16, device=x.device)
+    second_output = torch.empty((x.shape[0], second.n), dtype=torch.bfloat16, device=x.device)
+    _i8gemm_dynamic_scaled_mm_pair(first_output, second_output, x, first.packed_weight, first.weight_scale,
+                                   int(first.k), int(first.n), second.packed_weight, second.weight_scale,
+                                   int(second.n))
+    return first_output, second_output
 
 
 __all__ = [

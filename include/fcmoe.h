@@ -170,6 +170,15 @@ int fcmoe_i8gemm(const void* x, int x_is_f32, int64_t m, int64_t k, const void* 
                  int64_t n, const float* bias, void* out, int out_is_bf16, void* workspace, size_t workspace_bytes,
                  hipStream_t stream);
 
+/* Two bf16-output GEMMs of one bf16 input [m, k] sharing a single per-row
+ * activation quantisation (ties to even; scale = max|x|/127): out1 [m, n1]
+ * and out2 [m, n2], no bias. Replaces i8gemm_dynamic_scaled_mm_pair
+ * (csrc/i8gemm.cpp:453-570) behind i8gemm.dynamic_scaled_mm_pair
+ * (src/fused_cpp/i8gemm.py:151-189). Workspace: fcmoe_i8gemm_workspace_bytes(m, k). */
+int fcmoe_i8gemm_pair(const uint16_t* x, int64_t m, int64_t k, const void* w1_packed, const float* w1_scale,
+                      int64_t n1, const void* w2_packed, const float* w2_scale, int64_t n2, uint16_t* out1,
+                      uint16_t* out2, void* workspace, size_t workspace_bytes, hipStream_t stream);
+
 /* ---- diagnostics (stage-level parity checks) ---------------------------- */
 
 /* Grouped int8 GEMM returning raw int32 accumulators: for each expert e and

@@ -235,3 +235,16 @@ def test_w8a16_entry_points_fail_loudly_without_a_gpu():
                      (moe.prepare_fused_moe_w8a16_tiled_quantized_weights, (None, None, None, None))):
         with pytest.raises(RuntimeError, match="ROCm device"):
             fn(*args)
+
+
+def test_deepseek_v4_w8a8_surface_matches_reference_names():
+    """src/fused_cpp/deepseek_v4_w8a8.py __all__; entry points fail loudly without a GPU."""
+    from fused_cpp_amd import deepseek_v4_w8a8 as ds
+
+    assert set(ds.__all__) == {
+        "PreparedDeepSeekV4W8A8LinearWeight", "_HAS_DEEPSEEK_V4_W8A8", "deepseek_v4_w8a8_linear",
+        "deepseek_v4_w8a8_linear_pair", "deepseek_v4_wo_b_w8a8", "prepare_deepseek_v4_w8a8_linear_quantized_weight",
+        "prepare_deepseek_v4_w8a8_linear_weight"}
+    if not ds._HAS_DEEPSEEK_V4_W8A8:
+        with pytest.raises(RuntimeError):
+            ds.prepare_deepseek_v4_w8a8_linear_weight(torch.zeros((4, 8), dtype=torch.bfloat16))

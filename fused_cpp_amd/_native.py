@@ -42,5 +42,14 @@ def gpu_available() -> bool:
 def validate_ids_default() -> bool:
     """Range-check topk_ids after each call (one device->host read), as the
     reference does on the host (csrc/moe/arm/i8mm_w8a8/kernels.cpp:583-587).
-    Set FUSED_CPP_AMD_VALIDATE_IDS=0 to skip the read on latency-critical paths."""
-    return os.environ.get("FUSED_CPP_AMD_VALIDATE_IDS", "1") != "0"
+    Set FUSED_CPP_AMD_VALIDATE_IDS=0 to skip the read on latency-critical paths.
+    The read is skipped while the current stream is being captured into a
+    HIP graph (a host read cannot be captured; invalid ids then contribute
+    nothing, as with the variable set to 0)."""
+    if os.environ.get("FUSED_CPP_AMD_VALIDATE_IDS", "1") == "0":
+        return False
+    import torch
+
+    if not torch.cuda.is_initialized():
+        return True  # nothing can be capturing before the device is initialised
+    return not torch.cuda.is_current_stream_capturing()

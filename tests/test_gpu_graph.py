@@ -1,0 +1,110 @@
+"""The fused-MoE operators under HIP graph capture (torch.cuda.CUDAGraph).
+
+Each graph is replayed several times with new inputs copied into its static
+buffers and unrelated eager work plus synchronisations between replays; every
+replay must equal the eager result bit for bit (the same kernels run).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from tests import helpers as H
+
+pytestmark = pytest.mark.gpu
+
+
+def _replay_matches_eager(fn, make_inputs, static_inputs, replays=3):
+    torch.cuda.synchronize()
+    # warm up on a side stream (allocator pools, side streams, lazily created events)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(2):
+            fn(*static_inputs)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        static_out = fn(*static_inputs)
+    for r in range(replays):
+        fresh = make_inputs(r)
+        for dst, src in zip(static_inputs, fresh):
+            if isinstance(dst, torch.Tensor):
+                dst.copy_(src)
+        noise = torch.randn(4096, device=static_out.device).sum()  # eager work between replays
+        g.replay()
+        torch.cuda.synchronize()
+        expected = fn(*fresh)
+        torch.cuda.synchronize()
+        assert torch.equal(static_out, expected), f"replay {r} differs from eager"
+        assert torch.isfinite(noise)
+
+
+def test_w8a8_forward_graph_replays(gpu):
+    from fused_cpp_amd import moe
+
+    case = H.w8a8_case(21, 48, 1024, 512, 17, 4)
+    x, ids, w, q13, s13, q2, s2 = case
+    t = torch.from_numpy
+    prepared = moe.prepare_routed_shared_moe_w8a8_tiled_quantized_weights(
+        t(q13[:-1]), t(s13[:-1]), t(q2[:-1]), t(s2[:-1]), t(q13[-1]), t(s13[-1]), t(q2[-1]), t(s2[-1]))
+    ids = np.minimum(ids, 15)
+    rng = np.random.default_rng(0)
+
+    def make(r):
+        xr = torch.from_numpy(H.bf16_bits(rng.standard_normal((48, 1024)).astype(np.float32)).view(np.int16))
+        idr = torch.from_numpy(rng.integers(0, 16, size=(48, 4)).astype(np.int64))
+        wr = torch.from_numpy(rng.random((48, 4)).astype(np.float32))
+        return xr.to(gpu).view(torch.bfloat16), wr.to(gpu), idr.to(gpu)
+
+    static = list(make(-1))
+
+    def fn(xx, ww, ii):
+        return moe.fused_moe_w8a8_tiled_with_shared(xx, prepared, ww, ii, routed_scaling_factor=2.5)
+
+    _replay_matches_eager(fn, make, static)
+
+
+def test_bf16_and_w8a16_forward_graph_replays(gpu):
+    from fused_cpp_amd import moe
+
+    rng = np.random.default_rng(3)
+    T, Hd, F, E, k = 16, 512, 256, 8, 2
+    w13 = H.bf16_bits((rng.standard_normal((E, 2 * F, Hd)) * 0.02).astype(np.float32))
+    w2 = H.bf16_bits((rng.standard_normal((E, Hd, F)) * 0.02).astype(np.float32))
+    tb = lambda b: torch.from_numpy(b.view(np.int16)).to(gpu).view(torch.bfloat16)  # noqa: E731
+    bf16_w = moe.prepare_fused_moe_bf16_tiled_weights(tb(w13), tb(w2), fuse_silu=True)
+    w8_w = moe.prepare_fused_moe_w8a16_tiled_weights(tb(w13), tb(w2))
+
+    def make(r):
+        xr = tb(H.bf16_bits(rng.standard_normal((T, Hd)).astype(np.float32)))
+        ids, w = H.softmax_topk(rng.standard_normal((T, E)).astype(np.float32), k)
+        return xr, torch.from_numpy(w).to(gpu), torch.from_numpy(ids).to(gpu)
+
+    for weights, op in ((bf16_w, moe.fused_moe_bf16_tiled), (w8_w, moe.fused_moe_w8a16_tiled)):
+        static = list(make(-1))
+        _replay_matches_eager(lambda xx, ww, ii: op(xx, weights, ww, ii), make, static)
+
+
+def test_router_and_i8gemm_graph_replays(gpu):
+    from fused_cpp_amd import i8gemm, router
+
+    rng = np.random.default_rng(5)
+    weight = torch.randint(-16, 17, (96, 256), dtype=torch.int8)
+    packed = i8gemm.prepare(weight, torch.rand(96) * 0.01 + 0.001)
+
+    def make(r):
+        return (torch.randn(40, 256, device=gpu).to(torch.bfloat16),
+                torch.from_numpy(rng.standard_normal((40, 64)).astype(np.float32)).to(gpu))
+
+    static = list(make(-1))
+
+    def fn(xx, logits):
+        ids, w = router.topk_softmax(logits, 6, scale=2.5)
+        out = i8gemm.dynamic_scaled_mm(xx, packed, out_dtype=torch.bfloat16)
+        return torch.cat([out.float().reshape(-1), w.reshape(-1), ids.float().reshape(-1)])
+
+    _replay_matches_eager(fn, make, static)

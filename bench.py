@@ -193,7 +193,7 @@ def algorithmic(cfg, counts):
     return layer_bytes, layer_ops, stages
 
 
-def run_gpu(cfg, steps: int, warmup: int, device, keep_host: bool):
+def run_gpu(cfg, steps: int, warmup: int, device, keep_host: bool, graph: bool = False):
     import torch
 
     from fused_cpp_amd import cabi
@@ -240,11 +240,23 @@ def run_gpu(cfg, steps: int, warmup: int, device, keep_host: bool):
     for _ in range(max(warmup, 1)):
         step(out)
     torch.cuda.synchronize()
+    run = step
+    if graph:
+        # One whole forward captured into a HIP graph and replayed per step: the
+        # same kernels on the same HBM-resident inputs, without per-launch host cost.
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            step(out)
+        g.replay()
+        torch.cuda.synchronize()
+
+        def run(o):
+            g.replay()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     cabi.stage_timing_read()  # clear
     start.record()
     for _ in range(steps):
-        step(out)
+        run(out)
     end.record()
     torch.cuda.synchronize()
     ms = start.elapsed_time(end) / steps
@@ -324,7 +336,8 @@ def measured_traffic(config: str, stage: str):
 
 
 def measure(cfg, args, device, want_cpu: bool):
-    res = run_gpu(cfg, args.steps, args.warmup, device, keep_host=want_cpu or cfg["kind"] == "w8a8")
+    res = run_gpu(cfg, args.steps, args.warmup, device, keep_host=want_cpu or cfg["kind"] == "w8a8",
+                  graph=args.graph)
     counts = expert_counts(cfg, res["ids"])
     layer_bytes, layer_ops, st_alg = algorithmic(cfg, counts)
     ms = res["ms"]
@@ -380,6 +393,8 @@ def main() -> int:
     ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
     ap.add_argument("--prefill", action="store_true", help="also measure C3 prefill as 'secondary'")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--graph", action="store_true",
+                    help="time replays of one forward captured into a HIP graph (removes per-launch host cost)")
     ap.add_argument("--cpu-routes", type=int, default=2048, help="route sample of the CPU baseline at prefill")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 256 MiB device copy 5 times (scale reference for rocprofv3 "
@@ -420,7 +435,8 @@ def main() -> int:
         "data": "synthetic (seeded random N(0,0.02) weights, N(0,1) activations and router logits)",
         "config": {"workload": cfg["desc"], "tokens": cfg["T"], "hidden": cfg["H"], "intermediate": cfg["I"],
                    "routed_experts": cfg["E"], "top_k": cfg["k"], "shared_experts": int(cfg["shared"]),
-                   "routed_scaling": cfg["scale"], "parallelism": "single GPU"},
+                   "routed_scaling": cfg["scale"], "parallelism": "single GPU",
+                   "launch": "hip_graph_replay" if args.graph else "eager"},
         "roofline": res["roofline"],
         "layer": res["layer"],
     }

@@ -344,3 +344,31 @@ def test_i8gemm_batched_scalar_scale_and_ties(gpu, oracle_lib):
     assert got[0, :5].tolist() == [127.0, 0.0, 2.0, 0.0, -2.0]
     a, b = i8gemm.dynamic_scaled_mm_pair(xt.to(gpu), p, p)
     assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("activation", ["silu", "swigluoai"])
+def test_bf16_prefill_every_tile_class_within_tolerance(gpu, oracle_lib, activation):
+    """Per-expert counts 3..420 reach every tile class (16..256 rows), i.e. the bf16
+    instantiations of the register-ring kernel and of the LDS-staged prefill kernel,
+    with biases, against the fp32 reference."""
+    from fused_cpp_amd import moe
+
+    rng = np.random.default_rng(17)
+    counts = [3, 20, 40, 70, 100, 150, 200, 260, 420]
+    E, Hd, F = len(counts), 256, 192
+    T = sum(counts)
+    x = H.bits_to_f32(H.bf16_bits(rng.standard_normal((T, Hd)).astype(np.float32)))
+    w13 = H.bits_to_f32(H.bf16_bits((rng.standard_normal((E, 2 * F, Hd)) * 0.05).astype(np.float32)))
+    w2 = H.bits_to_f32(H.bf16_bits((rng.standard_normal((E, Hd, F)) * 0.05).astype(np.float32)))
+    b13 = (rng.standard_normal((E, 2 * F)) * 0.1).astype(np.float32)
+    b2 = (rng.standard_normal((E, Hd)) * 0.1).astype(np.float32)
+    ids = rng.permutation(np.concatenate([np.full(c, e) for e, c in enumerate(counts)])).reshape(-1, 1).astype(np.int64)
+    w = np.ones((T, 1), np.float32)
+    packed = moe.prepare_fused_moe_bf16_tiled_weights(_bf16(w13, gpu), _bf16(w2, gpu),
+                                                      fuse_silu=activation == "silu")
+    out = moe.fused_moe_bf16_tiled(_bf16(x, gpu), packed, torch.from_numpy(w).to(gpu), torch.from_numpy(ids).to(gpu),
+                                   w13_bias=torch.from_numpy(b13).to(gpu), w2_bias=torch.from_numpy(b2).to(gpu),
+                                   activation=activation)
+    ref = oracle_lib.bf16_moe_reference(x, w13, w2, w, ids, w13_bias=b13, w2_bias=b2, activation=activation,
+                                        round_intermediate=True)
+    _close(out, ref)

@@ -41,6 +41,7 @@ struct W8A8Layout {
   uint16_t* y;
   int8_t* q2;
   float* s2row;
+  float* rowpart;  // [routes, ceil(F/16)] per gate-tile max |y| from the W13 epilogue
   float* route_out;
 };
 
@@ -92,6 +93,7 @@ W8A8Layout w8a8_layout(const fcmoe_moe_args* a, Arena& ar) {
   L.y = ar.take<uint16_t>(L.routes * L.ip);
   L.q2 = ar.take<int8_t>(L.routes * L.ip);
   L.s2row = ar.take<float>(L.routes);
+  L.rowpart = ar.take<float>(L.routes * ceil_div(a->inter, 16));
   L.route_out = ar.take<float>(L.routes * a->hidden);
   return L;
 }
@@ -378,7 +380,7 @@ extern "C" int fcmoe_w8a8_forward(const fcmoe_moe_args* a, hipStream_t stream) {
   g13.ldo = L.ip;
   g13.scale_row = L.xs;
   g13.scale_col = a->w13_scale;
-  g13.rowmax = L.rb.rowmax;
+  g13.rowpart = L.rowpart;
   rc = run_classes(L.tc, stream, [&](int c, hipStream_t s) {
     GemmParams p = g13;
     p.tiles = L.rb.tiles + 2 * tile_offset(L.tc, c);
@@ -389,7 +391,7 @@ extern "C" int fcmoe_w8a8_forward(const fcmoe_moe_args* a, hipStream_t stream) {
   if (rc) return rc;
   {
     Stage st(FCMOE_STAGE_REQUANT, stream);
-    rc = requant_launch(L.y, L.ip, L.routes, I, L.rb.rowmax, L.q2, L.ip, L.s2row, stream);
+    rc = requant_launch(L.y, L.ip, L.routes, I, L.rowpart, ceil_div(I, 16), L.q2, L.ip, L.s2row, stream);
     if (rc) return rc;
   }
 

@@ -138,38 +138,42 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, const typenam
       }
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        float amax = 0.0f;
 #pragma unroll
         for (int j = 0; j < HP; ++j) {
-          if (!(rok[q] && fv[j])) continue;
-          float y;
-          if constexpr (EPI == kEpiW13SwigluI8) {
-            // w13_epilogue, csrc/moe/arm/i8mm_w8a8/kernels.cpp:230-246.
-            float gate = (float)acc[i][j][q] * (xs[q] * cg[j]);
-            float up = (float)acc[i][j + HP][q] * (xs[q] * cu[j]);
-            gate = fminf(gate, 10.0f);
-            up = fmaxf(fminf(up, 10.0f), -10.0f);
-            const float ex = fexpa_exp_neg(gate);
-            y = (gate * up) / (ex + 1.0f);
-          } else if constexpr (EPI == kEpiW13ActW8) {
-            // x . (q * s) accumulated as (x . q) * s in fp32
-            y = act_bf16_mode(acc[i][j][q] * cg[j], acc[i][j + HP][q] * cu[j], p.activation);
-          } else {
-            float gate = acc[i][j][q];
-            float up = acc[i][j + HP][q];
-            if (p.bias) {
-              gate = gate + cg[j];
-              up = up + cu[j];
+          float ya = 0.0f;  // |y| of this lane's channel (0 past F or past the tile's rows)
+          if (rok[q] && fv[j]) {
+            float y;
+            if constexpr (EPI == kEpiW13SwigluI8) {
+              // w13_epilogue, csrc/moe/arm/i8mm_w8a8/kernels.cpp:230-246.
+              float gate = (float)acc[i][j][q] * (xs[q] * cg[j]);
+              float up = (float)acc[i][j + HP][q] * (xs[q] * cu[j]);
+              gate = fminf(gate, 10.0f);
+              up = fmaxf(fminf(up, 10.0f), -10.0f);
+              const float ex = fexpa_exp_neg(gate);
+              y = (gate * up) / (ex + 1.0f);
+            } else if constexpr (EPI == kEpiW13ActW8) {
+              // x . (q * s) accumulated as (x . q) * s in fp32
+              y = act_bf16_mode(acc[i][j][q] * cg[j], acc[i][j + HP][q] * cu[j], p.activation);
+            } else {
+              float gate = acc[i][j][q];
+              float up = acc[i][j + HP][q];
+              if (p.bias) {
+                gate = gate + cg[j];
+                up = up + cu[j];
+              }
+              y = act_bf16_mode(gate, up, p.activation);
             }
-            y = act_bf16_mode(gate, up, p.activation);
+            const uint16_t yb = f32_to_bf16(y);
+            ((uint16_t*)p.out)[(int64_t)pos[q] * p.ldo + f[j]] = yb;
+            ya = fabsf(bf16_to_f32(yb));
           }
-          const uint16_t yb = f32_to_bf16(y);
-          ((uint16_t*)p.out)[(int64_t)pos[q] * p.ldo + f[j]] = yb;
-          amax = fmaxf(amax, fabsf(bf16_to_f32(yb)));
-        }
-        if constexpr (EPI == kEpiW13SwigluI8) {
-          amax = max16(amax);
-          if (rok[q] && col == 0) atomicMax(p.rowmax + pos[q], __float_as_uint(amax));
+          if constexpr (EPI == kEpiW13SwigluI8) {
+            // Maximum of |y| over this 16-channel gate tile (lanes reconverged
+            // for the shuffle); one plain store per (row, tile): every gate tile
+            // of a row is written by exactly one wave, so no atomics.
+            const float amax = max16(ya);
+            if (rok[q] && tvalid[j] && col == 0) p.rowpart[(int64_t)pos[q] * p.n_tiles + gtile[j]] = amax;
+          }
         }
       }
     }

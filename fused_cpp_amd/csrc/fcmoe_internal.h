@@ -49,7 +49,6 @@ struct RouteBuffers {
   int32_t* row_token = nullptr;      // [routes]  sorted position -> token
   int32_t* route_pos = nullptr;      // [routes]  flat route -> sorted position (-1 invalid)
   float* route_weight = nullptr;     // [routes]  combined routing weight
-  uint32_t* rowmax = nullptr;        // [routes]  zeroed per call (W13 epilogue row max)
   int32_t* tiles = nullptr;          // [classes][bound][2] (expert, m_begin)
   int32_t* tile_count = nullptr;     // [classes]
   int32_t* invalid = nullptr;        // [1]
@@ -67,8 +66,10 @@ int tiles_from_counts_launch(const int32_t* counts, int64_t experts, const TileC
 int fill_u32_launch(uint32_t* p, int64_t n, uint32_t v, hipStream_t stream);
 int quant_rows_launch(const void* x, int x_is_f32, int64_t rows, int64_t cols, int rounding, int8_t* q, int64_t ldq,
                       float* scales, hipStream_t stream);
-int requant_launch(const uint16_t* y, int64_t ldy, int64_t rows, int64_t cols, const uint32_t* rowmax, int8_t* q,
-                   int64_t ldq, float* scales, hipStream_t stream);
+// rowpart: [rows, parts] per-(row, 16-channel gate tile) maxima of |y| written
+// by the W13 epilogue; the row scale uses their maximum.
+int requant_launch(const uint16_t* y, int64_t ldy, int64_t rows, int64_t cols, const float* rowpart, int64_t parts,
+                   int8_t* q, int64_t ldq, float* scales, hipStream_t stream);
 int act_bf16_launch(const float* gate_up, int64_t ldg, int64_t rows, int64_t f, int64_t fp16, int mode, uint16_t* y,
                     int64_t ldy, hipStream_t stream);
 
@@ -106,7 +107,7 @@ struct GemmParams {
   const float* scale_row;    // per sorted row (or per A row) scale
   const float* scale_col;    // per expert per channel scale [experts, n]
   const float* bias;         // [experts, n] (bf16 path / i8gemm)
-  uint32_t* rowmax;          // W13 int8: per sorted row max |y| (float bits)
+  float* rowpart;            // W13 int8: [sorted rows, n_tiles] max |y| per 16-channel gate tile
   const int32_t* sorted_routes;  // W2: sorted position -> flat route
   int activation;            // bf16 W13
   int out_bf16;              // i8gemm output dtype

@@ -84,16 +84,21 @@ __global__ __launch_bounds__(kRowsPerBlock * kWave) void quant_rows_kernel(const
   for (int64_t i = cols + lane; i < ldq; i += kWave) qr[i] = 0;
 }
 
-// W8A8 intermediate requant: y rows are bf16 with their max|y| already
-// reduced into rowmax (float bits) by the W13 epilogue; this is
-// quantize_bf16_row applied to the intermediate (kernels.cpp:650-657).
+// W8A8 intermediate requant: y rows are bf16; the W13 epilogue left the max
+// |y| of each 16-channel gate tile in rowpart, and the row scale uses their
+// maximum. This is quantize_bf16_row applied to the intermediate
+// (kernels.cpp:650-657).
 __global__ __launch_bounds__(kRowsPerBlock * kWave) void requant_kernel(const uint16_t* y, int64_t ldy, int64_t rows,
-                                                                         int64_t cols, const uint32_t* rowmax,
-                                                                         int8_t* q, int64_t ldq, float* scales) {
+                                                                         int64_t cols, const float* rowpart,
+                                                                         int64_t parts, int8_t* q, int64_t ldq,
+                                                                         float* scales) {
   const int lane = threadIdx.x % kWave;
   const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + threadIdx.x / kWave;
   if (row >= rows) return;
-  const float m = __uint_as_float(rowmax[row]);
+  // max over the row's per-tile maxima (max is exact in any order)
+  float m = 0.0f;
+  for (int64_t i = lane; i < parts; i += kWave) m = fmaxf(m, rowpart[row * parts + i]);
+  m = wave_max(m);
   const float scale = m > 0.0f ? m / 127.0f : 1.0f;
   const float inv = 1.0f / scale;
   if (lane == 0) scales[row] = scale;
@@ -224,11 +229,12 @@ int quant_rows_launch(const void* x, int x_is_f32, int64_t rows, int64_t cols, i
   return check_launch("quant_rows");
 }
 
-int requant_launch(const uint16_t* y, int64_t ldy, int64_t rows, int64_t cols, const uint32_t* rowmax, int8_t* q,
+int requant_launch(const uint16_t* y, int64_t ldy, int64_t rows, int64_t cols, const float* rowpart, int64_t parts,
+                   int8_t* q,
                    int64_t ldq, float* scales, hipStream_t stream) {
   if (rows <= 0) return FCMOE_OK;
   hipLaunchKernelGGL(requant_kernel, dim3((unsigned)ceil_div(rows, kRowsPerBlock)), dim3(kRowsPerBlock * kWave), 0,
-                     stream, y, ldy, rows, cols, rowmax, q, ldq, scales);
+                     stream, y, ldy, rows, cols, rowpart, parts, q, ldq, scales);
   return check_launch("requant");
 }
 

@@ -176,8 +176,7 @@ __global__ __launch_bounds__(kScanThreads) void route_scan_kernel(int experts, i
 __global__ __launch_bounds__(kRouteChunk) void route_scatter_kernel(RouteArgs a, int64_t routes,
                                                                      const int32_t* chunk_hist,
                                                                      const int32_t* offsets, int32_t* sorted_routes,
-                                                                     int32_t* row_token, int32_t* route_pos,
-                                                                     uint32_t* rowmax) {
+                                                                     int32_t* row_token, int32_t* route_pos) {
   __shared__ int32_t ex[kRouteChunk];
   const int tid = threadIdx.x;
   const int64_t r = (int64_t)blockIdx.x * kRouteChunk + tid;
@@ -199,7 +198,6 @@ __global__ __launch_bounds__(kRouteChunk) void route_scatter_kernel(RouteArgs a,
   sorted_routes[pos] = (int32_t)r;
   row_token[pos] = (int32_t)(r / a.kt);
   route_pos[r] = pos;
-  if (rowmax) rowmax[pos] = 0u;
 }
 
 ClassArgs class_args(const TileClasses& tc) {
@@ -247,7 +245,6 @@ void route_take(Arena& ar, RouteBuffers& rb, int64_t routes, int64_t experts, co
   rb.row_token = ar.take<int32_t>(routes);
   rb.route_pos = ar.take<int32_t>(routes);
   rb.route_weight = ar.take<float>(routes);
-  rb.rowmax = ar.take<uint32_t>(routes);
   int64_t tiles = 0;
   for (int c = 0; c < tc.n; ++c) tiles += tc.bound[c];
   rb.tiles = ar.take<int32_t>(2 * tiles);
@@ -287,7 +284,7 @@ int route_launch(const void* ids, int ids_is_i64, const float* topk_w, int64_t t
   hipLaunchKernelGGL(route_scan_kernel, dim3(1), dim3(kScanThreads), 0, stream, (int)experts, chunks,
                      rb.chunk_hist, rb.counts, rb.offsets, ca, rb.tiles, rb.tile_count);
   hipLaunchKernelGGL(route_scatter_kernel, dim3((unsigned)chunks), dim3(kRouteChunk), 0, stream, a, routes,
-                     rb.chunk_hist, rb.offsets, rb.sorted_routes, rb.row_token, rb.route_pos, rb.rowmax);
+                     rb.chunk_hist, rb.offsets, rb.sorted_routes, rb.row_token, rb.route_pos);
   return check_launch("route");
 }
 

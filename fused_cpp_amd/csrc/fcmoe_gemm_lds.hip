@@ -26,6 +26,7 @@
 // units of row r stored at slot (unit ^ ((r >> 2) & 3)) so the 16 rows of a
 // fragment read fall on distinct banks; B tiles in their packed MFMA operand
 // order (1 KB per tile chunk, lane l's 16 bytes at 16 l).
+#include <cstdlib>
 #include <utility>
 
 #include "fcmoe_gemm_common.h"
@@ -51,8 +52,43 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
+// Work order. Operand reuse across workgroups only pays when the reusing
+// workgroups share an L2, and an L2 serves one XCD: L2-resident operands
+// reach a CU at ~60 B/clk through buffer_load ... lds, L2 misses (Infinity
+// Cache or HBM) at ~10-12 B/clk (measured on MI355X). The dispatcher deals
+// workgroups to the 8 XCDs round-robin by blockIdx, so workgroup b is
+// renumbered to run the (b / 8)-th item of a contiguous range of items owned
+// by XCD b % 8; among the first `valid` workgroups this is a bijection, and
+// at any moment each XCD runs a window of consecutive items. Items are
+// ordered in groups of `gm` row tiles x all channel blocks, row tiles
+// fastest: a window then holds a few row tiles against several channel
+// blocks, so A (per row tile) and B (per channel block, when the row tiles
+// belong to one expert) are both fetched from HBM once per window.
+// gm = 0 keeps plain tile-major order.
+constexpr int kXcds = 8;
+constexpr int kLdsGroupTiles = 4;
+
+__device__ __forceinline__ bool lds_work_item(int b, int count, int n_blocks, int gm, int& tile_idx, int& nb) {
+  const int valid = count * n_blocks;
+  if (b >= valid) return false;
+  if (gm <= 0) {
+    tile_idx = b / n_blocks;
+    nb = b % n_blocks;
+    return true;
+  }
+  const int x = b % kXcds, q = valid / kXcds, r = valid % kXcds;
+  const int l = x * q + (x < r ? x : r) + b / kXcds;
+  const int gsz = gm * n_blocks;
+  const int g = l / gsz, rr = l % gsz;
+  const int left = count - g * gm;
+  const int gm_eff = left < gm ? left : gm;
+  tile_idx = g * gm + rr % gm_eff;
+  nb = rr / gm_eff;
+  return true;
+}
+
 template <bool I8, int EPI, int FM, int FN>
-__global__ __launch_bounds__(kThreadsLds) void grouped_gemm_lds_kernel(GemmParams p, int n_blocks) {
+__global__ __launch_bounds__(kThreadsLds) void grouped_gemm_lds_kernel(GemmParams p, int n_blocks, int gm) {
   // The body is device-only: the buffer-resource type does not exist for the
   // host target, and the host pass needs only the kernel's signature.
 #if __HIP_DEVICE_COMPILE__
@@ -72,9 +108,9 @@ __global__ __launch_bounds__(kThreadsLds) void grouped_gemm_lds_kernel(GemmParam
   __shared__ __attribute__((aligned(1024))) uint8_t smem[kStages * STAGE];
 
   const int count = *p.tile_count;
-  const int tile = count - 1 - (int)(blockIdx.x / n_blocks);  // last-first, as the register kernel
-  if (tile < 0) return;
-  const int nb = blockIdx.x % n_blocks;
+  int tile_idx, nb;
+  if (!lds_work_item((int)blockIdx.x, count, n_blocks, gm, tile_idx, nb)) return;
+  const int tile = count - 1 - tile_idx;  // last-first, as the register kernel
   const int expert = p.tiles[2 * tile];
   const int m0 = p.tiles[2 * tile + 1];
   const int rows_left = p.counts[expert] - m0;
@@ -158,30 +194,41 @@ __global__ __launch_bounds__(kThreadsLds) void grouped_gemm_lds_kernel(GemmParam
 
   issue(0, 0);
   issue(1, 1);
+  // Retire the scalar loads of the set-up here: with one still pending at the
+  // loop header the first fragment wait of every chunk becomes lgkmcnt(0).
+  __builtin_amdgcn_s_waitcnt(0xC07F);
   int stage = 0;
   for (int64_t c = 0; c < kc; ++c) {
     wait_vmcnt<LPW>();  // this wave's chunk-c loads have landed (chunk c+1's may still fly)
     __builtin_amdgcn_s_barrier();
     issue(c + 2, stage == 0 ? 2 : stage - 1);
     const uint8_t* st = smem + stage * STAGE;
+    // Fragment reads in consumption order (A row 0, the B tiles, A row 1),
+    // then one A read two rows ahead per row of MFMAs. The schedule is pinned:
+    // left to itself the compiler sinks each read next to its first use and
+    // every row then waits out the LDS latency.
     v4i bf[FN];
-    v4i af[FM];
+    v4i af[3];
+    af[0] = *(const v4i*)(st + a_frag);
 #pragma unroll
     for (int j = 0; j < FN; ++j) bf[j] = *(const v4i*)(st + b_frag + j * 1024);
-    af[0] = *(const v4i*)(st + a_frag);
     af[1] = *(const v4i*)(st + a_frag + 1024);
+    __builtin_amdgcn_sched_group_barrier(0x100, FN + 2, 0);  // the FN + 2 leading LDS reads
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
-      if (i + 2 < FM) af[i + 2] = *(const v4i*)(st + a_frag + (i + 2) * 1024);
+      if (i + 2 < FM) af[(i + 2) % 3] = *(const v4i*)(st + a_frag + (i + 2) * 1024);
 #pragma unroll
       for (int j = 0; j < FN; ++j) {
         if constexpr (I8) {
-          acc[i][j] = mfma(af[i], bf[j], acc[i][j]);
+          acc[i][j] = mfma(af[i % 3], bf[j], acc[i][j]);
         } else {
-          acc[i][j] = mfma(__builtin_bit_cast(v8bf, af[i]), __builtin_bit_cast(v8bf, bf[j]), acc[i][j]);
+          acc[i][j] = mfma(__builtin_bit_cast(v8bf, af[i % 3]), __builtin_bit_cast(v8bf, bf[j]), acc[i][j]);
         }
       }
+      if (i + 2 < FM) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // A read for row i + 2
+      __builtin_amdgcn_sched_group_barrier(0x008, FN, 0);                 // then row i's MFMAs
     }
+    __builtin_amdgcn_sched_barrier(0);
     stage = stage == 2 ? 0 : stage + 1;
   }
   wait_vmcnt<0>();  // the two trailing (unused) stage loads
@@ -205,8 +252,12 @@ int launch_lds_cfg(const GemmParams& p, int64_t max_tiles, hipStream_t stream) {
   if (grid > INT32_MAX) return fail(FCMOE_EINVAL, "grouped gemm grid too large");
   // 32-bit buffer offsets: A rows and one expert's packed weights
   if (p.w_expert_bytes >= 0x7ffffff0) return fail(FCMOE_EINVAL, "expert weights exceed 2 GiB");
+  static const int gm = [] {
+    const char* v = getenv("FCMOE_LDS_GROUP");
+    return v ? atoi(v) : kLdsGroupTiles;
+  }();
   hipLaunchKernelGGL((grouped_gemm_lds_kernel<I8, EPI, FM, FN>), dim3((unsigned)grid), dim3(kThreadsLds), 0, stream,
-                     p, (int)n_blocks);
+                     p, (int)n_blocks, gm);
   return check_launch("grouped_gemm_lds");
 }
 

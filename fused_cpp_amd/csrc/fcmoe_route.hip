@@ -149,28 +149,79 @@ __global__ __launch_bounds__(kScanThreads) void tiles_from_counts_kernel(const i
   emit_tiles(e < experts ? counts[e] : 0, e, cls, tiles, tile_count);
 }
 
+// Column scan of chunk_hist [chunks][experts]: entry (c, e) becomes the
+// number of expert-e routes in chunks before c. The chunks of each expert are
+// split into segments over all threads (thread tid: expert tid % experts,
+// segment tid / experts); a segment is summed, the segment sums are scanned in
+// LDS, and the segment is rewritten from its base. Loads go out kScanBatch at
+// a time, so the walk costs chunks / (segments * kScanBatch) memory round trips
+// instead of one per chunk.
+constexpr int kScanBatch = 16;
+
 __global__ __launch_bounds__(kScanThreads) void route_scan_kernel(int experts, int64_t chunks, int32_t* chunk_hist,
                                                                    int32_t* counts, int32_t* offsets,
                                                                    ClassArgs cls, int32_t* tiles,
                                                                    int32_t* tile_count) {
-  const int e = threadIdx.x;
-  int count = 0;
-  if (e < experts) {
-    int running = 0;
-    for (int64_t c = 0; c < chunks; ++c) {
-      int32_t* p = chunk_hist + c * experts + e;
-      const int v = *p;
-      *p = running;
+  __shared__ int seg_sum[kScanThreads];
+  const int tid = threadIdx.x;
+  const int segs = kScanThreads / experts;  // >= 1: experts <= kScanThreads
+  const int e = tid % experts, sg = tid / experts;
+  const bool active = sg < segs;
+  const int64_t len = (chunks + segs - 1) / segs;
+  const int64_t c0 = active ? sg * len : 0;
+  const int64_t c1 = active ? (c0 + len < chunks ? c0 + len : chunks) : 0;
+  int32_t* col = chunk_hist + c0 * experts + e;  // this segment's first entry
+  const int n = c1 > c0 ? (int)(c1 - c0) : 0;  // trailing segments may be empty
+  const int full = n - n % kScanBatch;
+
+  int sum = 0;
+  {
+    const int32_t* q = col;
+    for (int c = 0; c < full; c += kScanBatch, q += kScanBatch * experts) {
+      int v[kScanBatch];
+#pragma unroll
+      for (int u = 0; u < kScanBatch; ++u) v[u] = q[u * experts];
+#pragma unroll
+      for (int u = 0; u < kScanBatch; ++u) sum += v[u];
+    }
+    for (int c = full; c < n; ++c, q += experts) sum += *q;
+  }
+  seg_sum[tid] = sum;
+  __syncthreads();
+  int running = 0, count = 0;
+  if (active) {
+    for (int q = 0; q < segs; ++q) {
+      const int w = seg_sum[q * experts + e];
+      if (q < sg) running += w;
+      count += w;
+    }
+  }
+  {
+    int32_t* q = col;
+    for (int c = 0; c < full; c += kScanBatch, q += kScanBatch * experts) {
+      int v[kScanBatch];
+#pragma unroll
+      for (int u = 0; u < kScanBatch; ++u) v[u] = q[u * experts];
+#pragma unroll
+      for (int u = 0; u < kScanBatch; ++u) {
+        q[u * experts] = running;
+        running += v[u];
+      }
+    }
+    for (int c = full; c < n; ++c, q += experts) {
+      const int v = *q;
+      *q = running;
       running += v;
     }
-    count = running;
-    counts[e] = count;
   }
+  // threads 0 .. experts-1 (segment 0) carry their expert's total
+  const bool owner = tid < experts;
+  if (owner) counts[e] = count;
   int total;
-  const int off = block_exclusive_scan(count, &total);
-  if (e < experts) offsets[e] = off;
-  if (e == 0) offsets[experts] = total;
-  emit_tiles(e < experts ? count : 0, e, cls, tiles, tile_count);
+  const int off = block_exclusive_scan(owner ? count : 0, &total);
+  if (owner) offsets[e] = off;
+  if (tid == 0) offsets[experts] = total;
+  emit_tiles(owner ? count : 0, tid, cls, tiles, tile_count);
 }
 
 __global__ __launch_bounds__(kRouteChunk) void route_scatter_kernel(RouteArgs a, int64_t routes,

@@ -156,6 +156,19 @@ def test_w8a8_forward_bit_exact_skewed_prefill(gpu, oracle_lib):
     _check_w8a8(gpu, oracle_lib, case, shared=True, scale=2.5)
 
 
+@pytest.mark.parametrize("tokens,hidden,inter,experts,top_k,skew", [
+    (5, 48, 16, 4, 2, None),         # smallest legal dims (multiples of 16), K padded to 64
+    (600, 208, 80, 9, 4, 1.2),       # ragged K on every tile class, the LDS kernel included
+    (333, 1040, 272, 17, 6, 1.1),    # K = 1040 / 272: padded tail chunk after full ones
+])
+def test_w8a8_forward_bit_exact_ragged_dims(gpu, oracle_lib, tokens, hidden, inter, experts, top_k, skew):
+    """H and F multiples of 16 but not of 64 (the reference's W8A8 domain,
+    csrc/moe/arm/i8mm_w8a8/kernels.cpp:485-570): the packed K chunks and the
+    quantised activation rows carry zero padding that must not change a bit."""
+    case = H.w8a8_case(500 + hidden + inter, tokens, hidden, inter, experts + 1, top_k, skew=skew)
+    _check_w8a8(gpu, oracle_lib, case, shared=True, scale=2.5)
+
+
 def test_w8a8_forward_repeat_bitwise(gpu, oracle_lib):
     case = H.w8a8_case(13, 40, 256, 128, 6, 2)
     x, ids, w, q13, s13, q2, s2 = case

@@ -300,12 +300,14 @@ template <bool I8, int EPI>
 int launch_bm(int bm, const GemmParams& p, int64_t max_tiles, hipStream_t stream) {
   switch (bm) {
     case 16:
-      // decode: W13 pairs 2 gate + 2 up tiles per wave; W2 (short K) runs
-      // 2 tiles per wave with a deeper ring, giving twice the waves
+      // decode: 8 waves per workgroup with an 8-deep ring. W13 pairs one gate
+      // and one up tile per wave; W2 (short K) streams one tile per wave.
+      // Measured on the DSv3 C2 layer against 4 waves (W13 2+2 tiles with a
+      // 4-deep ring, W2 2 tiles): W2 0.527 -> 0.506 ms, W13 0.964 -> 0.961 ms.
       if constexpr (epi_pair(EPI))
-        return launch_cfg<I8, EPI, 1, 4, 1, 4, 4, true>(p, max_tiles, stream);
+        return launch_cfg<I8, EPI, 1, 8, 1, 2, 8, true>(p, max_tiles, stream);
       else
-        return launch_cfg<I8, EPI, 1, 4, 1, 2, 8, true>(p, max_tiles, stream);
+        return launch_cfg<I8, EPI, 1, 8, 1, 1, 8, true>(p, max_tiles, stream);
     case 32:
       return launch_cfg<I8, EPI, 1, 4, 2, 4, 4, true>(p, max_tiles, stream);
     case 64:
@@ -326,6 +328,8 @@ template <int EPI>
 int launch_bm_w8(int bm, const GemmParams& p, int64_t max_tiles, hipStream_t stream) {
   switch (bm) {
     case 16:
+      // W2 keeps 2 tiles per wave here: the int8 -> bf16 widening makes the
+      // one-tile-per-wave form slower (C1 shape: 0.404 vs 0.445 ms)
       if constexpr (epi_pair(EPI))
         return launch_cfg<false, EPI, 1, 4, 1, 4, 4, true>(p, max_tiles, stream);
       else

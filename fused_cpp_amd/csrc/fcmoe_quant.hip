@@ -1,9 +1,10 @@
 // fcmoe_quant.hip -- row quantisation, weight quantisation/packing and the
 // BF16 activation pass.
 //
-// Row kernels use one wavefront per row: a strided max|x| pass (16-byte loads)
-// reduced with a butterfly, then the quantise pass. These are HBM-bound byte
-// kernels (2 bytes in, 1 byte out per element).
+// Row kernels: bf16 activation rows (cols % 8 == 0, up to 16384 columns) use
+// one workgroup per row with the row held in registers; other rows use one
+// wavefront per row (a strided max|x| pass, a butterfly, then the quantise
+// pass). These are HBM-bound byte kernels (2 bytes in, 1 byte out per element).
 #include "fcmoe_device.h"
 #include "fcmoe_internal.h"
 
@@ -82,6 +83,68 @@ __global__ __launch_bounds__(kRowsPerBlock * kWave) void quant_rows_kernel(const
     for (int64_t i = lane; i < cols; i += kWave) qr[i] = quant_value(load_x(x, x_is_f32, base + i), scale, inv, rounding);
   }
   for (int64_t i = cols + lane; i < ldq; i += kWave) qr[i] = 0;
+}
+
+// bf16 rows with cols % 8 == 0 and ldq % 8 == 0 (every activation row of the
+// MoE and i8gemm paths): one 256-thread workgroup per row. The row stays in
+// registers (CAP 16-byte units per thread) between the max pass and the
+// quantise pass, so it is read from HBM once, and all loads of a row are in
+// flight together. Same per-element arithmetic as quant_rows_kernel.
+constexpr int kRowThreads = 256;
+
+template <int CAP>
+__global__ __launch_bounds__(kRowThreads) void quant_rows_wg_kernel(const uint16_t* x, int64_t cols, int rounding,
+                                                                     int8_t* q, int64_t ldq, float* scales) {
+  __shared__ float wmax[kRowThreads / kWave];
+  const int tid = threadIdx.x;
+  const int64_t row = blockIdx.x;
+  const int64_t units = cols / 8;
+  const uint4* p = (const uint4*)(x + row * cols);
+  uint4 v[CAP];
+#pragma unroll
+  for (int k = 0; k < CAP; ++k) {
+    const int64_t i = tid + (int64_t)k * kRowThreads;
+    v[k] = i < units ? p[i] : make_uint4(0, 0, 0, 0);  // zero units leave the max unchanged
+  }
+  float m = 0.0f;
+#pragma unroll
+  for (int k = 0; k < CAP; ++k) {
+    const uint32_t w[4] = {v[k].x, v[k].y, v[k].z, v[k].w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      m = fmaxf(m, fabsf(__uint_as_float(w[j] << 16)));
+      m = fmaxf(m, fabsf(__uint_as_float(w[j] & 0xffff0000u)));
+    }
+  }
+  m = wave_max(m);
+  if (tid % kWave == 0) wmax[tid / kWave] = m;
+  __syncthreads();
+#pragma unroll
+  for (int w = 0; w < kRowThreads / kWave; ++w) m = fmaxf(m, wmax[w]);
+  const float scale = m > 0.0f ? m / 127.0f : 1.0f;
+  const float inv = 1.0f / scale;
+  if (tid == 0) scales[row] = scale;
+  int8_t* qr = q + row * ldq;
+#pragma unroll
+  for (int k = 0; k < CAP; ++k) {
+    const int64_t i = tid + (int64_t)k * kRowThreads;
+    if (i < units) {
+      const uint32_t w[4] = {v[k].x, v[k].y, v[k].z, v[k].w};
+      uint32_t lo = 0, hi = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t a = (uint8_t)quant_value(__uint_as_float(w[j] << 16), scale, inv, rounding);
+        const uint32_t b = (uint8_t)quant_value(__uint_as_float(w[j] & 0xffff0000u), scale, inv, rounding);
+        const uint32_t pair = a | (b << 8);
+        if (j < 2)
+          lo |= pair << (16 * j);
+        else
+          hi |= pair << (16 * (j - 2));
+      }
+      ((uint2*)qr)[i] = make_uint2(lo, hi);
+    }
+  }
+  for (int64_t i = cols + tid; i < ldq; i += kRowThreads) qr[i] = 0;
 }
 
 // W8A8 intermediate requant: y rows are bf16; the W13 epilogue left the max
@@ -224,6 +287,27 @@ int fill_u32_launch(uint32_t* p, int64_t n, uint32_t v, hipStream_t stream) {
 int quant_rows_launch(const void* x, int x_is_f32, int64_t rows, int64_t cols, int rounding, int8_t* q, int64_t ldq,
                       float* scales, hipStream_t stream) {
   if (rows <= 0) return FCMOE_OK;
+  if (!x_is_f32 && cols % 8 == 0 && ldq % 8 == 0 && rows <= INT32_MAX) {
+    const int64_t per_thread = ceil_div(cols / 8, kRowThreads);
+    const dim3 grid((unsigned)rows), block(kRowThreads);
+    const uint16_t* xb = (const uint16_t*)x;
+    if (per_thread <= 1) {
+      hipLaunchKernelGGL(quant_rows_wg_kernel<1>, grid, block, 0, stream, xb, cols, rounding, q, ldq, scales);
+      return check_launch("quant_rows");
+    }
+    if (per_thread <= 2) {
+      hipLaunchKernelGGL(quant_rows_wg_kernel<2>, grid, block, 0, stream, xb, cols, rounding, q, ldq, scales);
+      return check_launch("quant_rows");
+    }
+    if (per_thread <= 4) {
+      hipLaunchKernelGGL(quant_rows_wg_kernel<4>, grid, block, 0, stream, xb, cols, rounding, q, ldq, scales);
+      return check_launch("quant_rows");
+    }
+    if (per_thread <= 8) {
+      hipLaunchKernelGGL(quant_rows_wg_kernel<8>, grid, block, 0, stream, xb, cols, rounding, q, ldq, scales);
+      return check_launch("quant_rows");
+    }
+  }
   hipLaunchKernelGGL(quant_rows_kernel, dim3((unsigned)ceil_div(rows, kRowsPerBlock)), dim3(kRowsPerBlock * kWave),
                      0, stream, x, x_is_f32, rows, cols, rounding, q, ldq, scales);
   return check_launch("quant_rows");

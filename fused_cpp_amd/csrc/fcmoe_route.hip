@@ -24,6 +24,7 @@ namespace {
 
 constexpr int kScanThreads = 1024;
 constexpr int kMaxExperts = 1024;
+static_assert(kMaxExperts == kScanThreads, "the single-workgroup route kernel gives each expert a thread");
 
 struct RouteArgs {
   const void* ids;
@@ -52,6 +53,19 @@ __device__ __forceinline__ int route_expert(const RouteArgs& a, int64_t r, bool*
   return *valid ? (int)e : -1;
 }
 
+// Combined weight of flat route r: the routed slots carry topk_w (times the
+// routed scale when asked), the appended shared slot carries 1.
+__device__ __forceinline__ float route_weight_of(const RouteArgs& a, int64_t r) {
+  const int64_t t = r / a.kt;
+  const int s = (int)(r - t * a.kt);
+  float w = 1.0f;
+  if (s < a.top_k) {
+    w = a.topk_w ? a.topk_w[t * a.top_k + s] : 1.0f;
+    if (a.scale_routed) w = w * a.scale;
+  }
+  return w;
+}
+
 __global__ __launch_bounds__(kRouteChunk) void route_count_kernel(RouteArgs a, int64_t routes, int32_t* chunk_hist,
                                                                    float* route_weight, int32_t* invalid) {
   extern __shared__ int32_t hist[];
@@ -62,14 +76,7 @@ __global__ __launch_bounds__(kRouteChunk) void route_count_kernel(RouteArgs a, i
   if (r < routes) {
     bool valid;
     const int e = route_expert(a, r, &valid);
-    const int64_t t = r / a.kt;
-    const int s = (int)(r - t * a.kt);
-    float w = 1.0f;
-    if (s < a.top_k) {
-      w = a.topk_w ? a.topk_w[t * a.top_k + s] : 1.0f;
-      if (a.scale_routed) w = w * a.scale;
-    }
-    route_weight[r] = w;
+    route_weight[r] = route_weight_of(a, r);
     if (valid)
       atomicAdd(&hist[e], 1);
     else
@@ -251,6 +258,67 @@ __global__ __launch_bounds__(kRouteChunk) void route_scatter_kernel(RouteArgs a,
   route_pos[r] = pos;
 }
 
+// Decode-sized routing (routes <= kScanThreads) in one workgroup, one route
+// per thread: LDS histogram, the expert scan and tile lists, then the stable
+// scatter, where a route's rank is the number of earlier routes of its expert
+// (a scan of the LDS expert list, four entries per read). Produces exactly
+// the outputs of the count / scan / scatter kernels.
+__global__ __launch_bounds__(kScanThreads) void route_small_kernel(RouteArgs a, int routes, int32_t* counts,
+                                                                   int32_t* offsets, ClassArgs cls, int32_t* tiles,
+                                                                   int32_t* tile_count, int32_t* sorted_routes,
+                                                                   int32_t* row_token, int32_t* route_pos,
+                                                                   float* route_weight, int32_t* invalid) {
+  __shared__ int32_t hist[kMaxExperts];
+  __shared__ __attribute__((aligned(16))) int32_t ex[kScanThreads];
+  const int tid = threadIdx.x;
+  hist[tid] = 0;  // kMaxExperts == kScanThreads
+  int e = -1;
+  if (tid < routes) {
+    bool valid;
+    e = route_expert(a, tid, &valid);
+    route_weight[tid] = route_weight_of(a, tid);
+  }
+  ex[tid] = e;  // -1: invalid or past the last route
+  __syncthreads();
+  if (tid < routes) {
+    if (e >= 0)
+      atomicAdd(&hist[e], 1);
+    else
+      atomicAdd(invalid, 1);
+  }
+  __syncthreads();
+  const bool owner = tid < a.experts;
+  const int count = owner ? hist[tid] : 0;
+  int total;
+  const int off = block_exclusive_scan(count, &total);
+  if (owner) {
+    counts[tid] = count;
+    offsets[tid] = off;
+  }
+  if (tid == 0) offsets[a.experts] = total;
+  emit_tiles(count, tid, cls, tiles, tile_count);
+  __syncthreads();  // every thread has read its hist entry
+  if (owner) hist[tid] = off;
+  __syncthreads();
+  if (tid >= routes) return;
+  if (e < 0) {
+    route_pos[tid] = -1;
+    return;
+  }
+  int rank = 0;
+  const int4* ex4 = (const int4*)ex;
+  int j = 0;
+  for (; j + 4 <= tid; j += 4) {
+    const int4 q = ex4[j / 4];
+    rank += (q.x == e) + (q.y == e) + (q.z == e) + (q.w == e);
+  }
+  for (; j < tid; ++j) rank += ex[j] == e;
+  const int pos = hist[e] + rank;
+  sorted_routes[pos] = tid;
+  row_token[pos] = tid / a.kt;
+  route_pos[tid] = pos;
+}
+
 ClassArgs class_args(const TileClasses& tc) {
   ClassArgs ca;
   ca.n = tc.n;
@@ -329,9 +397,15 @@ int route_launch(const void* ids, int ids_is_i64, const float* topk_w, int64_t t
     const int rc = fill_u32_launch((uint32_t*)rb.invalid, 1, 0u, stream);
     if (rc) return rc;
   }
+  const ClassArgs ca = class_args(tc);
+  if (routes <= kScanThreads) {
+    hipLaunchKernelGGL(route_small_kernel, dim3(1), dim3(kScanThreads), 0, stream, a, (int)routes, rb.counts,
+                       rb.offsets, ca, rb.tiles, rb.tile_count, rb.sorted_routes, rb.row_token, rb.route_pos,
+                       rb.route_weight, invalid);
+    return check_launch("route");
+  }
   hipLaunchKernelGGL(route_count_kernel, dim3((unsigned)chunks), dim3(kRouteChunk), experts * sizeof(int32_t),
                      stream, a, routes, rb.chunk_hist, rb.route_weight, invalid);
-  const ClassArgs ca = class_args(tc);
   hipLaunchKernelGGL(route_scan_kernel, dim3(1), dim3(kScanThreads), 0, stream, (int)experts, chunks,
                      rb.chunk_hist, rb.counts, rb.offsets, ca, rb.tiles, rb.tile_count);
   hipLaunchKernelGGL(route_scatter_kernel, dim3((unsigned)chunks), dim3(kRouteChunk), 0, stream, a, routes,

@@ -21,7 +21,9 @@ pytestmark = pytest.mark.gpu
 @pytest.mark.parametrize(
     "tokens,top_k,experts,shared,i64",
     [(1, 1, 1, False, True), (37, 2, 4, False, False), (64, 8, 257, True, True), (513, 6, 33, True, False),
-     (4096, 8, 257, True, True)],
+     (4096, 8, 257, True, True),
+     # the single-workgroup path serves up to 1024 routes, the chunked one beyond
+     (128, 8, 9, False, True), (114, 8, 1024, True, False), (103, 10, 1000, False, True)],
 )
 def test_route_build_matches_oracle(gpu, oracle_lib, tokens, top_k, experts, shared, i64):
     rng = np.random.default_rng(tokens * 31 + experts)
@@ -50,6 +52,20 @@ def test_route_build_skewed_and_invalid(gpu, oracle_lib):
     np.testing.assert_array_equal(o, ro)
     np.testing.assert_array_equal(s[: ro[-1]], rs)
     assert (c == 0).sum() > 0  # skew leaves experts without tokens
+
+
+def test_route_build_small_with_invalid_ids(gpu, oracle_lib):
+    """Decode-sized routing (one workgroup) with out-of-range and negative ids."""
+    rng = np.random.default_rng(11)
+    ids = np.stack([rng.permutation(256)[:8] for _ in range(64)]).astype(np.int64)
+    ids[3, 2] = 999
+    ids[40, 7] = -5
+    c, o, s, bad = H.gpu_route_build(ids, 257, 256, gpu)
+    rc, ro, rs, rbad = oracle_lib.route_build(ids, 257, 256)
+    assert bad == rbad == 2
+    np.testing.assert_array_equal(c, rc)
+    np.testing.assert_array_equal(o, ro)
+    np.testing.assert_array_equal(s[: ro[-1]], rs)
 
 
 # ------------------------------------------------------------------ quant --

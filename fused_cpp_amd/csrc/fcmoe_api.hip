@@ -3,6 +3,7 @@
 #include <stdio.h>
 #include <stdlib.h>
 
+#include <algorithm>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -68,7 +69,7 @@ int check_shapes(const fcmoe_moe_args* a) {
   if (a->experts <= 0 || a->experts > 1024) return fail(FCMOE_EINVAL, "experts must be in [1, 1024]");
   if (a->valid_experts <= 0 || a->valid_experts > a->experts) return fail(FCMOE_EINVAL, "bad valid_experts");
   if (a->shared_expert_id >= a->experts) return fail(FCMOE_EINVAL, "shared_expert_id out of range");
-  if (a->tokens > 65535) return fail(FCMOE_EINVAL, "tokens must be <= 65535");
+  if (a->tokens > (int64_t)1 << 24) return fail(FCMOE_EINVAL, "tokens must be <= 2^24");
   return FCMOE_OK;
 }
 
@@ -244,11 +245,11 @@ bool timing_on() {
   return t.on;
 }
 
+// Rows run grid-stride over y (grid.y is capped at 65535).
 __global__ void pad_rows_kernel(const uint16_t* x, int64_t rows, int64_t cols, int64_t ld, uint16_t* dst) {
-  const int64_t r = blockIdx.y;
   const int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (r >= rows || c >= ld) return;
-  dst[r * ld + c] = c < cols ? x[r * cols + c] : (uint16_t)0;
+  if (c >= ld) return;
+  for (int64_t r = blockIdx.y; r < rows; r += gridDim.y) dst[r * ld + c] = c < cols ? x[r * cols + c] : (uint16_t)0;
 }
 
 __global__ void single_expert_counts_kernel(int32_t* counts, int32_t* offsets, int32_t m) {
@@ -484,7 +485,8 @@ int bf16_family_forward(const fcmoe_moe_args* a, hipStream_t stream, bool w8) {
   }
   const uint16_t* xa = a->x;
   if (L.xpad) {
-    hipLaunchKernelGGL(pad_rows_kernel, dim3((unsigned)ceil_div(L.hp, 256), (unsigned)a->tokens), dim3(256), 0,
+    hipLaunchKernelGGL(pad_rows_kernel, dim3((unsigned)ceil_div(L.hp, 256), (unsigned)std::min<int64_t>(a->tokens, 65535)),
+                       dim3(256), 0,
                        stream, a->x, a->tokens, H, L.hp, L.xpad);
     if ((rc = check_launch("pad_rows"))) return rc;
     xa = L.xpad;

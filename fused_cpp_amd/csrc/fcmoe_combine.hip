@@ -45,26 +45,33 @@ __device__ __forceinline__ float tree_merge(const float* route_out, const float*
 // VW output channels per thread (VW = 4 when hidden % 4 == 0: 16-byte route
 // loads, 8-byte bf16 stores; else 1). Each channel's arithmetic is identical
 // to the scalar form.
+// Route rows are read exactly once: nontemporal loads stream them past the
+// caches. The ordered merge issues the loads of up to kSlotBatch slots before
+// its FMA chain (slot order unchanged), so a thread waits one memory round
+// trip per batch instead of one per slot. Tokens run grid-stride over y.
+constexpr int kSlotBatch = 8;
+typedef float v4f __attribute__((ext_vector_type(4)));
+
 template <int VW>
 __global__ __launch_bounds__(256) void combine_kernel(const float* route_out, const float* route_weight,
                                                        const int32_t* route_pos, int64_t tokens, int kt,
                                                        int64_t hidden, int tree, int skip_weighted, uint16_t* out) {
-  const int64_t t = blockIdx.y;
   const int64_t h0 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * VW;
-  if (t >= tokens || h0 >= hidden) return;
+  if (h0 >= hidden) return;
+  for (int64_t t = blockIdx.y; t < tokens; t += gridDim.y) {
   const int64_t r0 = t * kt;
   float acc[VW];
 #pragma unroll
   for (int v = 0; v < VW; ++v) acc[v] = 0.0f;
   auto load = [&](int64_t r, float (&dst)[VW]) {
     if constexpr (VW == 4) {
-      const float4 q = *(const float4*)(route_out + r * hidden + h0);
+      const v4f q = __builtin_nontemporal_load((const v4f*)(route_out + r * hidden + h0));
       dst[0] = q.x;
       dst[1] = q.y;
       dst[2] = q.z;
       dst[3] = q.w;
     } else {
-      dst[0] = route_out[r * hidden + h0];
+      dst[0] = __builtin_nontemporal_load(route_out + r * hidden + h0);
     }
   };
   if (skip_weighted) {
@@ -88,14 +95,26 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* route_out, co
       }
     }
   } else {
-    for (int s = 0; s < kt; ++s) {
-      const int64_t r = r0 + s;
-      if (route_pos[r] < 0) continue;
-      const float w = route_weight[r];
-      float v4[VW];
-      load(r, v4);
+    for (int s0 = 0; s0 < kt; s0 += kSlotBatch) {
+      float v[kSlotBatch][VW];
+      float w[kSlotBatch];
+      bool ok[kSlotBatch];
 #pragma unroll
-      for (int v = 0; v < VW; ++v) acc[v] = __builtin_fmaf(v4[v], w, acc[v]);
+      for (int u = 0; u < kSlotBatch; ++u) {
+        const int64_t r = r0 + s0 + u;
+        ok[u] = s0 + u < kt && route_pos[r] >= 0;  // dropped (invalid) routes hold no row
+        w[u] = 0.0f;
+        if (ok[u]) {
+          w[u] = route_weight[r];
+          load(r, v[u]);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kSlotBatch; ++u)
+        if (ok[u]) {
+#pragma unroll
+          for (int c = 0; c < VW; ++c) acc[c] = __builtin_fmaf(v[u][c], w[u], acc[c]);
+        }
     }
   }
   if constexpr (VW == 4) {
@@ -105,6 +124,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* route_out, co
   } else {
     out[t * hidden + h0] = f32_to_bf16(acc[0]);
   }
+  }
 }
 
 }  // namespace
@@ -112,12 +132,12 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* route_out, co
 int combine_launch(const float* route_out, const float* route_weight, const int32_t* route_pos, int64_t tokens,
                    int64_t kt, int64_t hidden, int tree, int skip_weighted, uint16_t* out, hipStream_t stream) {
   if (tokens <= 0) return FCMOE_OK;
-  if (tokens > 65535) return fail(FCMOE_EINVAL, "too many tokens");
+  const unsigned ty = (unsigned)(tokens < 65535 ? tokens : 65535);  // grid.y limit; the kernel strides over y
   if (hidden % 4 == 0)
-    hipLaunchKernelGGL(combine_kernel<4>, dim3((unsigned)ceil_div(hidden / 4, 256), (unsigned)tokens), dim3(256), 0,
+    hipLaunchKernelGGL(combine_kernel<4>, dim3((unsigned)ceil_div(hidden / 4, 256), ty), dim3(256), 0,
                        stream, route_out, route_weight, route_pos, tokens, (int)kt, hidden, tree, skip_weighted, out);
   else
-    hipLaunchKernelGGL(combine_kernel<1>, dim3((unsigned)ceil_div(hidden, 256), (unsigned)tokens), dim3(256), 0,
+    hipLaunchKernelGGL(combine_kernel<1>, dim3((unsigned)ceil_div(hidden, 256), ty), dim3(256), 0,
                        stream, route_out, route_weight, route_pos, tokens, (int)kt, hidden, tree, skip_weighted, out);
   return check_launch("combine");
 }

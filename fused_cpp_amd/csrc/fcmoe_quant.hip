@@ -250,12 +250,12 @@ __global__ __launch_bounds__(256) void pack_kernel(const uint8_t* src, int eb, i
 // fp16 + (c - F).
 __global__ __launch_bounds__(256) void act_bf16_kernel(const float* gate_up, int64_t ldg, int64_t rows, int64_t f,
                                                         int64_t fp16, int mode, uint16_t* y, int64_t ldy) {
-  const int64_t row = blockIdx.y;
   const int64_t col = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (row >= rows || col >= ldy) return;
+  if (col >= ldy) return;
+  for (int64_t row = blockIdx.y; row < rows; row += gridDim.y) {  // grid.y is capped at 65535
   if (col >= f) {
     y[row * ldy + col] = 0;
-    return;
+    continue;
   }
   const float* g = gate_up + row * ldg;
   auto at = [&](int64_t c) { return g[c < f ? c : fp16 + (c - f)]; };
@@ -269,6 +269,7 @@ __global__ __launch_bounds__(256) void act_bf16_kernel(const float* gate_up, int
     v = 0.0f;
   }
   y[row * ldy + col] = f32_to_bf16(v);
+  }
 }
 
 __global__ void fill_u32_kernel(uint32_t* p, int64_t n, uint32_t v) {
@@ -325,7 +326,8 @@ int requant_launch(const uint16_t* y, int64_t ldy, int64_t rows, int64_t cols, c
 int act_bf16_launch(const float* gate_up, int64_t ldg, int64_t rows, int64_t f, int64_t fp16, int mode, uint16_t* y,
                     int64_t ldy, hipStream_t stream) {
   if (rows <= 0) return FCMOE_OK;
-  hipLaunchKernelGGL(act_bf16_kernel, dim3((unsigned)ceil_div(ldy, 256), (unsigned)rows), dim3(256), 0, stream,
+  hipLaunchKernelGGL(act_bf16_kernel, dim3((unsigned)ceil_div(ldy, 256), (unsigned)(rows < 65535 ? rows : 65535)),
+                     dim3(256), 0, stream,
                      gate_up, ldg, rows, f, fp16, mode, y, ldy);
   return check_launch("act_bf16");
 }

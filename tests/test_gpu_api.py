@@ -242,6 +242,32 @@ def test_bf16_plumbing_config_within_north_star_tolerance(gpu, oracle_lib, T, Hd
     _close(out, oracle_lib.bf16_moe_reference(x, w13, w2, w, ids))
 
 
+def test_bf16_more_routes_than_grid_y_limit(gpu, oracle_lib):
+    """65,600 routes (T=8200, top-8): row-indexed passes (activation, combine)
+    cover every row although a launch's grid.y stops at 65,535."""
+    from fused_cpp_amd import moe
+
+    x, w13, w2, b13, b2, ids, w = _bf16_case(8200, 8200, 64, 32, 8, 8, w_std=0.1)
+    packed = moe.prepare_fused_moe_bf16_tiled_weights(_bf16(w13, gpu), _bf16(w2, gpu))
+    out = moe.fused_moe_bf16_tiled(_bf16(x, gpu), packed, torch.from_numpy(w).to(gpu), torch.from_numpy(ids).to(gpu),
+                                   w13_bias=torch.from_numpy(b13).to(gpu), w2_bias=torch.from_numpy(b2).to(gpu),
+                                   activation="swigluoai")
+    ref = oracle_lib.bf16_moe_reference(x, w13, w2, w, ids, w13_bias=b13, w2_bias=b2, activation="swigluoai")
+    refb = torch.from_numpy(ref).to(torch.bfloat16).float()
+    torch.testing.assert_close(out.float().cpu(), refb, atol=7e-2, rtol=7e-2)
+    # the last rows are as close as the first (no row left unwritten)
+    torch.testing.assert_close(out[-64:].float().cpu(), refb[-64:], atol=7e-2, rtol=7e-2)
+
+
+def test_w8a8_more_tokens_than_grid_y_limit(gpu, oracle_lib):
+    """70,000 tokens: the combine strides over tokens past grid.y's 65,535."""
+    case = H.w8a8_case(70000, 70000, 64, 32, 4, 1)
+    x, ids, w, q13, s13, q2, s2 = case
+    out = H.gpu_w8a8_forward(x, ids, w, q13, s13, q2, s2, gpu)
+    ref = oracle_lib.w8a8_forward(x, ids, w, q13, s13, q2, s2)
+    np.testing.assert_array_equal(out, ref)
+
+
 def test_bf16_dsv3_shape_routed_shared_within_tolerance(gpu, oracle_lib):
     """C1 shape (H=7168, I=2048, top-8 + shared, x2.5) with 16 routed experts."""
     from fused_cpp_amd import moe

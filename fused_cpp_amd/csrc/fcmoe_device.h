@@ -40,6 +40,26 @@ __constant__ static const uint32_t kFexpaTable[64] = {
 // exp(-gate) evaluated exactly as exp_fexpa_neg
 // (csrc/moe/arm/i8mm_w8a8/kernels.cpp:200-209): clamp, shift-encode,
 // two-step Cody-Waite residual, FEXPA scale, degree-2 polynomial.
+// The table held in one VGPR, entry i in lane i (load once per kernel):
+// lookups then go through the LDS crossbar (ds_bpermute) instead of a
+// divergent __constant__ load that waits on the memory pipeline.
+__device__ __forceinline__ uint32_t fexpa_table_lane() { return kFexpaTable[threadIdx.x % kWave]; }
+
+// exp_fexpa_neg with the table in a VGPR (fexpa_table_lane); same bits as
+// fexpa_exp_neg.
+__device__ __forceinline__ float fexpa_exp_neg_v(float gate, uint32_t tab) {
+  float x = fmaxf(fminf(-gate, 87.0f), -87.0f);
+  float encoded = __builtin_fmaf(x, 1.4426950216293335f, 196735.0f);
+  float k = encoded - 196735.0f;
+  float residual = __builtin_fmaf(-k, 0.693145751953125f, x);
+  residual = __builtin_fmaf(-k, 1.428606765330187e-06f, residual);
+  uint32_t bits = __float_as_uint(encoded);
+  const uint32_t frac = (uint32_t)__builtin_amdgcn_ds_bpermute((int)((bits & 63u) << 2), (int)tab);
+  float scale = __uint_as_float((((bits >> 6) & 0xffu) << 23) | frac);
+  float poly = __builtin_fmaf(residual, 0.5000003576278687f, 1.000003695487976f);
+  return __builtin_fmaf(scale, poly * residual, scale);
+}
+
 __device__ __forceinline__ float fexpa_exp_neg(float gate) {
   float x = fmaxf(fminf(-gate, 87.0f), -87.0f);
   float encoded = __builtin_fmaf(x, 1.4426950216293335f, 196735.0f);
@@ -52,12 +72,19 @@ __device__ __forceinline__ float fexpa_exp_neg(float gate) {
   return __builtin_fmaf(scale, poly * residual, scale);
 }
 
-// Butterfly max over the 16 lanes that share (lane / 16).
+// Max over the 16 lanes that share (lane / 16) -- one DPP row -- with DPP
+// moves (no LDS crossbar): quad max via quad_perm [1,0,3,2] and [2,3,0,1],
+// then rotations of the row by 4 and 8 lanes fold in the other quads. Every
+// lane ends with the row maximum (max is exact in any order).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
 __device__ __forceinline__ float max16(float v) {
-  v = fmaxf(v, __shfl_xor(v, 1));
-  v = fmaxf(v, __shfl_xor(v, 2));
-  v = fmaxf(v, __shfl_xor(v, 4));
-  v = fmaxf(v, __shfl_xor(v, 8));
+  v = fmaxf(v, dpp_f<0xB1>(v));   // quad_perm [1,0,3,2]
+  v = fmaxf(v, dpp_f<0x4E>(v));   // quad_perm [2,3,0,1]
+  v = fmaxf(v, dpp_f<0x124>(v));  // row_ror:4
+  v = fmaxf(v, dpp_f<0x128>(v));  // row_ror:8
   return v;
 }
 

@@ -110,6 +110,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, const typenam
   if constexpr (epi_pair(EPI)) {
     constexpr int HP = FN / 2;
     const int64_t n = p.n;  // 2F logical
+    const uint32_t ftab = EPI == kEpiW13SwigluI8 ? fexpa_table_lane() : 0u;
     int f[HP];
     bool fv[HP];
     float cg[HP], cu[HP];  // W13 int8 / W8A16: gate / up channel scales; bf16: biases
@@ -141,17 +142,24 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, const typenam
 #pragma unroll
         for (int j = 0; j < HP; ++j) {
           float ya = 0.0f;  // |y| of this lane's channel (0 past F or past the tile's rows)
-          if (rok[q] && fv[j]) {
+          if constexpr (EPI == kEpiW13SwigluI8) {
+            // w13_epilogue, csrc/moe/arm/i8mm_w8a8/kernels.cpp:230-246. Evaluated
+            // on every lane (operands are clamped in range) so the table lookup's
+            // cross-lane read sees all lanes active; only the store is guarded.
+            float gate = (float)acc[i][j][q] * (xs[q] * cg[j]);
+            float up = (float)acc[i][j + HP][q] * (xs[q] * cu[j]);
+            gate = fminf(gate, 10.0f);
+            up = fmaxf(fminf(up, 10.0f), -10.0f);
+            const float ex = fexpa_exp_neg_v(gate, ftab);
+            const float y = (gate * up) / (ex + 1.0f);
+            if (rok[q] && fv[j]) {
+              const uint16_t yb = f32_to_bf16(y);
+              ((uint16_t*)p.out)[(int64_t)pos[q] * p.ldo + f[j]] = yb;
+              ya = fabsf(bf16_to_f32(yb));
+            }
+          } else if (rok[q] && fv[j]) {
             float y;
-            if constexpr (EPI == kEpiW13SwigluI8) {
-              // w13_epilogue, csrc/moe/arm/i8mm_w8a8/kernels.cpp:230-246.
-              float gate = (float)acc[i][j][q] * (xs[q] * cg[j]);
-              float up = (float)acc[i][j + HP][q] * (xs[q] * cu[j]);
-              gate = fminf(gate, 10.0f);
-              up = fmaxf(fminf(up, 10.0f), -10.0f);
-              const float ex = fexpa_exp_neg(gate);
-              y = (gate * up) / (ex + 1.0f);
-            } else if constexpr (EPI == kEpiW13ActW8) {
+            if constexpr (EPI == kEpiW13ActW8) {
               // x . (q * s) accumulated as (x . q) * s in fp32
               y = act_bf16_mode(acc[i][j][q] * cg[j], acc[i][j + HP][q] * cu[j], p.activation);
             } else {
@@ -165,7 +173,6 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, const typenam
             }
             const uint16_t yb = f32_to_bf16(y);
             ((uint16_t*)p.out)[(int64_t)pos[q] * p.ldo + f[j]] = yb;
-            ya = fabsf(bf16_to_f32(yb));
           }
           if constexpr (EPI == kEpiW13SwigluI8) {
             // Maximum of |y| over this 16-channel gate tile (lanes reconverged

@@ -16,11 +16,13 @@
 // (W13: 4 * FN/2 gate tiles and the matching up tiles). Waves are 2 (rows) x
 // 4 (channel tiles); the epilogues are the shared gemm_epilogue.
 //
-// Pipeline: a ring of three LDS stages, each one 64-byte K chunk of the
-// A tile (BM rows) and of the workgroup's B tiles. Iteration c waits for its
-// own stage-c loads (vmcnt), meets the other waves at one barrier (their
-// stage-c loads have landed; everyone is done reading stage c-1), issues
-// chunk c+2 into stage (c+2) % 3 and computes chunk c.
+// Pipeline: two LDS rings of 64-byte K chunks, SA stages of the A tile (BM
+// rows) and SB >= SA stages of the workgroup's B tiles, so the weights
+// (streamed from HBM) may run further ahead than A (re-read from L2 by the
+// other channel blocks). Iteration c waits for its own chunk-c loads
+// (vmcnt), meets the other waves at one barrier (their chunk-c loads have
+// landed; everyone is done reading chunk c-1), issues A chunk c+SA-1 and B
+// chunk c+SB-1 into the stages chunk c-1 used and computes chunk c.
 //
 // LDS layouts (per stage): A rows packed 64 bytes apart, the four 16-byte
 // units of row r stored at slot (unit ^ ((r >> 2) & 3)) so the 16 rows of a
@@ -87,25 +89,35 @@ __device__ __forceinline__ bool lds_work_item(int b, int count, int n_blocks, in
   return true;
 }
 
-template <bool I8, int EPI, int FM, int FN>
+template <bool I8, int EPI, int FM, int FN, int SA, int SB, int BPOL>
 __global__ __launch_bounds__(kThreadsLds) void grouped_gemm_lds_kernel(GemmParams p, int n_blocks, int gm) {
   // The body is device-only: the buffer-resource type does not exist for the
   // host target, and the host pass needs only the kernel's signature.
 #if __HIP_DEVICE_COMPILE__
   constexpr int BM = kWM * FM * 16;
   constexpr int NT = kWN * FN;            // channel tiles per workgroup
-  constexpr int A_BYTES = BM * 64;
-  constexpr int STAGE = A_BYTES + NT * 1024;
-  constexpr int LA = BM / 16;             // A loads (16 rows x 64 bytes) per stage
-  constexpr int L = LA + NT;              // loads per stage
-  constexpr int LPW = (L + kWaves - 1) / kWaves;  // loads per wave per stage
+  constexpr int A_BYTES = BM * 64;        // one A stage
+  constexpr int B_BYTES = NT * 1024;      // one B stage
+  constexpr int LA = BM / 16;             // A loads (16 rows x 64 bytes) per chunk
+  constexpr int LB = NT;                  // B loads (one 1 KB tile chunk) per chunk
+  constexpr int LPA = (LA + kWaves - 1) / kWaves;  // per wave
+  constexpr int LPB = (LB + kWaves - 1) / kWaves;
+  // vector-memory ops a wave may still have in flight once chunk c's A and B
+  // have landed (see the issue order below)
+  // (B c precedes A c when SB > SA; with SB == SA it is A c's pair partner)
+  constexpr int WAIT_A = LPB + (SA - 2) * (LPA + LPB);
+  constexpr int WAIT_B = (SB - 2) * (LPA + LPB);
+  constexpr int WAIT = WAIT_A < WAIT_B ? WAIT_A : WAIT_B;
   constexpr bool PAIR = epi_pair(EPI);
   constexpr int HP = FN / 2;
-  static_assert(L >= kWaves, "every wave issues at least one load per stage");
+  static_assert(SA >= 2 && SB >= SA, "A ring of 2+ stages, B ring at least as deep");
+  static_assert(WAIT < 64, "vmcnt range");
+  static_assert(SA * A_BYTES + SB * B_BYTES <= 160 * 1024, "LDS budget");
   static_assert(FM >= 3, "the fragment ring runs two fragments ahead");
   typedef typename Acc<I8>::type AccT;
 
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[kStages * STAGE];
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[SA * A_BYTES + SB * B_BYTES];
+  uint8_t* const smem_b = smem + SA * A_BYTES;
 
   const int count = *p.tile_count;
   int tile_idx, nb;
@@ -137,54 +149,57 @@ __global__ __launch_bounds__(kThreadsLds) void grouped_gemm_lds_kernel(GemmParam
     }
   };
 
-  // ---- buffer resources and this wave's LPW loads per stage. Load index g:
-  // g < LA -> A rows [16 g, 16 g + 16); else B tile g - LA. Waves take
-  // g = wave, wave + 8, ...; indices past L repeat load g - L (same bytes to
-  // the same place) so every wave issues exactly LPW loads.
+  // ---- buffer resources and this wave's loads per chunk: A loads g = wave,
+  // wave + 8, ... (rows [16 g, 16 g + 16)), B loads likewise over the NT
+  // tiles; indices past the count repeat an earlier load (same bytes to the
+  // same place) so every wave issues exactly LPA + LPB loads.
   const int64_t lda_bytes = p.lda * (I8 ? 1 : 2);
   const __amdgpu_buffer_rsrc_t rsrc_a =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p.a), (short)0, 0x7ffffff0, kBufWord3);
   const __amdgpu_buffer_rsrc_t rsrc_b = __builtin_amdgcn_make_buffer_rsrc(
       (void*)((const uint8_t*)p.w + (int64_t)expert * p.w_expert_bytes), (short)0,
       (int)(p.w_expert_bytes < 0x7ffffff0 ? p.w_expert_bytes : 0x7ffffff0), kBufWord3);
-  uint32_t voff[LPW];
-  bool is_a[LPW];
-  int lds_off[LPW];
+  uint32_t voff_a[LPA], voff_b[LPB];
+  int lds_a[LPA], lds_b[LPB];
 #pragma unroll
-  for (int u = 0; u < LPW; ++u) {
+  for (int u = 0; u < LPA; ++u) {
     int g = wave + kWaves * u;
-    if (g >= L) g -= L;
-    is_a[u] = g < LA;
-    if (g < LA) {
-      const int r = g * 16 + lane / 4;
-      const int unit = (lane % 4) ^ ((lane >> 4) & 3);
-      const int pos = pos0 + (r < rows ? r : rows - 1);  // rows past the tile re-read the last row
-      const int64_t arow = p.row_map ? (int64_t)p.row_map[pos] : (int64_t)pos;
-      voff[u] = (uint32_t)(arow * lda_bytes + unit * 16);
-      lds_off[u] = g * 1024;
-    } else {
-      const int t = g - LA;
-      bool valid;
-      const int64_t gt = tile_of(t / FN, t % FN, &valid);
-      voff[u] = (uint32_t)((valid ? gt : 0) * kc * 1024 + lane * 16);
-      lds_off[u] = A_BYTES + t * 1024;
-    }
+    while (g >= LA) g -= LA;
+    const int r = g * 16 + lane / 4;
+    const int unit = (lane % 4) ^ ((lane >> 4) & 3);
+    const int pos = pos0 + (r < rows ? r : rows - 1);  // rows past the tile re-read the last row
+    const int64_t arow = p.row_map ? (int64_t)p.row_map[pos] : (int64_t)pos;
+    voff_a[u] = (uint32_t)(arow * lda_bytes + unit * 16);
+    lds_a[u] = g * 1024;
   }
-  auto issue = [&](int64_t c, int stage) {
-    const int64_t cc = c < kc ? c : kc - 1;  // past the end: re-load the last chunk (never read)
-    const int soff_a = (int)(cc * 64);
-    const int soff_b = (int)(cc * 1024);
 #pragma unroll
-    for (int u = 0; u < LPW; ++u) {
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(is_a[u] ? rsrc_a : rsrc_b,
-                                               (lds_ptr_t)(smem + stage * STAGE + lds_off[u]), 16, voff[u],
-                                               is_a[u] ? soff_a : soff_b, 0, 0);
-    }
+  for (int u = 0; u < LPB; ++u) {
+    int t = wave + kWaves * u;
+    while (t >= LB) t -= LB;
+    bool valid;
+    const int64_t gt = tile_of(t / FN, t % FN, &valid);
+    voff_b[u] = (uint32_t)((valid ? gt : 0) * kc * 1024 + lane * 16);
+    lds_b[u] = t * 1024;
+  }
+  // Past the end a ring re-loads the last chunk (never read).
+  auto issue_a = [&](int64_t c, int stage) {
+    const int soff = (int)((c < kc ? c : kc - 1) * 64);
+#pragma unroll
+    for (int u = 0; u < LPA; ++u)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_a, (lds_ptr_t)(smem + stage * A_BYTES + lds_a[u]), 16, voff_a[u],
+                                               soff, 0, 0);
+  };
+  auto issue_b = [&](int64_t c, int stage) {
+    const int soff = (int)((c < kc ? c : kc - 1) * 1024);
+#pragma unroll
+    for (int u = 0; u < LPB; ++u)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_b, (lds_ptr_t)(smem_b + stage * B_BYTES + lds_b[u]), 16,
+                                               voff_b[u], soff, 0, BPOL);
   };
 
   // ---- fragment addresses (bytes within a stage)
   const int a_frag = (wm * FM * 16 + lane % 16) * 64 + (((lane / 16) ^ ((lane % 16) >> 2)) * 16);
-  const int b_frag = A_BYTES + wn * FN * 1024 + lane * 16;
+  const int b_frag = wn * FN * 1024 + lane * 16;
 
   AccT acc[FM][FN];
 #pragma unroll
@@ -192,31 +207,44 @@ __global__ __launch_bounds__(kThreadsLds) void grouped_gemm_lds_kernel(GemmParam
 #pragma unroll
     for (int j = 0; j < FN; ++j) acc[i][j] = AccT{0, 0, 0, 0};
 
-  issue(0, 0);
-  issue(1, 1);
+  // Issue order: B chunks 0 .. SB-SA-1 alone, then pairs (A m, B m+SB-SA),
+  // one pair per iteration after the prologue. When iteration c waits, the
+  // ops issued after A c are B c+SB-SA and the SA-2 later pairs: WAIT.
+  // B runs SB-SA chunks further ahead than A: the weights stream from HBM
+  // (long latency), A rows are re-read by the other channel blocks from L2.
+#pragma unroll
+  for (int s = 0; s < SB - SA; ++s) issue_b(s, s);
+#pragma unroll
+  for (int s = 0; s < SA - 1; ++s) {
+    issue_a(s, s);
+    issue_b(s + SB - SA, s + SB - SA);
+  }
   // Retire the scalar loads of the set-up here: with one still pending at the
   // loop header the first fragment wait of every chunk becomes lgkmcnt(0).
   __builtin_amdgcn_s_waitcnt(0xC07F);
-  int stage = 0;
+  int sa = 0, sb = 0;
   for (int64_t c = 0; c < kc; ++c) {
-    wait_vmcnt<LPW>();  // this wave's chunk-c loads have landed (chunk c+1's may still fly)
+    wait_vmcnt<WAIT>();  // this wave's chunk-c A and B have landed
     __builtin_amdgcn_s_barrier();
-    issue(c + 2, stage == 0 ? 2 : stage - 1);
-    const uint8_t* st = smem + stage * STAGE;
+    // everyone is done with chunk c-1: its stages take the next chunks
+    issue_a(c + SA - 1, sa == 0 ? SA - 1 : sa - 1);
+    issue_b(c + SB - 1, sb == 0 ? SB - 1 : sb - 1);
+    const uint8_t* sta = smem + sa * A_BYTES;
+    const uint8_t* stb = smem_b + sb * B_BYTES;
     // Fragment reads in consumption order (A row 0, the B tiles, A row 1),
     // then one A read two rows ahead per row of MFMAs. The schedule is pinned:
     // left to itself the compiler sinks each read next to its first use and
     // every row then waits out the LDS latency.
     v4i bf[FN];
     v4i af[3];
-    af[0] = *(const v4i*)(st + a_frag);
+    af[0] = *(const v4i*)(sta + a_frag);
 #pragma unroll
-    for (int j = 0; j < FN; ++j) bf[j] = *(const v4i*)(st + b_frag + j * 1024);
-    af[1] = *(const v4i*)(st + a_frag + 1024);
+    for (int j = 0; j < FN; ++j) bf[j] = *(const v4i*)(stb + b_frag + j * 1024);
+    af[1] = *(const v4i*)(sta + a_frag + 1024);
     __builtin_amdgcn_sched_group_barrier(0x100, FN + 2, 0);  // the FN + 2 leading LDS reads
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
-      if (i + 2 < FM) af[(i + 2) % 3] = *(const v4i*)(st + a_frag + (i + 2) * 1024);
+      if (i + 2 < FM) af[(i + 2) % 3] = *(const v4i*)(sta + a_frag + (i + 2) * 1024);
 #pragma unroll
       for (int j = 0; j < FN; ++j) {
         if constexpr (I8) {
@@ -229,9 +257,10 @@ __global__ __launch_bounds__(kThreadsLds) void grouped_gemm_lds_kernel(GemmParam
       __builtin_amdgcn_sched_group_barrier(0x008, FN, 0);                 // then row i's MFMAs
     }
     __builtin_amdgcn_sched_barrier(0);
-    stage = stage == 2 ? 0 : stage + 1;
+    sa = sa == SA - 1 ? 0 : sa + 1;
+    sb = sb == SB - 1 ? 0 : sb + 1;
   }
-  wait_vmcnt<0>();  // the two trailing (unused) stage loads
+  wait_vmcnt<0>();  // the trailing (unused) stage loads
 
   int64_t gtile[FN];
   bool tvalid[FN];
@@ -241,7 +270,7 @@ __global__ __launch_bounds__(kThreadsLds) void grouped_gemm_lds_kernel(GemmParam
 #endif
 }
 
-template <bool I8, int EPI, int FM, int FN>
+template <bool I8, int EPI, int FM, int FN, int SA, int SB, int BPOL>
 int launch_lds_cfg(const GemmParams& p, int64_t max_tiles, hipStream_t stream) {
   constexpr bool PAIR = epi_pair(EPI);
   const int64_t per_block = PAIR ? (int64_t)kWN * (FN / 2) : (int64_t)kWN * FN;
@@ -256,20 +285,27 @@ int launch_lds_cfg(const GemmParams& p, int64_t max_tiles, hipStream_t stream) {
     const char* v = getenv("FCMOE_LDS_GROUP");
     return v ? atoi(v) : kLdsGroupTiles;
   }();
-  hipLaunchKernelGGL((grouped_gemm_lds_kernel<I8, EPI, FM, FN>), dim3((unsigned)grid), dim3(kThreadsLds), 0, stream,
-                     p, (int)n_blocks, gm);
+  hipLaunchKernelGGL((grouped_gemm_lds_kernel<I8, EPI, FM, FN, SA, SB, BPOL>), dim3((unsigned)grid), dim3(kThreadsLds),
+                     0, stream, p, (int)n_blocks, gm);
   return check_launch("grouped_gemm_lds");
 }
 
 template <bool I8, int EPI>
 int launch_lds_bm(int bm, const GemmParams& p, int64_t max_tiles, hipStream_t stream) {
+  // Weight stages of the 128/192-row classes load nontemporal: an expert in
+  // those classes has one row tile, so its weights are read exactly once and
+  // caching them only evicts the A rows the other channel blocks re-read.
+  // The 256-row class holds every larger expert, whose row tiles re-read the
+  // same weights, which stay cached (C4: W13 bm192 2.48 -> 2.40 ms; C3's
+  // W2 bm256 0.63 -> 0.66 ms with nontemporal weights).
+  constexpr int kNT = 2;  // buffer-load cache policy bit: nontemporal
   switch (bm) {
     case 128:
-      return launch_lds_cfg<I8, EPI, 4, 8>(p, max_tiles, stream);
+      return launch_lds_cfg<I8, EPI, 4, 8, 3, 3, kNT>(p, max_tiles, stream);
     case 192:
-      return launch_lds_cfg<I8, EPI, 6, 8>(p, max_tiles, stream);
+      return launch_lds_cfg<I8, EPI, 6, 8, 3, 3, kNT>(p, max_tiles, stream);
     case 256:
-      return launch_lds_cfg<I8, EPI, 8, 6>(p, max_tiles, stream);
+      return launch_lds_cfg<I8, EPI, 8, 6, 3, 3, 0>(p, max_tiles, stream);
     default:
       return fail(FCMOE_EINVAL, "unsupported LDS tile rows");
   }

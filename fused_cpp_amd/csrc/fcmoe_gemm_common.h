@@ -97,11 +97,45 @@ __device__ __forceinline__ void i8x16_to_bf16(v4i b, v4i& lo, v4i& hi) {
 // that fragment's stores: the output may alias those arrays as far as the
 // compiler knows, so a load left between stores would wait for each store.
 // Channels, positions and routes fit in 32 bits (checked by the launchers).
-template <bool I8, int EPI, int FM, int FN>
+//
+// Staged metadata (LM): the LDS kernel loads the tile's per-row values (row
+// scale, output row) and per-channel scales into LDS before its K loop
+// (EpiMeta). Loaded here instead, a row value load issued after a
+// fragment's stores waits for those stores too (vmcnt counts both, in
+// order), and the W13 row scale is a dependent pair of loads: six fragments
+// made the epilogue a chain of ~30 memory round trips.
+// The pointers are typed as LDS (address space 3): as generic pointers the
+// reads compile to flat loads, which count in vmcnt as well and may alias
+// the output, so each one waited for every store before it.
+typedef __attribute__((address_space(3))) const float* lds_cfloat_ptr;
+typedef __attribute__((address_space(3))) const int* lds_cint_ptr;
+struct EpiMeta {
+  lds_cfloat_ptr rs;  // [BM] row scale (W13: x scale of the row's token)
+  lds_cint_ptr orow;  // [BM] output row (W2: flat route; else sorted position)
+  lds_cfloat_ptr cs;  // [NT * 16] per-channel scale of channel tile slot s
+  int cbase;          // this wave's first slot
+};
+
+// Epilogues whose per-channel values are scales (staged by the LDS kernel);
+// the bias epilogues load their biases here (one round trip, before any
+// store).
+__host__ __device__ constexpr bool epi_col_scale(int epi) {
+  return epi == kEpiW13SwigluI8 || epi == kEpiW2RouteI8 || epi == kEpiI8Gemm;
+}
+__host__ __device__ constexpr bool epi_route(int epi) {
+  return epi == kEpiW2RouteI8 || epi == kEpiW2RouteBf16 || epi == kEpiW2RouteW8;
+}
+
+template <bool I8, int EPI, int FM, int FN, bool LM = false>
 __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, const typename Acc<I8>::type (&acc)[FM][FN],
                                               const int64_t (&gtile)[FN], const bool (&tvalid)[FN], int row_base,
-                                              int rows, int pos0, int expert, int lane) {
+                                              int rows, int pos0, int expert, int lane, const EpiMeta& m = {}) {
   const int col = lane % 16;
+  // tile-local row of (fragment i, register q), clamped like row_of
+  auto lrow = [&](int i, int q) -> int {
+    const int r = row_base + i * 16 + (lane / 16) * 4 + q;
+    return r < rows ? r : rows - 1;
+  };
   auto row_of = [&](int i, int q, bool* ok) -> int {
     const int r = row_base + i * 16 + (lane / 16) * 4 + q;
     *ok = r < rows;
@@ -119,7 +153,10 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, const typenam
       f[j] = (int)(gtile[j] * 16 + col);  // gate channel (group 0)
       fv[j] = tvalid[j] && f[j] < p.n_half;
       const int64_t fc = fv[j] ? f[j] : 0;
-      if constexpr (EPI == kEpiW13SwigluI8 || EPI == kEpiW13ActW8) {
+      if constexpr (LM && epi_col_scale(EPI)) {
+        cg[j] = m.cs[(m.cbase + j) * 16 + col];
+        cu[j] = m.cs[(m.cbase + j + HP) * 16 + col];
+      } else if constexpr (EPI == kEpiW13SwigluI8 || EPI == kEpiW13ActW8) {
         cg[j] = p.scale_col[(int64_t)expert * n + fc];
         cu[j] = p.scale_col[(int64_t)expert * n + p.n_half + fc];
       } else {
@@ -135,7 +172,12 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, const typenam
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         pos[q] = row_of(i, q, &rok[q]);
-        if constexpr (EPI == kEpiW13SwigluI8) xs[q] = p.scale_row[p.row_map ? p.row_map[pos[q]] : pos[q]];
+        if constexpr (EPI == kEpiW13SwigluI8) {
+          if constexpr (LM)
+            xs[q] = m.rs[lrow(i, q)];
+          else
+            xs[q] = p.scale_row[p.row_map ? p.row_map[pos[q]] : pos[q]];
+        }
       }
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
@@ -200,9 +242,14 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, const typenam
       dch[j] = EPI == kEpiRawF32Bias ? (int)(gtile[j] * 16 + col) : ch[j];  // RawF32Bias: packed order
       cs[j] = 0.0f;
       cb[j] = 0.0f;
-      if constexpr (EPI == kEpiW2RouteI8 || EPI == kEpiW2RouteW8) cs[j] = p.scale_col[(int64_t)expert * p.n + ch[j]];
-      if constexpr (EPI == kEpiI8Gemm) {
+      if constexpr (LM && epi_col_scale(EPI)) {
+        cs[j] = m.cs[(m.cbase + j) * 16 + col];
+      } else if constexpr (EPI == kEpiW2RouteI8 || EPI == kEpiW2RouteW8) {
+        cs[j] = p.scale_col[(int64_t)expert * p.n + ch[j]];
+      } else if constexpr (EPI == kEpiI8Gemm) {
         cs[j] = p.scale_col[ch[j]];
+      }
+      if constexpr (EPI == kEpiI8Gemm) {
         if (p.bias) cb[j] = p.bias[ch[j]];
       }
       if constexpr (EPI == kEpiRawF32Bias || EPI == kEpiW2RouteBf16) {
@@ -217,8 +264,13 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, const typenam
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int pos = row_of(i, q, &rok[q]);
-        orow[q] = ROUTE ? p.sorted_routes[pos] : pos;
-        rs[q] = ROWSCALE ? p.scale_row[pos] : 0.0f;
+        if constexpr (LM) {
+          orow[q] = m.orow[lrow(i, q)];
+          rs[q] = ROWSCALE ? m.rs[lrow(i, q)] : 0.0f;
+        } else {
+          orow[q] = ROUTE ? p.sorted_routes[pos] : pos;
+          rs[q] = ROWSCALE ? p.scale_row[pos] : 0.0f;
+        }
       }
 #pragma unroll
       for (int q = 0; q < 4; ++q) {

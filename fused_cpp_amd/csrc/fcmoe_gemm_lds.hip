@@ -89,6 +89,123 @@ __device__ __forceinline__ bool lds_work_item(int b, int count, int n_blocks, in
   return true;
 }
 
+// ---- staged W8A8 epilogues. The generic epilogue stores each accumulator
+// value from its MFMA lane: one bf16 (W13) or one fp32 (W2) per lane and
+// instruction, 16-lane pieces of four rows, plus a dword per (row, gate tile)
+// for the W13 row maxima -- 192 store instructions per wave at BM = 192.
+// Measured on C4 (one workgroup per CU, so nothing overlaps the epilogue),
+// the W13 epilogue cost as much as 0.77 ms of a 2.4 ms launch. Here each
+// wave writes a 16-row fragment into its own slice of the (now idle) stage
+// memory and stores it back as row-contiguous 16-byte pieces: full cache
+// lines, 8x (W13) / 4x (W2) fewer store instructions. The arithmetic is the
+// generic epilogue's, value for value.
+typedef __attribute__((address_space(3))) uint8_t* lds_u8_ptr;
+
+template <int FN>
+constexpr int staged_slice_bytes(int epi) {
+  return epi == kEpiW13SwigluI8 ? 16 * ((FN / 2) * 32 + 16) + 16 * (FN / 2) * 4 : 16 * (FN * 64 + 16);
+}
+
+template <int EPI, int FM, int FN>
+__device__ __forceinline__ void staged_epilogue(const GemmParams& p, const v4i (&acc)[FM][FN],
+                                                const int64_t (&gtile)[FN], const bool (&tvalid)[FN], int row_base,
+                                                int rows, int pos0, int expert, int lane, const EpiMeta& m,
+                                                lds_u8_ptr slice) {
+  const int col = lane % 16;
+  const int rq = (lane / 16) * 4;  // first fragment row of this lane's registers
+  if constexpr (EPI == kEpiW13SwigluI8) {
+    constexpr int HP = FN / 2;
+    constexpr int RS = HP * 32 + 16;   // bytes per staged row (HP*16 bf16 + pad: rows 4 apart on other banks)
+    constexpr int UPR = HP * 2;        // 16-byte units per row
+    const lds_u8_ptr rp = slice + 16 * RS;  // [16 rows][HP] row maxima
+    const uint32_t ftab = fexpa_table_lane();
+    float cg[HP], cu[HP];
+    bool fv[HP];
+#pragma unroll
+    for (int j = 0; j < HP; ++j) {
+      fv[j] = tvalid[j] && gtile[j] * 16 + col < p.n_half;
+      cg[j] = m.cs[(m.cbase + j) * 16 + col];
+      cu[j] = m.cs[(m.cbase + j + HP) * 16 + col];
+    }
+    const int64_t f0 = gtile[0] * 16;  // the wave's gate channels are f0 .. f0 + 16 HP - 1
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      const int rbase = row_base + i * 16;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int r = rbase + rq + q;
+        const bool rok = r < rows;
+        const float xs = m.rs[rok ? r : rows - 1];
+#pragma unroll
+        for (int j = 0; j < HP; ++j) {
+          // w13_epilogue, csrc/moe/arm/i8mm_w8a8/kernels.cpp:230-246
+          float gate = (float)acc[i][j][q] * (xs * cg[j]);
+          float up = (float)acc[i][j + HP][q] * (xs * cu[j]);
+          gate = fminf(gate, 10.0f);
+          up = fmaxf(fminf(up, 10.0f), -10.0f);
+          const float ex = fexpa_exp_neg_v(gate, ftab);
+          const uint16_t yb = f32_to_bf16((gate * up) / (ex + 1.0f));
+          *(__attribute__((address_space(3))) uint16_t*)(slice + (rq + q) * RS + (j * 16 + col) * 2) = yb;
+          const float amax = max16(rok && fv[j] ? fabsf(bf16_to_f32(yb)) : 0.0f);
+          if (col == 0) *(__attribute__((address_space(3))) float*)(rp + ((rq + q) * HP + j) * 4) = amax;
+        }
+      }
+#pragma unroll
+      for (int h = 0; h < (16 * UPR + kWave - 1) / kWave; ++h) {
+        const int idx = h * kWave + lane;
+        const int row = idx / UPR, u = idx % UPR;
+        const int r = rbase + row;
+        const int64_t ch = f0 + u * 8;
+        if (idx < 16 * UPR && r < rows && ch < p.n_half) {
+          const v4i v = *(__attribute__((address_space(3))) const v4i*)(slice + row * RS + u * 16);
+          *(v4i*)((uint16_t*)p.out + (int64_t)(pos0 + r) * p.ldo + ch) = v;
+        }
+      }
+      if (lane < 16 * HP) {
+        const int row = lane / HP, jj = lane % HP;
+        const int r = rbase + row;
+        const int64_t t = gtile[0] + jj;  // the wave's gate tiles are consecutive
+        if (r < rows && t < p.n_tiles)
+          p.rowpart[(int64_t)(pos0 + r) * p.n_tiles + t] =
+              *(__attribute__((address_space(3))) const float*)(rp + lane * 4);
+      }
+    }
+  } else {  // kEpiW2RouteI8: store_w2, csrc/moe/arm/i8mm_w8a8/kernels.cpp:248-257
+    constexpr int RS = FN * 64 + 16;  // bytes per staged row (FN*16 fp32 + pad)
+    constexpr int UPR = FN * 4;       // 16-byte units per row
+    float cs[FN];
+#pragma unroll
+    for (int j = 0; j < FN; ++j) cs[j] = m.cs[(m.cbase + j) * 16 + col];
+    const int64_t c0 = gtile[0] * 16;  // the wave's channels are c0 .. c0 + 16 FN - 1
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      const int rbase = row_base + i * 16;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int r = rbase + rq + q;
+        const float rs = m.rs[r < rows ? r : rows - 1];
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+          *(__attribute__((address_space(3))) float*)(slice + (rq + q) * RS + (j * 16 + col) * 4) =
+              (float)acc[i][j][q] * (rs * cs[j]);
+      }
+#pragma unroll
+      for (int h = 0; h < 16 * UPR / kWave; ++h) {
+        const int idx = h * kWave + lane;
+        const int row = idx / UPR, u = idx % UPR;
+        const int r = rbase + row;
+        const int64_t ch = c0 + u * 4;
+        if (r < rows && ch < p.n) {
+          const int orow = m.orow[r];
+          const v4i v = *(__attribute__((address_space(3))) const v4i*)(slice + row * RS + u * 16);
+          *(v4i*)((float*)p.out + (int64_t)orow * p.ldo + ch) = v;
+        }
+      }
+    }
+  }
+  (void)expert;
+}
+
 template <bool I8, int EPI, int FM, int FN, int SA, int SB, int BPOL>
 __global__ __launch_bounds__(kThreadsLds) void grouped_gemm_lds_kernel(GemmParams p, int n_blocks, int gm) {
   // The body is device-only: the buffer-resource type does not exist for the
@@ -112,11 +229,20 @@ __global__ __launch_bounds__(kThreadsLds) void grouped_gemm_lds_kernel(GemmParam
   constexpr int HP = FN / 2;
   static_assert(SA >= 2 && SB >= SA, "A ring of 2+ stages, B ring at least as deep");
   static_assert(WAIT < 64, "vmcnt range");
-  static_assert(SA * A_BYTES + SB * B_BYTES <= 160 * 1024, "LDS budget");
+  static_assert(SA * A_BYTES + SB * B_BYTES + 8 * BM + 64 * NT <= 160 * 1024, "LDS budget");
+  static_assert(NT * 16 <= kThreadsLds && BM <= kThreadsLds, "one metadata value per thread");
   static_assert(FM >= 3, "the fragment ring runs two fragments ahead");
   typedef typename Acc<I8>::type AccT;
 
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[SA * A_BYTES + SB * B_BYTES];
+  // One LDS object: the stage rings, then the epilogue metadata. (With a
+  // second __shared__ object the compiler could no longer tell the fragment
+  // reads apart from the in-flight buffer_load ... lds writes and put a
+  // vmcnt(0) in every K iteration, draining the prefetch ring.)
+  constexpr int META = SA * A_BYTES + SB * B_BYTES;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[META + 8 * BM + 64 * NT];
+  float* const meta_rs = (float*)(smem + META);
+  int* const meta_orow = (int*)(smem + META + 4 * BM);
+  float* const meta_cs = (float*)(smem + META + 8 * BM);
   uint8_t* const smem_b = smem + SA * A_BYTES;
 
   const int count = *p.tile_count;
@@ -207,6 +333,32 @@ __global__ __launch_bounds__(kThreadsLds) void grouped_gemm_lds_kernel(GemmParam
 #pragma unroll
     for (int j = 0; j < FN; ++j) acc[i][j] = AccT{0, 0, 0, 0};
 
+  // ---- epilogue metadata, phase 1: per-row (thread t < BM: row t) and
+  // per-channel (thread t: slot t / 16, column t % 16) values into registers.
+  // Their round trip coincides with the row_map loads the A offsets above
+  // already wait for; phase 2 follows the prologue.
+  constexpr bool ROUTE = epi_route(EPI);
+  constexpr bool COLS = epi_col_scale(EPI);
+  const int mt = threadIdx.x;
+  int m_row = 0, m_orow = 0;
+  float m_rs = 0.0f, m_cs = 0.0f;
+  if (mt < BM) {
+    const int pos = pos0 + (mt < rows ? mt : rows - 1);
+    if constexpr (EPI == kEpiW13SwigluI8) m_row = p.row_map ? p.row_map[pos] : pos;
+    if constexpr (EPI == kEpiW2RouteI8 || EPI == kEpiI8Gemm) m_rs = p.scale_row[pos];
+    m_orow = ROUTE ? p.sorted_routes[pos] : pos;
+  }
+  if constexpr (COLS) {
+    if (mt < NT * 16) {
+      bool valid;
+      const int64_t gt = tile_of(mt / 16 / FN, (mt / 16) % FN, &valid);
+      const int64_t g = gt / p.n_tiles;
+      const int64_t cin = (gt - g * p.n_tiles) * 16 + mt % 16;
+      if (valid && cin < p.n_half)
+        m_cs = p.scale_col[(EPI == kEpiI8Gemm ? 0 : (int64_t)expert * p.n) + g * p.n_half + cin];
+    }
+  }
+
   // Issue order: B chunks 0 .. SB-SA-1 alone, then pairs (A m, B m+SB-SA),
   // one pair per iteration after the prologue. When iteration c waits, the
   // ops issued after A c are B c+SB-SA and the SA-2 later pairs: WAIT.
@@ -218,6 +370,16 @@ __global__ __launch_bounds__(kThreadsLds) void grouped_gemm_lds_kernel(GemmParam
   for (int s = 0; s < SA - 1; ++s) {
     issue_a(s, s);
     issue_b(s + SB - SA, s + SB - SA);
+  }
+  // ---- epilogue metadata, phase 2: the W13 row scale (indexed by the row's
+  // token) and the LDS writes; the K loop's first barrier publishes them.
+  if (mt < BM) {
+    if constexpr (EPI == kEpiW13SwigluI8) m_rs = p.scale_row[m_row];
+    meta_rs[mt] = m_rs;
+    meta_orow[mt] = m_orow;
+  }
+  if constexpr (COLS) {
+    if (mt < NT * 16) meta_cs[mt] = m_cs;
   }
   // Retire the scalar loads of the set-up here: with one still pending at the
   // loop header the first fragment wait of every chunk becomes lgkmcnt(0).
@@ -266,7 +428,16 @@ __global__ __launch_bounds__(kThreadsLds) void grouped_gemm_lds_kernel(GemmParam
   bool tvalid[FN];
 #pragma unroll
   for (int j = 0; j < FN; ++j) gtile[j] = tile_of(wn, j, &tvalid[j]);
-  gemm_epilogue<I8, EPI, FM, FN>(p, acc, gtile, tvalid, wm * FM * 16, rows, pos0, expert, lane);
+  const EpiMeta meta{(lds_cfloat_ptr)meta_rs, (lds_cint_ptr)meta_orow, (lds_cfloat_ptr)meta_cs, wn * FN};
+  if constexpr (EPI == kEpiW13SwigluI8 || EPI == kEpiW2RouteI8) {
+    static_assert(kWaves * staged_slice_bytes<FN>(EPI) <= SA * A_BYTES + SB * B_BYTES, "staging slices fit the stages");
+    // every wave is past its last chunk's fragment reads: the stages are free
+    __builtin_amdgcn_s_barrier();
+    staged_epilogue<EPI, FM, FN>(p, acc, gtile, tvalid, wm * FM * 16, rows, pos0, expert, lane, meta,
+                                 (lds_u8_ptr)(smem + wave * staged_slice_bytes<FN>(EPI)));
+  } else {
+    gemm_epilogue<I8, EPI, FM, FN, true>(p, acc, gtile, tvalid, wm * FM * 16, rows, pos0, expert, lane, meta);
+  }
 #endif
 }
 

@@ -45,19 +45,34 @@ __constant__ static const uint32_t kFexpaTable[64] = {
 // divergent __constant__ load that waits on the memory pipeline.
 __device__ __forceinline__ uint32_t fexpa_table_lane() { return kFexpaTable[threadIdx.x % kWave]; }
 
-// exp_fexpa_neg with the table in a VGPR (fexpa_table_lane); same bits as
-// fexpa_exp_neg.
-__device__ __forceinline__ float fexpa_exp_neg_v(float gate, uint32_t tab) {
+// exp_fexpa_neg with the table in a VGPR (fexpa_table_lane), split so a
+// caller can issue many lookups before it waits for any: fexpa_reduce computes
+// the argument's encoding and residual, fexpa_lookup reads the table entry
+// (ds_bpermute, all lanes active), fexpa_finish forms the result. Together
+// they give exactly fexpa_exp_neg's bits.
+struct FexpaArg {
+  uint32_t bits;   // encoded value's bits: exponent in [13:6], table index in [5:0]
+  float residual;
+};
+__device__ __forceinline__ FexpaArg fexpa_reduce(float gate) {
   float x = fmaxf(fminf(-gate, 87.0f), -87.0f);
   float encoded = __builtin_fmaf(x, 1.4426950216293335f, 196735.0f);
   float k = encoded - 196735.0f;
   float residual = __builtin_fmaf(-k, 0.693145751953125f, x);
   residual = __builtin_fmaf(-k, 1.428606765330187e-06f, residual);
-  uint32_t bits = __float_as_uint(encoded);
-  const uint32_t frac = (uint32_t)__builtin_amdgcn_ds_bpermute((int)((bits & 63u) << 2), (int)tab);
-  float scale = __uint_as_float((((bits >> 6) & 0xffu) << 23) | frac);
-  float poly = __builtin_fmaf(residual, 0.5000003576278687f, 1.000003695487976f);
-  return __builtin_fmaf(scale, poly * residual, scale);
+  return FexpaArg{__float_as_uint(encoded), residual};
+}
+__device__ __forceinline__ uint32_t fexpa_lookup(uint32_t bits, uint32_t tab) {
+  return (uint32_t)__builtin_amdgcn_ds_bpermute((int)((bits & 63u) << 2), (int)tab);
+}
+__device__ __forceinline__ float fexpa_finish(FexpaArg a, uint32_t frac) {
+  float scale = __uint_as_float((((a.bits >> 6) & 0xffu) << 23) | frac);
+  float poly = __builtin_fmaf(a.residual, 0.5000003576278687f, 1.000003695487976f);
+  return __builtin_fmaf(scale, poly * a.residual, scale);
+}
+__device__ __forceinline__ float fexpa_exp_neg_v(float gate, uint32_t tab) {
+  const FexpaArg a = fexpa_reduce(gate);
+  return fexpa_finish(a, fexpa_lookup(a.bits, tab));
 }
 
 __device__ __forceinline__ float fexpa_exp_neg(float gate) {

@@ -131,23 +131,50 @@ __device__ __forceinline__ void staged_epilogue(const GemmParams& p, const v4i (
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
       const int rbase = row_base + i * 16;
+      // Batches of QB registers x HP tiles: every table lookup of a batch is
+      // issued before the first is used and the batch's 16-lane maxima run
+      // side by side (one lookup and max at a time, each waited out alone,
+      // made this the slowest part of the epilogue).
+      constexpr int QB = 2;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int r = rbase + rq + q;
-        const bool rok = r < rows;
-        const float xs = m.rs[rok ? r : rows - 1];
+      for (int q0 = 0; q0 < 4; q0 += QB) {
+        float gate[QB][HP], up[QB][HP], ya[QB][HP];
+        FexpaArg ea[QB][HP];
+        uint32_t frac[QB][HP];
+        bool rok[QB];
 #pragma unroll
-        for (int j = 0; j < HP; ++j) {
-          // w13_epilogue, csrc/moe/arm/i8mm_w8a8/kernels.cpp:230-246
-          float gate = (float)acc[i][j][q] * (xs * cg[j]);
-          float up = (float)acc[i][j + HP][q] * (xs * cu[j]);
-          gate = fminf(gate, 10.0f);
-          up = fmaxf(fminf(up, 10.0f), -10.0f);
-          const float ex = fexpa_exp_neg_v(gate, ftab);
-          const uint16_t yb = f32_to_bf16((gate * up) / (ex + 1.0f));
-          *(__attribute__((address_space(3))) uint16_t*)(slice + (rq + q) * RS + (j * 16 + col) * 2) = yb;
-          const float amax = max16(rok && fv[j] ? fabsf(bf16_to_f32(yb)) : 0.0f);
-          if (col == 0) *(__attribute__((address_space(3))) float*)(rp + ((rq + q) * HP + j) * 4) = amax;
+        for (int b = 0; b < QB; ++b) {
+          const int r = rbase + rq + q0 + b;
+          rok[b] = r < rows;
+          const float xs = m.rs[rok[b] ? r : rows - 1];
+#pragma unroll
+          for (int j = 0; j < HP; ++j) {
+            // w13_epilogue, csrc/moe/arm/i8mm_w8a8/kernels.cpp:230-246
+            gate[b][j] = fminf((float)acc[i][j][q0 + b] * (xs * cg[j]), 10.0f);
+            up[b][j] = fmaxf(fminf((float)acc[i][j + HP][q0 + b] * (xs * cu[j]), 10.0f), -10.0f);
+            ea[b][j] = fexpa_reduce(gate[b][j]);
+            frac[b][j] = fexpa_lookup(ea[b][j].bits, ftab);
+          }
+        }
+#pragma unroll
+        for (int b = 0; b < QB; ++b)
+#pragma unroll
+          for (int j = 0; j < HP; ++j) {
+            const float ex = fexpa_finish(ea[b][j], frac[b][j]);
+            const uint16_t yb = f32_to_bf16((gate[b][j] * up[b][j]) / (ex + 1.0f));
+            *(__attribute__((address_space(3))) uint16_t*)(slice + (rq + q0 + b) * RS + (j * 16 + col) * 2) = yb;
+            ya[b][j] = rok[b] && fv[j] ? fabsf(bf16_to_f32(yb)) : 0.0f;
+          }
+#pragma unroll
+        for (int b = 0; b < QB; ++b)
+#pragma unroll
+          for (int j = 0; j < HP; ++j) ya[b][j] = max16(ya[b][j]);
+        if (col == 0) {
+#pragma unroll
+          for (int b = 0; b < QB; ++b)
+#pragma unroll
+            for (int j = 0; j < HP; ++j)
+              *(__attribute__((address_space(3))) float*)(rp + ((rq + q0 + b) * HP + j) * 4) = ya[b][j];
         }
       }
 #pragma unroll

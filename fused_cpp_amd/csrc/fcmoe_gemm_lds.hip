@@ -233,16 +233,24 @@ __device__ __forceinline__ void staged_epilogue(const GemmParams& p, const v4i (
   (void)expert;
 }
 
-template <bool I8, int EPI, int FM, int FN, int SA, int SB, int BPOL>
+template <bool I8, int EPI, int FM, int FN, int SA, int SB, int BPOL, int AW>
 __global__ __launch_bounds__(kThreadsLds) void grouped_gemm_lds_kernel(GemmParams p, int n_blocks, int gm) {
   // The body is device-only: the buffer-resource type does not exist for the
   // host target, and the host pass needs only the kernel's signature.
 #if __HIP_DEVICE_COMPILE__
   constexpr int BM = kWM * FM * 16;
   constexpr int NT = kWN * FN;            // channel tiles per workgroup
-  constexpr int A_BYTES = BM * 64;        // one A stage
+  // AW = 128: each A stage holds two K chunks (128 bytes of every row) and
+  // is loaded as full 128-byte lines, 8 rows per load. A half-line load (16
+  // rows x 64 bytes) costs the CU's L1 one L2 request per 64 bytes; the
+  // number of requests a CU keeps in flight, not HBM or L2 bandwidth, bounded
+  // the A+B intake (~12 B/clk per CU at 80% L2 hits, L1 pending-stalled 33%
+  // of the time).
+  static_assert(AW == 64 || AW == 128, "A stage K width");
+  constexpr bool AWIDE = AW == 128;
+  constexpr int A_BYTES = BM * AW;        // one A stage
   constexpr int B_BYTES = NT * 1024;      // one B stage
-  constexpr int LA = BM / 16;             // A loads (16 rows x 64 bytes) per chunk
+  constexpr int LA = BM * AW / 1024;      // A loads (1 KB each) per stage
   constexpr int LB = NT;                  // B loads (one 1 KB tile chunk) per chunk
   constexpr int LPA = (LA + kWaves - 1) / kWaves;  // per wave
   constexpr int LPB = (LB + kWaves - 1) / kWaves;
@@ -252,6 +260,11 @@ __global__ __launch_bounds__(kThreadsLds) void grouped_gemm_lds_kernel(GemmParam
   constexpr int WAIT_A = LPB + (SA - 2) * (LPA + LPB);
   constexpr int WAIT_B = (SB - 2) * (LPA + LPB);
   constexpr int WAIT = WAIT_A < WAIT_B ? WAIT_A : WAIT_B;
+  // AW = 128 (SA = 2 stages of two chunks, SB = 3): even iterations wait for
+  // A c/2 and B c, odd ones for B c (see the loop)
+  constexpr int WAIT_EVEN = LPB;
+  constexpr int WAIT_ODD = LPA + LPB;
+  static_assert(!AWIDE || (SA == 2 && SB == 3), "wide A runs 2 A stages and 3 B stages");
   constexpr bool PAIR = epi_pair(EPI);
   constexpr int HP = FN / 2;
   static_assert(SA >= 2 && SB >= SA, "A ring of 2+ stages, B ring at least as deep");
@@ -318,8 +331,12 @@ __global__ __launch_bounds__(kThreadsLds) void grouped_gemm_lds_kernel(GemmParam
   for (int u = 0; u < LPA; ++u) {
     int g = wave + kWaves * u;
     while (g >= LA) g -= LA;
-    const int r = g * 16 + lane / 4;
-    const int unit = (lane % 4) ^ ((lane >> 4) & 3);
+    // AW = 64: rows 16 g + lane / 4, 16-byte unit (lane % 4) stored at slot
+    // unit ^ ((r >> 2) & 3). AW = 128: rows 8 g + lane / 8, unit u of row r
+    // stored at slot u ^ ((r >> 1) & 7). Either way the 16 rows of a
+    // fragment read fall on distinct banks.
+    const int r = AWIDE ? g * 8 + lane / 8 : g * 16 + lane / 4;
+    const int unit = AWIDE ? (lane % 8) ^ ((r >> 1) & 7) : (lane % 4) ^ ((lane >> 4) & 3);
     const int pos = pos0 + (r < rows ? r : rows - 1);  // rows past the tile re-read the last row
     const int64_t arow = p.row_map ? (int64_t)p.row_map[pos] : (int64_t)pos;
     voff_a[u] = (uint32_t)(arow * lda_bytes + unit * 16);
@@ -335,12 +352,19 @@ __global__ __launch_bounds__(kThreadsLds) void grouped_gemm_lds_kernel(GemmParam
     lds_b[u] = t * 1024;
   }
   // Past the end a ring re-loads the last chunk (never read).
+  // AW = 128: c counts stages (pairs of chunks). With an odd chunk count the
+  // last stage's second half lies past K (past the buffer for the last A
+  // row): its lanes re-load the first half instead (never read).
+  const int64_t a_stages = AWIDE ? (kc + 1) / 2 : kc;
+  const bool a_hi = AWIDE && ((lane % 8) ^ ((((wave & 1) << 2) | (lane >> 4)) & 7)) >= 4;
   auto issue_a = [&](int64_t c, int stage) {
-    const int soff = (int)((c < kc ? c : kc - 1) * 64);
+    const int64_t cc = c < a_stages ? c : a_stages - 1;
+    const int soff = (int)(cc * AW);
+    const bool fold = AWIDE && 2 * cc + 1 >= kc;
 #pragma unroll
     for (int u = 0; u < LPA; ++u)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_a, (lds_ptr_t)(smem + stage * A_BYTES + lds_a[u]), 16, voff_a[u],
-                                               soff, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_a, (lds_ptr_t)(smem + stage * A_BYTES + lds_a[u]), 16,
+                                               fold && a_hi ? voff_a[u] - 64 : voff_a[u], soff, 0, 0);
   };
   auto issue_b = [&](int64_t c, int stage) {
     const int soff = (int)((c < kc ? c : kc - 1) * 1024);
@@ -351,7 +375,10 @@ __global__ __launch_bounds__(kThreadsLds) void grouped_gemm_lds_kernel(GemmParam
   };
 
   // ---- fragment addresses (bytes within a stage)
-  const int a_frag = (wm * FM * 16 + lane % 16) * 64 + (((lane / 16) ^ ((lane % 16) >> 2)) * 16);
+  constexpr int A_FRAG = 16 * AW;  // bytes per 16-row fragment in a stage
+  const int a_frag = AWIDE ? (wm * FM * 16 + lane % 16) * 128 + (((lane / 16) ^ ((lane % 16) >> 1)) * 16)
+                           : (wm * FM * 16 + lane % 16) * 64 + (((lane / 16) ^ ((lane % 16) >> 2)) * 16);
+
   const int b_frag = wn * FN * 1024 + lane * 16;
 
   AccT acc[FM][FN];
@@ -386,17 +413,25 @@ __global__ __launch_bounds__(kThreadsLds) void grouped_gemm_lds_kernel(GemmParam
     }
   }
 
-  // Issue order: B chunks 0 .. SB-SA-1 alone, then pairs (A m, B m+SB-SA),
-  // one pair per iteration after the prologue. When iteration c waits, the
-  // ops issued after A c are B c+SB-SA and the SA-2 later pairs: WAIT.
-  // B runs SB-SA chunks further ahead than A: the weights stream from HBM
-  // (long latency), A rows are re-read by the other channel blocks from L2.
+  // Issue order (AW = 64): B chunks 0 .. SB-SA-1 alone, then pairs
+  // (A m, B m+SB-SA), one pair per iteration after the prologue. When
+  // iteration c waits, the ops issued after A c are B c+SB-SA and the SA-2
+  // later pairs: WAIT. B runs SB-SA chunks further ahead than A: the weights
+  // stream from HBM (long latency), A rows are re-read from L2.
+  // AW = 128: A stage 0, B 0, B 1; then even iteration c issues A stage
+  // c/2 + 1 and B c+2, odd iteration c issues B c+2.
+  if constexpr (AWIDE) {
+    issue_a(0, 0);
+    issue_b(0, 0);
+    issue_b(1, 1);
+  } else {
 #pragma unroll
-  for (int s = 0; s < SB - SA; ++s) issue_b(s, s);
+    for (int s = 0; s < SB - SA; ++s) issue_b(s, s);
 #pragma unroll
-  for (int s = 0; s < SA - 1; ++s) {
-    issue_a(s, s);
-    issue_b(s + SB - SA, s + SB - SA);
+    for (int s = 0; s < SA - 1; ++s) {
+      issue_a(s, s);
+      issue_b(s + SB - SA, s + SB - SA);
+    }
   }
   // ---- epilogue metadata, phase 2: the W13 row scale (indexed by the row's
   // token) and the LDS writes; the K loop's first barrier publishes them.
@@ -411,29 +446,21 @@ __global__ __launch_bounds__(kThreadsLds) void grouped_gemm_lds_kernel(GemmParam
   // Retire the scalar loads of the set-up here: with one still pending at the
   // loop header the first fragment wait of every chunk becomes lgkmcnt(0).
   __builtin_amdgcn_s_waitcnt(0xC07F);
-  int sa = 0, sb = 0;
-  for (int64_t c = 0; c < kc; ++c) {
-    wait_vmcnt<WAIT>();  // this wave's chunk-c A and B have landed
-    __builtin_amdgcn_s_barrier();
-    // everyone is done with chunk c-1: its stages take the next chunks
-    issue_a(c + SA - 1, sa == 0 ? SA - 1 : sa - 1);
-    issue_b(c + SB - 1, sb == 0 ? SB - 1 : sb - 1);
-    const uint8_t* sta = smem + sa * A_BYTES;
-    const uint8_t* stb = smem_b + sb * B_BYTES;
-    // Fragment reads in consumption order (A row 0, the B tiles, A row 1),
-    // then one A read two rows ahead per row of MFMAs. The schedule is pinned:
-    // left to itself the compiler sinks each read next to its first use and
-    // every row then waits out the LDS latency.
+  // One chunk: fragment reads in consumption order (A row 0, the B tiles, A
+  // row 1), then one A read two rows ahead per row of MFMAs. The schedule is
+  // pinned: left to itself the compiler sinks each read next to its first use
+  // and every row then waits out the LDS latency.
+  auto compute = [&](const uint8_t* sta, const uint8_t* stb) {
     v4i bf[FN];
     v4i af[3];
-    af[0] = *(const v4i*)(sta + a_frag);
+    af[0] = *(const v4i*)(sta);
 #pragma unroll
     for (int j = 0; j < FN; ++j) bf[j] = *(const v4i*)(stb + b_frag + j * 1024);
-    af[1] = *(const v4i*)(sta + a_frag + 1024);
+    af[1] = *(const v4i*)(sta + A_FRAG);
     __builtin_amdgcn_sched_group_barrier(0x100, FN + 2, 0);  // the FN + 2 leading LDS reads
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
-      if (i + 2 < FM) af[(i + 2) % 3] = *(const v4i*)(sta + a_frag + (i + 2) * 1024);
+      if (i + 2 < FM) af[(i + 2) % 3] = *(const v4i*)(sta + (i + 2) * A_FRAG);
 #pragma unroll
       for (int j = 0; j < FN; ++j) {
         if constexpr (I8) {
@@ -446,8 +473,39 @@ __global__ __launch_bounds__(kThreadsLds) void grouped_gemm_lds_kernel(GemmParam
       __builtin_amdgcn_sched_group_barrier(0x008, FN, 0);                 // then row i's MFMAs
     }
     __builtin_amdgcn_sched_barrier(0);
-    sa = sa == SA - 1 ? 0 : sa + 1;
-    sb = sb == SB - 1 ? 0 : sb + 1;
+  };
+  if constexpr (AWIDE) {
+    int sa = 0, sb = 0;
+    for (int64_t c = 0; c < kc; c += 2) {
+      wait_vmcnt<WAIT_EVEN>();  // A stage c/2 and B c have landed
+      __builtin_amdgcn_s_barrier();
+      // everyone is done with chunk c-1: A stage c/2-1 and B stage c-1 are free
+      issue_a(c / 2 + 1, sa ^ 1);
+      issue_b(c + 2, sb == 0 ? 2 : sb - 1);
+      compute(smem + sa * A_BYTES + a_frag, smem_b + sb * B_BYTES);
+      sb = sb == 2 ? 0 : sb + 1;
+      if (c + 1 < kc) {
+        wait_vmcnt<WAIT_ODD>();  // B c+1 has landed
+        __builtin_amdgcn_s_barrier();
+        issue_b(c + 3, sb == 0 ? 2 : sb - 1);
+        // second chunk of the stage: units 4..7, i.e. slot bit 2 flipped ((4 | u) ^ x == (u ^ x) ^ 4)
+        compute(smem + sa * A_BYTES + (a_frag ^ 64), smem_b + sb * B_BYTES);
+        sb = sb == 2 ? 0 : sb + 1;
+      }
+      sa ^= 1;
+    }
+  } else {
+    int sa = 0, sb = 0;
+    for (int64_t c = 0; c < kc; ++c) {
+      wait_vmcnt<WAIT>();  // this wave's chunk-c A and B have landed
+      __builtin_amdgcn_s_barrier();
+      // everyone is done with chunk c-1: its stages take the next chunks
+      issue_a(c + SA - 1, sa == 0 ? SA - 1 : sa - 1);
+      issue_b(c + SB - 1, sb == 0 ? SB - 1 : sb - 1);
+      compute(smem + sa * A_BYTES + a_frag, smem_b + sb * B_BYTES);
+      sa = sa == SA - 1 ? 0 : sa + 1;
+      sb = sb == SB - 1 ? 0 : sb + 1;
+    }
   }
   wait_vmcnt<0>();  // the trailing (unused) stage loads
 
@@ -468,12 +526,19 @@ __global__ __launch_bounds__(kThreadsLds) void grouped_gemm_lds_kernel(GemmParam
 #endif
 }
 
-template <bool I8, int EPI, int FM, int FN, int SA, int SB, int BPOL>
-int launch_lds_cfg(const GemmParams& p, int64_t max_tiles, hipStream_t stream) {
+// Channel blocks per row tile of a workgroup whose waves hold FN 16-channel
+// tiles (W13: FN/2 gate/up pairs).
+template <int EPI>
+int64_t lds_blocks(int fn, const GemmParams& p) {
   constexpr bool PAIR = epi_pair(EPI);
-  const int64_t per_block = PAIR ? (int64_t)kWN * (FN / 2) : (int64_t)kWN * FN;
+  const int64_t per_block = PAIR ? (int64_t)kWN * (fn / 2) : (int64_t)kWN * fn;
   const int64_t units = PAIR ? p.n_tiles : (int64_t)p.n_groups * p.n_tiles;
-  const int64_t n_blocks = ceil_div(units, per_block);
+  return ceil_div(units, per_block);
+}
+
+template <bool I8, int EPI, int FM, int FN, int SA, int SB, int BPOL, int AW>
+int launch_lds_cfg(const GemmParams& p, int64_t max_tiles, hipStream_t stream) {
+  const int64_t n_blocks = lds_blocks<EPI>(FN, p);
   const int64_t grid = max_tiles * n_blocks;
   if (grid <= 0) return FCMOE_OK;
   if (grid > INT32_MAX) return fail(FCMOE_EINVAL, "grouped gemm grid too large");
@@ -483,8 +548,8 @@ int launch_lds_cfg(const GemmParams& p, int64_t max_tiles, hipStream_t stream) {
     const char* v = getenv("FCMOE_LDS_GROUP");
     return v ? atoi(v) : kLdsGroupTiles;
   }();
-  hipLaunchKernelGGL((grouped_gemm_lds_kernel<I8, EPI, FM, FN, SA, SB, BPOL>), dim3((unsigned)grid), dim3(kThreadsLds),
-                     0, stream, p, (int)n_blocks, gm);
+  hipLaunchKernelGGL((grouped_gemm_lds_kernel<I8, EPI, FM, FN, SA, SB, BPOL, AW>), dim3((unsigned)grid),
+                     dim3(kThreadsLds), 0, stream, p, (int)n_blocks, gm);
   return check_launch("grouped_gemm_lds");
 }
 
@@ -497,13 +562,15 @@ int launch_lds_bm(int bm, const GemmParams& p, int64_t max_tiles, hipStream_t st
   // same weights, which stay cached (C4: W13 bm192 2.48 -> 2.40 ms; C3's
   // W2 bm256 0.63 -> 0.66 ms with nontemporal weights).
   constexpr int kNT = 2;  // buffer-load cache policy bit: nontemporal
+  // A stages are 128 bytes of K (two chunks, full-line loads) where the
+  // register budget allows it; the 192-row tile would spill with them.
   switch (bm) {
     case 128:
-      return launch_lds_cfg<I8, EPI, 4, 8, 3, 3, kNT>(p, max_tiles, stream);
+      return launch_lds_cfg<I8, EPI, 4, 8, 2, 3, kNT, 128>(p, max_tiles, stream);
     case 192:
-      return launch_lds_cfg<I8, EPI, 6, 8, 3, 3, kNT>(p, max_tiles, stream);
+      return launch_lds_cfg<I8, EPI, 6, 8, 3, 3, kNT, 64>(p, max_tiles, stream);
     case 256:
-      return launch_lds_cfg<I8, EPI, 8, 6, 3, 3, 0>(p, max_tiles, stream);
+      return launch_lds_cfg<I8, EPI, 8, 6, 2, 3, 0, 128>(p, max_tiles, stream);
     default:
       return fail(FCMOE_EINVAL, "unsupported LDS tile rows");
   }

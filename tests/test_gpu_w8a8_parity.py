@@ -191,3 +191,22 @@ def test_w8a8_forward_repeat_bitwise(gpu, oracle_lib):
     a = H.gpu_w8a8_forward(x, ids, w, q13, s13, q2, s2, gpu)
     b = H.gpu_w8a8_forward(x, ids, w, q13, s13, q2, s2, gpu)
     np.testing.assert_array_equal(a, b)
+
+
+def test_w8a8_forward_bit_exact_odd_chunk_counts(gpu, oracle_lib):
+    """K = 1040 / 272 (17 / 5 chunks of 64 bytes): the LDS-staged kernel loads
+    A two chunks at a time, so its last A stage lies half past K; the 600- and
+    256-row experts run the 256-row tile on it."""
+    case = H.w8a8_case(61, 1200, 1040, 272, 9, 4, skew=1.2)
+    _check_w8a8(gpu, oracle_lib, case, shared=True, scale=2.5)
+    counts = np.asarray([129, 256, 600, 0, 2], np.int32)
+    rng = np.random.default_rng(5)
+    total = int(counts.sum())
+    a = rng.integers(-127, 128, size=(total + 3, 1088), dtype=np.int8)
+    row_map = rng.integers(0, total + 3, size=total).astype(np.int32)
+    w = rng.integers(-127, 128, size=(len(counts), 112, 1088), dtype=np.int8)
+    acc, offsets = H.gpu_grouped_gemm_acc(a, row_map, counts, w, gpu)
+    for e in range(len(counts)):
+        lo, hi = offsets[e], offsets[e + 1]
+        if hi > lo:
+            np.testing.assert_array_equal(acc[lo:hi], oracle_lib.gemm_i8_rows(a, row_map[lo:hi].astype(np.int64), w[e]))

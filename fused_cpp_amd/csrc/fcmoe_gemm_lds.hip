@@ -233,13 +233,15 @@ __device__ __forceinline__ void staged_epilogue(const GemmParams& p, const v4i (
   (void)expert;
 }
 
-template <bool I8, int EPI, int FM, int FN, int SA, int SB, int BPOL, int AW>
-__global__ __launch_bounds__(kThreadsLds) void grouped_gemm_lds_kernel(GemmParams p, int n_blocks, int gm) {
+template <bool I8, int EPI, int FM, int FN, int SA, int SB, int BPOL, int AW, int WMW, int WNW>
+__global__ __launch_bounds__(WMW * WNW * kWave) void grouped_gemm_lds_kernel(GemmParams p, int n_blocks, int gm) {
   // The body is device-only: the buffer-resource type does not exist for the
   // host target, and the host pass needs only the kernel's signature.
 #if __HIP_DEVICE_COMPILE__
-  constexpr int BM = kWM * FM * 16;
-  constexpr int NT = kWN * FN;            // channel tiles per workgroup
+  constexpr int WAVES = WMW * WNW;
+  constexpr int THREADS = WAVES * kWave;
+  constexpr int BM = WMW * FM * 16;
+  constexpr int NT = WNW * FN;            // channel tiles per workgroup
   // AW = 128: each A stage holds two K chunks (128 bytes of every row) and
   // is loaded as full 128-byte lines, 8 rows per load. A half-line load (16
   // rows x 64 bytes) costs the CU's L1 one L2 request per 64 bytes; the
@@ -252,8 +254,8 @@ __global__ __launch_bounds__(kThreadsLds) void grouped_gemm_lds_kernel(GemmParam
   constexpr int B_BYTES = NT * 1024;      // one B stage
   constexpr int LA = BM * AW / 1024;      // A loads (1 KB each) per stage
   constexpr int LB = NT;                  // B loads (one 1 KB tile chunk) per chunk
-  constexpr int LPA = (LA + kWaves - 1) / kWaves;  // per wave
-  constexpr int LPB = (LB + kWaves - 1) / kWaves;
+  constexpr int LPA = (LA + WAVES - 1) / WAVES;  // per wave
+  constexpr int LPB = (LB + WAVES - 1) / WAVES;
   // vector-memory ops a wave may still have in flight once chunk c's A and B
   // have landed (see the issue order below)
   // (B c precedes A c when SB > SA; with SB == SA it is A c's pair partner)
@@ -270,7 +272,7 @@ __global__ __launch_bounds__(kThreadsLds) void grouped_gemm_lds_kernel(GemmParam
   static_assert(SA >= 2 && SB >= SA, "A ring of 2+ stages, B ring at least as deep");
   static_assert(WAIT < 64, "vmcnt range");
   static_assert(SA * A_BYTES + SB * B_BYTES + 8 * BM + 64 * NT <= 160 * 1024, "LDS budget");
-  static_assert(NT * 16 <= kThreadsLds && BM <= kThreadsLds, "one metadata value per thread");
+  static_assert(NT * 16 <= THREADS && BM <= THREADS, "one metadata value per thread");
   static_assert(FM >= 3, "the fragment ring runs two fragments ahead");
   typedef typename Acc<I8>::type AccT;
 
@@ -297,19 +299,19 @@ __global__ __launch_bounds__(kThreadsLds) void grouped_gemm_lds_kernel(GemmParam
 
   const int lane = threadIdx.x % kWave;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-  const int wm = wave / kWN;
-  const int wn = wave % kWN;
+  const int wm = wave / WNW;
+  const int wn = wave % WNW;
   const int64_t kc = p.k_chunks;
   const int64_t total_tiles = (int64_t)p.n_groups * p.n_tiles;
 
   // channel tile (index within the expert) of wave column wn_, slot j
   auto tile_of = [&](int wn_, int j, bool* valid) -> int64_t {
     if constexpr (PAIR) {
-      const int64_t pr = ((int64_t)nb * kWN + wn_) * HP + (j % HP);
+      const int64_t pr = ((int64_t)nb * WNW + wn_) * HP + (j % HP);
       *valid = pr < p.n_tiles;
       return (j < HP ? 0 : p.n_tiles) + pr;
     } else {
-      const int64_t t = ((int64_t)nb * kWN + wn_) * FN + j;
+      const int64_t t = ((int64_t)nb * WNW + wn_) * FN + j;
       *valid = t < total_tiles;
       return t;
     }
@@ -329,7 +331,7 @@ __global__ __launch_bounds__(kThreadsLds) void grouped_gemm_lds_kernel(GemmParam
   int lds_a[LPA], lds_b[LPB];
 #pragma unroll
   for (int u = 0; u < LPA; ++u) {
-    int g = wave + kWaves * u;
+    int g = wave + WAVES * u;
     while (g >= LA) g -= LA;
     // AW = 64: rows 16 g + lane / 4, 16-byte unit (lane % 4) stored at slot
     // unit ^ ((r >> 2) & 3). AW = 128: rows 8 g + lane / 8, unit u of row r
@@ -344,7 +346,7 @@ __global__ __launch_bounds__(kThreadsLds) void grouped_gemm_lds_kernel(GemmParam
   }
 #pragma unroll
   for (int u = 0; u < LPB; ++u) {
-    int t = wave + kWaves * u;
+    int t = wave + WAVES * u;
     while (t >= LB) t -= LB;
     bool valid;
     const int64_t gt = tile_of(t / FN, t % FN, &valid);
@@ -515,7 +517,7 @@ __global__ __launch_bounds__(kThreadsLds) void grouped_gemm_lds_kernel(GemmParam
   for (int j = 0; j < FN; ++j) gtile[j] = tile_of(wn, j, &tvalid[j]);
   const EpiMeta meta{(lds_cfloat_ptr)meta_rs, (lds_cint_ptr)meta_orow, (lds_cfloat_ptr)meta_cs, wn * FN};
   if constexpr (EPI == kEpiW13SwigluI8 || EPI == kEpiW2RouteI8) {
-    static_assert(kWaves * staged_slice_bytes<FN>(EPI) <= SA * A_BYTES + SB * B_BYTES, "staging slices fit the stages");
+    static_assert(WAVES * staged_slice_bytes<FN>(EPI) <= SA * A_BYTES + SB * B_BYTES, "staging slices fit the stages");
     // every wave is past its last chunk's fragment reads: the stages are free
     __builtin_amdgcn_s_barrier();
     staged_epilogue<EPI, FM, FN>(p, acc, gtile, tvalid, wm * FM * 16, rows, pos0, expert, lane, meta,
@@ -529,16 +531,16 @@ __global__ __launch_bounds__(kThreadsLds) void grouped_gemm_lds_kernel(GemmParam
 // Channel blocks per row tile of a workgroup whose waves hold FN 16-channel
 // tiles (W13: FN/2 gate/up pairs).
 template <int EPI>
-int64_t lds_blocks(int fn, const GemmParams& p) {
+int64_t lds_blocks(int wn, int fn, const GemmParams& p) {
   constexpr bool PAIR = epi_pair(EPI);
-  const int64_t per_block = PAIR ? (int64_t)kWN * (fn / 2) : (int64_t)kWN * fn;
+  const int64_t per_block = PAIR ? (int64_t)wn * (fn / 2) : (int64_t)wn * fn;
   const int64_t units = PAIR ? p.n_tiles : (int64_t)p.n_groups * p.n_tiles;
   return ceil_div(units, per_block);
 }
 
-template <bool I8, int EPI, int FM, int FN, int SA, int SB, int BPOL, int AW>
+template <bool I8, int EPI, int FM, int FN, int SA, int SB, int BPOL, int AW, int WMW = kWM, int WNW = kWN>
 int launch_lds_cfg(const GemmParams& p, int64_t max_tiles, hipStream_t stream) {
-  const int64_t n_blocks = lds_blocks<EPI>(FN, p);
+  const int64_t n_blocks = lds_blocks<EPI>(WNW, FN, p);
   const int64_t grid = max_tiles * n_blocks;
   if (grid <= 0) return FCMOE_OK;
   if (grid > INT32_MAX) return fail(FCMOE_EINVAL, "grouped gemm grid too large");
@@ -548,8 +550,8 @@ int launch_lds_cfg(const GemmParams& p, int64_t max_tiles, hipStream_t stream) {
     const char* v = getenv("FCMOE_LDS_GROUP");
     return v ? atoi(v) : kLdsGroupTiles;
   }();
-  hipLaunchKernelGGL((grouped_gemm_lds_kernel<I8, EPI, FM, FN, SA, SB, BPOL, AW>), dim3((unsigned)grid),
-                     dim3(kThreadsLds), 0, stream, p, (int)n_blocks, gm);
+  hipLaunchKernelGGL((grouped_gemm_lds_kernel<I8, EPI, FM, FN, SA, SB, BPOL, AW, WMW, WNW>), dim3((unsigned)grid),
+                     dim3(WMW * WNW * kWave), 0, stream, p, (int)n_blocks, gm);
   return check_launch("grouped_gemm_lds");
 }
 
@@ -564,13 +566,22 @@ int launch_lds_bm(int bm, const GemmParams& p, int64_t max_tiles, hipStream_t st
   constexpr int kNT = 2;  // buffer-load cache policy bit: nontemporal
   // A stages are 128 bytes of K (two chunks, full-line loads) where the
   // register budget allows it; the 192-row tile would spill with them.
+  // A stages are 128 bytes of K (two chunks, full-line loads) where the
+  // register budget allows it; the 192-row tile would spill with them.
   switch (bm) {
     case 128:
       return launch_lds_cfg<I8, EPI, 4, 8, 2, 3, kNT, 128>(p, max_tiles, stream);
     case 192:
       return launch_lds_cfg<I8, EPI, 6, 8, 3, 3, kNT, 64>(p, max_tiles, stream);
     case 256:
-      return launch_lds_cfg<I8, EPI, 8, 6, 2, 3, 0, 128>(p, max_tiles, stream);
+      // W13 (gate/up pairs) on 4-wave workgroups, two per CU (2 x 2 waves of
+      // 128 x 96, 72 KB of LDS): another workgroup's K loop overlaps each
+      // item's epilogue (C3 W13 0.938 -> 0.927 ms, C4 0.455 -> 0.417 ms). W2
+      // ran slower that way (C3 0.530 -> 0.586 ms) and keeps 8 waves.
+      if constexpr (epi_pair(EPI))
+        return launch_lds_cfg<I8, EPI, 8, 6, 2, 3, 0, 64, 2, 2>(p, max_tiles, stream);
+      else
+        return launch_lds_cfg<I8, EPI, 8, 6, 2, 3, 0, 128>(p, max_tiles, stream);
     default:
       return fail(FCMOE_EINVAL, "unsupported LDS tile rows");
   }

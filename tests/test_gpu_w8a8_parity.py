@@ -196,7 +196,8 @@ def test_w8a8_forward_repeat_bitwise(gpu, oracle_lib):
 def test_w8a8_forward_bit_exact_odd_chunk_counts(gpu, oracle_lib):
     """K = 1040 / 272 (17 / 5 chunks of 64 bytes): the LDS-staged kernel loads
     A two chunks at a time, so its last A stage lies half past K; the 600- and
-    256-row experts run the 256-row tile on it."""
+    256-row experts run the 256-row tiles (W13 on 4-wave workgroups, W2 and
+    the raw-accumulator GEMM on 8-wave ones) on it."""
     case = H.w8a8_case(61, 1200, 1040, 272, 9, 4, skew=1.2)
     _check_w8a8(gpu, oracle_lib, case, shared=True, scale=2.5)
     counts = np.asarray([129, 256, 600, 0, 2], np.int32)

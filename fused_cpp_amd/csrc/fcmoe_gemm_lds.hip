@@ -344,13 +344,16 @@ __global__ __launch_bounds__(WMW * WNW * kWave) void grouped_gemm_lds_kernel(Gem
     voff_a[u] = (uint32_t)(arow * lda_bytes + unit * 16);
     lds_a[u] = g * 1024;
   }
+  // B: a load's tile is the same for the whole wave, so its offset goes in
+  // the scalar operand and every B load shares one lane offset register.
+  const uint32_t voff_lane = (uint32_t)lane * 16;
 #pragma unroll
   for (int u = 0; u < LPB; ++u) {
     int t = wave + WAVES * u;
     while (t >= LB) t -= LB;
     bool valid;
     const int64_t gt = tile_of(t / FN, t % FN, &valid);
-    voff_b[u] = (uint32_t)((valid ? gt : 0) * kc * 1024 + lane * 16);
+    voff_b[u] = (uint32_t)__builtin_amdgcn_readfirstlane((int)((valid ? gt : 0) * kc * 1024));
     lds_b[u] = t * 1024;
   }
   // Past the end a ring re-loads the last chunk (never read).
@@ -373,7 +376,7 @@ __global__ __launch_bounds__(WMW * WNW * kWave) void grouped_gemm_lds_kernel(Gem
 #pragma unroll
     for (int u = 0; u < LPB; ++u)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_b, (lds_ptr_t)(smem_b + stage * B_BYTES + lds_b[u]), 16,
-                                               voff_b[u], soff, 0, BPOL);
+                                               voff_lane, (int)voff_b[u] + soff, 0, BPOL);
   };
 
   // ---- fragment addresses (bytes within a stage)
@@ -565,14 +568,21 @@ int launch_lds_bm(int bm, const GemmParams& p, int64_t max_tiles, hipStream_t st
   // W2 bm256 0.63 -> 0.66 ms with nontemporal weights).
   constexpr int kNT = 2;  // buffer-load cache policy bit: nontemporal
   // A stages are 128 bytes of K (two chunks, full-line loads) where the
-  // register budget allows it; the 192-row tile would spill with them.
+  // register budget allows it.
   // A stages are 128 bytes of K (two chunks, full-line loads) where the
-  // register budget allows it; the 192-row tile would spill with them.
+  // register budget allows it.
   switch (bm) {
     case 128:
       return launch_lds_cfg<I8, EPI, 4, 8, 2, 3, kNT, 128>(p, max_tiles, stream);
     case 192:
-      return launch_lds_cfg<I8, EPI, 6, 8, 3, 3, kNT, 64>(p, max_tiles, stream);
+      // 128-byte A stages cut C4's W13 bm192 (streaming 11.3 GB of weights)
+      // from 2.33 to 2.10 ms: fewer L2 requests per A byte leave more of the
+      // CU's outstanding-request budget to the weight stream. The bf16
+      // epilogues would spill with them and keep 64-byte A stages.
+      if constexpr (I8)
+        return launch_lds_cfg<I8, EPI, 6, 8, 2, 3, kNT, 128>(p, max_tiles, stream);
+      else
+        return launch_lds_cfg<I8, EPI, 6, 8, 3, 3, kNT, 64>(p, max_tiles, stream);
     case 256:
       // W13 (gate/up pairs) on 4-wave workgroups, two per CU (2 x 2 waves of
       // 128 x 96, 72 KB of LDS): another workgroup's K loop overlaps each

@@ -70,22 +70,48 @@ __device__ __forceinline__ void wait_vmcnt() {
 constexpr int kXcds = 8;
 constexpr int kLdsGroupTiles = 4;
 
-__device__ __forceinline__ bool lds_work_item(int b, int count, int n_blocks, int gm, int& tile_idx, int& nb) {
-  const int valid = count * n_blocks;
-  if (b >= valid) return false;
+// When the channel dimension does not fill the last channel block (W13 at
+// F = 2048 on the 4-wave 256-row tile: 21 blocks of 6 gate/up pairs and one
+// of 2), those cheaper last-block items run after all full ones, on every
+// XCD: they then fill the slots left in the last round of full items instead
+// of forming a round of their own (C3's 256-row W13: 3080 items on 512
+// slots left 8 items, ~14% of the launch, in a seventh round). Each XCD
+// takes its share of the full items, in the order above, then its share of
+// the last-block items; the grid carries kXcds spare workgroups for the two
+// shares' rounding.
+__device__ __forceinline__ bool lds_work_item(int b, int count, int n_blocks, bool partial, int gm, int& tile_idx,
+                                              int& nb) {
+  const int nbf = partial ? n_blocks - 1 : n_blocks;  // full channel blocks per row tile
+  const int F = count * nbf, P = partial ? count : 0;
+  int l, lp;
   if (gm <= 0) {
-    tile_idx = b / n_blocks;
-    nb = b % n_blocks;
-    return true;
+    if (b < F) {
+      tile_idx = b / nbf;
+      nb = b % nbf;
+      return true;
+    }
+    lp = b - F;
+  } else {
+    const int x = b % kXcds, k = b / kXcds;
+    const int qf = F / kXcds, rf = F % kXcds, qp = P / kXcds, rp = P % kXcds;
+    const int nf = qf + (x < rf ? 1 : 0);
+    if (k < nf) {
+      l = x * qf + (x < rf ? x : rf) + k;
+      const int gsz = gm * nbf;
+      const int g = l / gsz, rr = l % gsz;
+      const int left = count - g * gm;
+      const int gm_eff = left < gm ? left : gm;
+      tile_idx = g * gm + rr % gm_eff;
+      nb = rr / gm_eff;
+      return true;
+    }
+    const int kp = k - nf;
+    if (kp >= qp + (x < rp ? 1 : 0)) return false;
+    lp = x * qp + (x < rp ? x : rp) + kp;
   }
-  const int x = b % kXcds, q = valid / kXcds, r = valid % kXcds;
-  const int l = x * q + (x < r ? x : r) + b / kXcds;
-  const int gsz = gm * n_blocks;
-  const int g = l / gsz, rr = l % gsz;
-  const int left = count - g * gm;
-  const int gm_eff = left < gm ? left : gm;
-  tile_idx = g * gm + rr % gm_eff;
-  nb = rr / gm_eff;
+  if (lp >= P) return false;
+  tile_idx = lp;
+  nb = n_blocks - 1;
   return true;
 }
 
@@ -234,7 +260,7 @@ __device__ __forceinline__ void staged_epilogue(const GemmParams& p, const v4i (
 }
 
 template <bool I8, int EPI, int FM, int FN, int SA, int SB, int BPOL, int AW, int WMW, int WNW>
-__global__ __launch_bounds__(WMW * WNW * kWave) void grouped_gemm_lds_kernel(GemmParams p, int n_blocks, int gm) {
+__global__ __launch_bounds__(WMW * WNW * kWave) void grouped_gemm_lds_kernel(GemmParams p, int n_blocks, int partial, int gm) {
   // The body is device-only: the buffer-resource type does not exist for the
   // host target, and the host pass needs only the kernel's signature.
 #if __HIP_DEVICE_COMPILE__
@@ -289,7 +315,7 @@ __global__ __launch_bounds__(WMW * WNW * kWave) void grouped_gemm_lds_kernel(Gem
 
   const int count = *p.tile_count;
   int tile_idx, nb;
-  if (!lds_work_item((int)blockIdx.x, count, n_blocks, gm, tile_idx, nb)) return;
+  if (!lds_work_item((int)blockIdx.x, count, n_blocks, partial != 0, gm, tile_idx, nb)) return;
   const int tile = count - 1 - tile_idx;  // last-first, as the register kernel
   const int expert = p.tiles[2 * tile];
   const int m0 = p.tiles[2 * tile + 1];
@@ -378,6 +404,20 @@ __global__ __launch_bounds__(WMW * WNW * kWave) void grouped_gemm_lds_kernel(Gem
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_b, (lds_ptr_t)(smem_b + stage * B_BYTES + lds_b[u]), 16,
                                                voff_lane, (int)voff_b[u] + soff, 0, BPOL);
   };
+
+  // A wave whose channel tiles all lie past the end (the last channel block
+  // of a launch whose channels do not fill it) skips its MFMAs; it still
+  // issues its share of the loads and meets every barrier. Compiled for the
+  // 6-tile waves only (the 256-row tiles, whose blocks do not divide the
+  // DeepSeek channel counts); elsewhere the branch cost the 192-row tile a
+  // register spill and its blocks divide evenly.
+  bool wave_live = FN != 6;
+#pragma unroll
+  for (int j = 0; j < FN; ++j) {
+    bool v;
+    (void)tile_of(wn, j, &v);
+    wave_live = wave_live || v;
+  }
 
   // ---- fragment addresses (bytes within a stage)
   constexpr int A_FRAG = 16 * AW;  // bytes per 16-row fragment in a stage
@@ -487,14 +527,14 @@ __global__ __launch_bounds__(WMW * WNW * kWave) void grouped_gemm_lds_kernel(Gem
       // everyone is done with chunk c-1: A stage c/2-1 and B stage c-1 are free
       issue_a(c / 2 + 1, sa ^ 1);
       issue_b(c + 2, sb == 0 ? 2 : sb - 1);
-      compute(smem + sa * A_BYTES + a_frag, smem_b + sb * B_BYTES);
+      if (wave_live) compute(smem + sa * A_BYTES + a_frag, smem_b + sb * B_BYTES);
       sb = sb == 2 ? 0 : sb + 1;
       if (c + 1 < kc) {
         wait_vmcnt<WAIT_ODD>();  // B c+1 has landed
         __builtin_amdgcn_s_barrier();
         issue_b(c + 3, sb == 0 ? 2 : sb - 1);
         // second chunk of the stage: units 4..7, i.e. slot bit 2 flipped ((4 | u) ^ x == (u ^ x) ^ 4)
-        compute(smem + sa * A_BYTES + (a_frag ^ 64), smem_b + sb * B_BYTES);
+        if (wave_live) compute(smem + sa * A_BYTES + (a_frag ^ 64), smem_b + sb * B_BYTES);
         sb = sb == 2 ? 0 : sb + 1;
       }
       sa ^= 1;
@@ -507,7 +547,7 @@ __global__ __launch_bounds__(WMW * WNW * kWave) void grouped_gemm_lds_kernel(Gem
       // everyone is done with chunk c-1: its stages take the next chunks
       issue_a(c + SA - 1, sa == 0 ? SA - 1 : sa - 1);
       issue_b(c + SB - 1, sb == 0 ? SB - 1 : sb - 1);
-      compute(smem + sa * A_BYTES + a_frag, smem_b + sb * B_BYTES);
+      if (wave_live) compute(smem + sa * A_BYTES + a_frag, smem_b + sb * B_BYTES);
       sa = sa == SA - 1 ? 0 : sa + 1;
       sb = sb == SB - 1 ? 0 : sb + 1;
     }
@@ -544,8 +584,11 @@ int64_t lds_blocks(int wn, int fn, const GemmParams& p) {
 template <bool I8, int EPI, int FM, int FN, int SA, int SB, int BPOL, int AW, int WMW = kWM, int WNW = kWN>
 int launch_lds_cfg(const GemmParams& p, int64_t max_tiles, hipStream_t stream) {
   const int64_t n_blocks = lds_blocks<EPI>(WNW, FN, p);
-  const int64_t grid = max_tiles * n_blocks;
-  if (grid <= 0) return FCMOE_OK;
+  if (max_tiles * n_blocks <= 0) return FCMOE_OK;
+  constexpr bool PAIR = epi_pair(EPI);
+  const int64_t units = PAIR ? p.n_tiles : (int64_t)p.n_groups * p.n_tiles;
+  const int partial = n_blocks * (PAIR ? WNW * (FN / 2) : WNW * FN) > units ? 1 : 0;
+  const int64_t grid = max_tiles * n_blocks + (partial ? kXcds : 0);
   if (grid > INT32_MAX) return fail(FCMOE_EINVAL, "grouped gemm grid too large");
   // 32-bit buffer offsets: A rows and one expert's packed weights
   if (p.w_expert_bytes >= 0x7ffffff0) return fail(FCMOE_EINVAL, "expert weights exceed 2 GiB");
@@ -554,7 +597,7 @@ int launch_lds_cfg(const GemmParams& p, int64_t max_tiles, hipStream_t stream) {
     return v ? atoi(v) : kLdsGroupTiles;
   }();
   hipLaunchKernelGGL((grouped_gemm_lds_kernel<I8, EPI, FM, FN, SA, SB, BPOL, AW, WMW, WNW>), dim3((unsigned)grid),
-                     dim3(WMW * WNW * kWave), 0, stream, p, (int)n_blocks, gm);
+                     dim3(WMW * WNW * kWave), 0, stream, p, (int)n_blocks, partial, gm);
   return check_launch("grouped_gemm_lds");
 }
 

@@ -1,0 +1,85 @@
+"""Code-generation invariants of the LDS-staged prefill GEMM (fcmoe_gemm_lds.hip).
+
+Compiles the source to gfx950 device assembly with the library's own flags (hipcc
+cross-compiles without a GPU) and checks two properties that the compiler can lose
+silently and that each cost a large share of the kernel's speed when lost:
+
+* the K loop waits on vector memory only through its own staged count(s): one
+  ``s_waitcnt vmcnt(N)`` per chunk (two per pair of chunks when A stages hold two
+  chunks), never ``vmcnt(0)``, which drains the prefetch ring. A second ``__shared__``
+  object once made the compiler insert one per iteration (the K loop of a C4-sized
+  launch went from 151 to 228 us per workgroup);
+* no flat memory instructions: LDS reads typed as generic pointers become flat loads,
+  which wait on vector-memory stores as well.
+"""
+
+from __future__ import annotations
+
+import re
+import subprocess
+
+import pytest
+
+from fused_cpp_amd.build import CSRC, HIP_FLAGS, ROCM
+
+_KERNEL = re.compile(r"^(_Z\w*grouped_gemm_lds_kernel\w*):", re.M)
+
+
+@pytest.fixture(scope="module")
+def lds_asm(tmp_path_factory) -> str:
+    hipcc = ROCM / "bin" / "hipcc"
+    if not hipcc.exists():
+        pytest.skip("hipcc not available")
+    out = tmp_path_factory.mktemp("isa") / "fcmoe_gemm_lds.s"
+    proc = subprocess.run([str(hipcc), *HIP_FLAGS, "--cuda-device-only", "-S", str(CSRC / "fcmoe_gemm_lds.hip"),
+                           "-o", str(out)], capture_output=True, text=True)
+    assert proc.returncode == 0, proc.stdout + proc.stderr
+    return out.read_text()
+
+
+def _kernels(asm: str) -> dict[str, list[str]]:
+    found = {}
+    for m in _KERNEL.finditer(asm):
+        end = asm.index(".Lfunc_end", m.end())
+        found[m.group(1)] = asm[m.end():end].splitlines()
+    return found
+
+
+def _k_loop(body: list[str]) -> list[str]:
+    """The K loop: the smallest backward-branch region holding both MFMAs and a
+    barrier (small set-up loops can be laid out with their latch after it)."""
+    labels = {}
+    best = None
+    for i, line in enumerate(body):
+        s = line.strip()
+        if s.startswith(".LBB") and ":" in s:
+            labels[s.split(":")[0]] = i
+        elif s.startswith("s_cbranch") or s.startswith("s_branch"):
+            target = s.split()[-1]
+            start = labels.get(target)
+            if start is None:
+                continue
+            region = body[start:i]
+            if any("v_mfma" in x for x in region) and any("s_barrier" in x for x in region):
+                if best is None or i - start < best[1] - best[0]:
+                    best = (start, i)
+    assert best is not None, "no K loop found"
+    return body[best[0]:best[1] + 1]
+
+
+def test_lds_kernels_present(lds_asm):
+    names = _kernels(lds_asm)
+    assert len(names) >= 12, sorted(names)
+
+
+def test_k_loop_waits_on_its_own_stage_count(lds_asm):
+    for name, body in _kernels(lds_asm).items():
+        waits = [int(m.group(1)) for line in _k_loop(body) for m in [re.search(r"s_waitcnt vmcnt\((\d+)\)", line)] if m]
+        assert 1 <= len(waits) <= 2, (name, waits)
+        assert all(w > 0 for w in waits), (name, waits)
+
+
+def test_no_flat_memory_instructions(lds_asm):
+    for name, body in _kernels(lds_asm).items():
+        flat = [line.strip() for line in body if line.strip().startswith("flat_")]
+        assert not flat, (name, flat[:3])

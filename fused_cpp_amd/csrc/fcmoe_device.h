@@ -91,9 +91,11 @@ __device__ __forceinline__ float fexpa_exp_neg(float gate) {
 // moves (no LDS crossbar): quad max via quad_perm [1,0,3,2] and [2,3,0,1],
 // then rotations of the row by 4 and 8 lanes fold in the other quads. Every
 // lane ends with the row maximum (max is exact in any order).
+// mov_dpp (no old operand; every source lane here lies inside the row) lets
+// the compiler fold the move into the v_max that consumes it (v_max_f32_dpp).
 template <int CTRL>
 __device__ __forceinline__ float dpp_f(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, true));
 }
 __device__ __forceinline__ float max16(float v) {
   v = fmaxf(v, dpp_f<0xB1>(v));   // quad_perm [1,0,3,2]

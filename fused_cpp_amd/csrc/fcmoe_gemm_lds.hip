@@ -8,26 +8,30 @@
 //     VGPRs, issued at almost no MFMA cost),
 //   * gives each wave a large 16 FM x 16 FN tile (96x128 / 128x96 / 64x128)
 //     so each LDS fragment read feeds FN or FM MFMAs,
-//   * keeps the accumulators in VGPRs at 2 waves per SIMD (8 waves per
-//     workgroup, one workgroup per CU).
+//   * keeps the accumulators in VGPRs at 2 waves per SIMD: 2 x 4 waves per
+//     workgroup and one workgroup per CU, or 2 x 2 waves and two workgroups
+//     per CU (the 256-row W13), whose K loops then overlap each other's
+//     epilogues.
 //
-// Work decomposition: grid.x = tiles * n_blocks; a workgroup computes rows
-// [m0, m0 + BM) of one expert against 4 * FN consecutive 16-channel tiles
-// (W13: 4 * FN/2 gate tiles and the matching up tiles). Waves are 2 (rows) x
-// 4 (channel tiles); the epilogues are the shared gemm_epilogue.
+// Work decomposition: grid.x = tiles * n_blocks (+ spare workgroups, see
+// lds_work_item); a workgroup computes rows [m0, m0 + BM) of one expert
+// against WNW * FN consecutive 16-channel tiles (W13: WNW * FN/2 gate tiles
+// and the matching up tiles). Waves are WMW (rows) x WNW (channel tiles).
 //
-// Pipeline: two LDS rings of 64-byte K chunks, SA stages of the A tile (BM
-// rows) and SB >= SA stages of the workgroup's B tiles, so the weights
-// (streamed from HBM) may run further ahead than A (re-read from L2 by the
-// other channel blocks). Iteration c waits for its own chunk-c loads
-// (vmcnt), meets the other waves at one barrier (their chunk-c loads have
-// landed; everyone is done reading chunk c-1), issues A chunk c+SA-1 and B
-// chunk c+SB-1 into the stages chunk c-1 used and computes chunk c.
+// Pipeline: two LDS rings, SA stages of the A tile (BM rows) and SB >= SA
+// stages of the workgroup's B tiles, one 64-byte K chunk per B stage and
+// AW = 64 or 128 bytes of K per A stage. Iteration c waits for its own
+// chunk-c loads (vmcnt), meets the other waves at one barrier (their chunk-c
+// loads have landed; everyone is done reading chunk c-1), issues the next A
+// and B stages into the ones chunk c-1 freed and computes chunk c.
 //
-// LDS layouts (per stage): A rows packed 64 bytes apart, the four 16-byte
-// units of row r stored at slot (unit ^ ((r >> 2) & 3)) so the 16 rows of a
-// fragment read fall on distinct banks; B tiles in their packed MFMA operand
-// order (1 KB per tile chunk, lane l's 16 bytes at 16 l).
+// LDS layouts (per stage): A rows packed AW bytes apart, 16-byte unit u of
+// row r at slot u ^ ((r >> 2) & 3) (AW = 64) or u ^ ((r >> 1) & 7) (AW =
+// 128), so the 16 rows of a fragment read fall on distinct banks; B tiles in
+// their packed MFMA operand order (1 KB per tile chunk, lane l's 16 bytes at
+// 16 l). The epilogue's per-row and per-channel values follow the rings in
+// the same LDS object, and the epilogue stages its output through the idle
+// ring memory (staged_epilogue).
 #include <cstdlib>
 #include <utility>
 
@@ -39,9 +43,6 @@ namespace {
 
 constexpr int kWM = 2;
 constexpr int kWN = 4;
-constexpr int kWaves = kWM * kWN;
-constexpr int kThreadsLds = kWaves * kWave;
-constexpr int kStages = 3;
 // Raw buffer resource word 3 for gfx9: 32-bit data format, no swizzle.
 constexpr int kBufWord3 = 0x00020000;
 
@@ -343,10 +344,11 @@ __global__ __launch_bounds__(WMW * WNW * kWave) void grouped_gemm_lds_kernel(Gem
     }
   };
 
-  // ---- buffer resources and this wave's loads per chunk: A loads g = wave,
-  // wave + 8, ... (rows [16 g, 16 g + 16)), B loads likewise over the NT
-  // tiles; indices past the count repeat an earlier load (same bytes to the
-  // same place) so every wave issues exactly LPA + LPB loads.
+  // ---- buffer resources and this wave's loads per stage: A loads g = wave,
+  // wave + WAVES, ... (1 KB each: 16 rows x 64 bytes, or 8 rows x 128
+  // bytes), B loads likewise over the NT tiles; indices past the count repeat
+  // an earlier load (same bytes to the same place) so every wave issues
+  // exactly LPA + LPB loads.
   const int64_t lda_bytes = p.lda * (I8 ? 1 : 2);
   const __amdgpu_buffer_rsrc_t rsrc_a =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p.a), (short)0, 0x7ffffff0, kBufWord3);

@@ -391,6 +391,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
+    ap.add_argument("--tokens", type=int, default=0,
+                    help="override the config's token count (e.g. small-batch decode on the C2 shape)")
     ap.add_argument("--prefill", action="store_true", help="also measure C3 prefill as 'secondary'")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--graph", action="store_true",
@@ -419,6 +421,8 @@ def main() -> int:
 
     device = torch.device("cuda", 0)
     cfg = CONFIGS[args.config]
+    if args.tokens > 0:
+        cfg = dict(cfg, T=args.tokens, desc=f"{cfg['desc']} (T overridden to {args.tokens})")
     res = measure(cfg, args, device, want_cpu=not args.no_cpu_baseline)
     line = {
         "metric": {"w8a8": "W8A8", "w8a16": "W8A16", "bf16": "BF16"}[cfg["kind"]] + " MoE-layer tokens/s",

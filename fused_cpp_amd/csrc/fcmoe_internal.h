@@ -43,6 +43,7 @@ TileClasses make_tile_classes(const int* bms, int n, int64_t routes, int64_t exp
 
 struct RouteBuffers {
   int32_t* chunk_hist = nullptr;     // [chunks, experts]
+  int32_t* chunk_invalid = nullptr;  // [chunks] invalid ids per chunk (multi-kernel path)
   int32_t* counts = nullptr;         // [experts]
   int32_t* offsets = nullptr;        // [experts + 1]
   int32_t* sorted_routes = nullptr;  // [routes]  sorted position -> flat route

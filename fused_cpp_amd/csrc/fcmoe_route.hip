@@ -66,11 +66,16 @@ __device__ __forceinline__ float route_weight_of(const RouteArgs& a, int64_t r) 
   return w;
 }
 
+// Invalid ids are counted per chunk (chunk_invalid, plain stores) and summed
+// by the scan kernel, which writes the total: the caller's counter needs no
+// zeroing launch beforehand.
 __global__ __launch_bounds__(kRouteChunk) void route_count_kernel(RouteArgs a, int64_t routes, int32_t* chunk_hist,
-                                                                   float* route_weight, int32_t* invalid) {
+                                                                   float* route_weight, int32_t* chunk_invalid) {
   extern __shared__ int32_t hist[];
+  __shared__ int32_t n_invalid;
   const int tid = threadIdx.x;
   for (int e = tid; e < a.experts; e += kRouteChunk) hist[e] = 0;
+  if (tid == 0) n_invalid = 0;
   __syncthreads();
   const int64_t r = (int64_t)blockIdx.x * kRouteChunk + tid;
   if (r < routes) {
@@ -80,9 +85,10 @@ __global__ __launch_bounds__(kRouteChunk) void route_count_kernel(RouteArgs a, i
     if (valid)
       atomicAdd(&hist[e], 1);
     else
-      atomicAdd(invalid, 1);
+      atomicAdd(&n_invalid, 1);
   }
   __syncthreads();
+  if (tid == 0) chunk_invalid[blockIdx.x] = n_invalid;
   int32_t* dst = chunk_hist + (int64_t)blockIdx.x * a.experts;
   for (int e = tid; e < a.experts; e += kRouteChunk) dst[e] = hist[e];
 }
@@ -168,9 +174,17 @@ constexpr int kScanBatch = 16;
 __global__ __launch_bounds__(kScanThreads) void route_scan_kernel(int experts, int64_t chunks, int32_t* chunk_hist,
                                                                    int32_t* counts, int32_t* offsets,
                                                                    ClassArgs cls, int32_t* tiles,
-                                                                   int32_t* tile_count) {
+                                                                   int32_t* tile_count, const int32_t* chunk_invalid,
+                                                                   int32_t* invalid) {
   __shared__ int seg_sum[kScanThreads];
   const int tid = threadIdx.x;
+  {
+    int v = 0;
+    for (int64_t c = tid; c < chunks; c += kScanThreads) v += chunk_invalid[c];
+    int total;
+    block_exclusive_scan(v, &total);
+    if (tid == 0) *invalid = total;
+  }
   const int segs = kScanThreads / experts;  // >= 1: experts <= kScanThreads
   const int e = tid % experts, sg = tid / experts;
   const bool active = sg < segs;
@@ -270,8 +284,10 @@ __global__ __launch_bounds__(kScanThreads) void route_small_kernel(RouteArgs a, 
                                                                    float* route_weight, int32_t* invalid) {
   __shared__ int32_t hist[kMaxExperts];
   __shared__ __attribute__((aligned(16))) int32_t ex[kScanThreads];
+  __shared__ int32_t n_invalid;
   const int tid = threadIdx.x;
   hist[tid] = 0;  // kMaxExperts == kScanThreads
+  if (tid == 0) n_invalid = 0;
   int e = -1;
   if (tid < routes) {
     bool valid;
@@ -284,9 +300,10 @@ __global__ __launch_bounds__(kScanThreads) void route_small_kernel(RouteArgs a, 
     if (e >= 0)
       atomicAdd(&hist[e], 1);
     else
-      atomicAdd(invalid, 1);
+      atomicAdd(&n_invalid, 1);
   }
   __syncthreads();
+  if (tid == 0) *invalid = n_invalid;  // the count is written, not accumulated
   const bool owner = tid < a.experts;
   const int count = owner ? hist[tid] : 0;
   int total;
@@ -358,6 +375,7 @@ TileClasses make_tile_classes(const int* bms, int n, int64_t routes, int64_t exp
 void route_take(Arena& ar, RouteBuffers& rb, int64_t routes, int64_t experts, const TileClasses& tc) {
   const int64_t chunks = ceil_div(routes, kRouteChunk);
   rb.chunk_hist = ar.take<int32_t>(chunks * experts);
+  rb.chunk_invalid = ar.take<int32_t>(chunks);
   rb.counts = ar.take<int32_t>(experts);
   rb.offsets = ar.take<int32_t>(experts + 1);
   rb.sorted_routes = ar.take<int32_t>(routes);
@@ -393,10 +411,6 @@ int route_launch(const void* ids, int ids_is_i64, const float* topk_w, int64_t t
   a.scale_routed = scale_routed ? 1 : 0;
   const int64_t chunks = ceil_div(routes, kRouteChunk);
   int32_t* invalid = invalid_out ? invalid_out : rb.invalid;
-  if (!invalid_out) {
-    const int rc = fill_u32_launch((uint32_t*)rb.invalid, 1, 0u, stream);
-    if (rc) return rc;
-  }
   const ClassArgs ca = class_args(tc);
   if (routes <= kScanThreads) {
     hipLaunchKernelGGL(route_small_kernel, dim3(1), dim3(kScanThreads), 0, stream, a, (int)routes, rb.counts,
@@ -405,9 +419,9 @@ int route_launch(const void* ids, int ids_is_i64, const float* topk_w, int64_t t
     return check_launch("route");
   }
   hipLaunchKernelGGL(route_count_kernel, dim3((unsigned)chunks), dim3(kRouteChunk), experts * sizeof(int32_t),
-                     stream, a, routes, rb.chunk_hist, rb.route_weight, invalid);
+                     stream, a, routes, rb.chunk_hist, rb.route_weight, rb.chunk_invalid);
   hipLaunchKernelGGL(route_scan_kernel, dim3(1), dim3(kScanThreads), 0, stream, (int)experts, chunks,
-                     rb.chunk_hist, rb.counts, rb.offsets, ca, rb.tiles, rb.tile_count);
+                     rb.chunk_hist, rb.counts, rb.offsets, ca, rb.tiles, rb.tile_count, rb.chunk_invalid, invalid);
   hipLaunchKernelGGL(route_scatter_kernel, dim3((unsigned)chunks), dim3(kRouteChunk), 0, stream, a, routes,
                      rb.chunk_hist, rb.offsets, rb.sorted_routes, rb.row_token, rb.route_pos);
   return check_launch("route");

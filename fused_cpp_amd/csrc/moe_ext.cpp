@@ -211,7 +211,7 @@ at::Tensor w8a8_forward(at::Tensor input, at::Tensor w13, int64_t w13_k, int64_t
                   w2.size(1) == fcmoe_packed_expert_bytes(1, w2_n, w2_k, 1),
               "W8A8 packed weight strides are invalid");
   at::Tensor output = output_for(input, out);
-  at::Tensor invalid = at::zeros({1}, input.options().dtype(at::kInt));
+  at::Tensor invalid = at::empty({1}, input.options().dtype(at::kInt));  // written by the route kernel
   fcmoe_moe_args a = base_args(input, topk_weights, topk_ids, e, shared_id, routed_scale, global_num_experts, output);
   a.inter = w2_k;
   a.w13 = w13.data_ptr();
@@ -275,7 +275,7 @@ at::Tensor bf16_forward(at::Tensor input, at::Tensor w13, int64_t w13_k, int64_t
   at::Tensor output = output_for(input, out);
   at::Tensor b13 = bias_f32(w13_bias, e, w13_n, input);
   at::Tensor b2 = bias_f32(w2_bias, e, w2_n, input);
-  at::Tensor invalid = at::zeros({1}, input.options().dtype(at::kInt));
+  at::Tensor invalid = at::empty({1}, input.options().dtype(at::kInt));  // written by the route kernel
   fcmoe_moe_args a = base_args(input, topk_weights, topk_ids, e, shared_id, routed_scale, global_num_experts, output);
   a.inter = w2_k;
   a.w13 = w13.data_ptr();
@@ -313,7 +313,7 @@ at::Tensor w8a16_forward(at::Tensor input, at::Tensor w13, int64_t w13_k, int64_
                   w2.size(1) == fcmoe_packed_expert_bytes(1, w2_n, w2_k, 1),
               "W8A16 packed weight strides are invalid");
   at::Tensor output = output_for(input, out);
-  at::Tensor invalid = at::zeros({1}, input.options().dtype(at::kInt));
+  at::Tensor invalid = at::empty({1}, input.options().dtype(at::kInt));  // written by the route kernel
   fcmoe_moe_args a = base_args(input, topk_weights, topk_ids, e, shared_id, routed_scale, global_num_experts, output);
   a.inter = w2_k;
   a.w13 = w13.data_ptr();

@@ -70,7 +70,8 @@ int fcmoe_pack_experts(const void* src, int elem_bytes, int64_t experts, int64_t
  * Replaces the route build of csrc/moe/arm/i8mm_w8a8/kernels.cpp:583-592 and
  * csrc/moe/arm/common/fused_moe_bf16_tiled.cpp:6454-6483. Outputs (device):
  * counts [experts], offsets [experts+1], sorted_routes [tokens*kt] (first
- * offsets[experts] valid), invalid_count [1] (ids outside [0, experts)).
+ * offsets[experts] valid), invalid_count [1] (the number of ids outside
+ * [0, experts); written, so it needs no zeroing beforehand).
  * workspace: fcmoe_route_workspace_bytes(). */
 size_t fcmoe_route_workspace_bytes(int64_t tokens, int64_t top_k, int64_t experts, int64_t shared_id);
 int fcmoe_route_build(const void* topk_ids, int ids_is_i64, int64_t tokens, int64_t top_k, int64_t experts,
@@ -124,7 +125,7 @@ typedef struct fcmoe_moe_args {
   int skip_weighted;          /* BF16 only, requires top_k == 1 and no shared expert */
   /* output */
   uint16_t* out;              /* [tokens, hidden] bf16 */
-  int32_t* invalid_count;     /* optional device int32 [1]: += number of invalid ids */
+  int32_t* invalid_count;     /* optional device int32 [1]: set to the number of invalid ids */
   void* workspace;
   size_t workspace_bytes;
 } fcmoe_moe_args;

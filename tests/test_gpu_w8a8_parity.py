@@ -214,12 +214,10 @@ def test_w8a8_forward_bit_exact_odd_chunk_counts(gpu, oracle_lib):
 
 
 @pytest.mark.parametrize("tokens", [1, 2, 5])
-def test_w8a8_forward_bit_exact_small_batch_split_k(gpu, oracle_lib, tokens):
-    """Small-batch decode: too few (tile, channel block) items to fill the GPU,
-    so the decode GEMMs split K over up to four workgroups and the last to
-    arrive sums the int32 partials (W13: 64 K chunks, W2: 32).
-    Bit-exact against the oracle, and repeatable (the arrival counters are
-    cleared between launches)."""
+def test_w8a8_forward_bit_exact_small_batch(gpu, oracle_lib, tokens):
+    """Small-batch decode (1-5 tokens, 4 routed experts each plus the shared
+    one): one-row tiles, most tile rows padding. Bit-exact against
+    the oracle, and repeatable across two calls."""
     case = H.w8a8_case(700 + tokens, tokens, 4096, 2048, 17, 4)
     a = _check_w8a8(gpu, oracle_lib, case, shared=True, scale=2.5)
     b = _check_w8a8(gpu, oracle_lib, case, shared=True, scale=2.5)

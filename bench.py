@@ -385,6 +385,32 @@ def measure(cfg, args, device, want_cpu: bool):
     return out
 
 
+def int_mm_reference() -> int:
+    """hipBLASLt int8 GEMM throughput at the shapes of C3/C4's large experts:
+    W13 of a 4096/2048/1792-row expert ([M, 7168] x [7168, 4096]), W2 of the
+    shared expert ([4096, 2048] x [2048, 7168]) and C4's shared W13 (8192 rows)."""
+    import torch
+
+    dev = torch.device("cuda", 0)
+    out = []
+    for m, k, n in [(4096, 7168, 4096), (2048, 7168, 4096), (1792, 7168, 4096), (4096, 2048, 7168),
+                    (8192, 7168, 4096)]:
+        a = torch.randint(-127, 128, (m, k), dtype=torch.int8, device=dev)
+        b = torch.randint(-127, 128, (n, k), dtype=torch.int8, device=dev).t()
+        for _ in range(3):
+            torch._int_mm(a, b)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(20):
+            torch._int_mm(a, b)
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / 20
+        out.append({"m": m, "k": k, "n": n, "us": round(ms * 1e3, 1), "TOPS": round(2 * m * k * n / ms / 1e9)})
+    print(json.dumps({"int_mm_reference": out}))
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -401,7 +427,13 @@ def main() -> int:
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 256 MiB device copy 5 times (scale reference for rocprofv3 "
                          "FETCH_SIZE / WRITE_SIZE counters)")
+    ap.add_argument("--int-mm-reference", action="store_true",
+                    help="only time the vendor int8 GEMM (torch._int_mm -> hipBLASLt, int32 out, no gather "
+                         "or epilogue) at the prefill experts' shapes, as a reference point for the grouped "
+                         "kernels' TOPS")
     args = ap.parse_args()
+    if args.int_mm_reference:
+        return int_mm_reference()
     if args.copy_calibration:
         import torch
 

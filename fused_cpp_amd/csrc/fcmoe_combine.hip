@@ -46,10 +46,13 @@ __device__ __forceinline__ float tree_merge(const float* route_out, const float*
 // loads, 8-byte bf16 stores; else 1). Each channel's arithmetic is identical
 // to the scalar form.
 // Route rows are read exactly once: nontemporal loads stream them past the
-// caches. The ordered merge issues the loads of up to kSlotBatch slots before
-// its FMA chain (slot order unchanged), so a thread waits one memory round
-// trip per batch instead of one per slot. Tokens run grid-stride over y.
-constexpr int kSlotBatch = 8;
+// caches. The ordered merge issues every load of up to kSlotBatch slots (row,
+// position, weight) before its FMA chain (slot order unchanged), so a thread
+// waits one memory round trip per batch. A row is loaded whatever its
+// position says (rows t*kt + s always lie inside route_out) and a dropped
+// route's row, which was never written, is left out by the select, not by
+// a multiply. Tokens run grid-stride over y.
+constexpr int kSlotBatch = 16;
 typedef float v4f __attribute__((ext_vector_type(4)));
 
 template <int VW>
@@ -98,20 +101,21 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* route_out, co
     for (int s0 = 0; s0 < kt; s0 += kSlotBatch) {
       float v[kSlotBatch][VW];
       float w[kSlotBatch];
-      bool ok[kSlotBatch];
+      int pos[kSlotBatch];
 #pragma unroll
       for (int u = 0; u < kSlotBatch; ++u) {
         const int64_t r = r0 + s0 + u;
-        ok[u] = s0 + u < kt && route_pos[r] >= 0;  // dropped (invalid) routes hold no row
+        pos[u] = -1;
         w[u] = 0.0f;
-        if (ok[u]) {
+        if (s0 + u < kt) {  // uniform over the grid
+          pos[u] = route_pos[r];
           w[u] = route_weight[r];
           load(r, v[u]);
         }
       }
 #pragma unroll
       for (int u = 0; u < kSlotBatch; ++u)
-        if (ok[u]) {
+        if (pos[u] >= 0) {  // dropped (invalid) routes hold no row
 #pragma unroll
           for (int c = 0; c < VW; ++c) acc[c] = __builtin_fmaf(v[u][c], w[u], acc[c]);
         }

@@ -335,21 +335,12 @@ def measured_traffic(config: str, stage: str):
         return None
 
 
-def measure(cfg, args, device, want_cpu: bool):
-    res = run_gpu(cfg, args.steps, args.warmup, device, keep_host=want_cpu or cfg["kind"] == "w8a8",
-                  graph=args.graph)
-    counts = expert_counts(cfg, res["ids"])
-    layer_bytes, layer_ops, st_alg = algorithmic(cfg, counts)
-    ms = res["ms"]
-    # dominant kernel: largest per-step GPU time among GEMM stages
-    best = None
-    for name, (tot, n) in res["stages"].items():
-        if name in st_alg and (best is None or tot > best[1]):
-            best = (name, tot, n)
+def kernel_roofline(args, best, st_alg, peak_ops):
+    """Roofline of the dominant GEMM stage: its algorithmic bytes or ops over its
+    average launch time (library hipEvents on the launch stream)."""
     name, tot, n = best
     avg_ms = tot / n
     a = st_alg[name]
-    peak_ops = INT8_PEAK_TOPS if cfg["kind"] == "w8a8" else BF16_PEAK_TFLOPS
     t_bytes = a["bytes"] / (HBM_PEAK_GBPS * 1e9)
     t_ops = a["ops"] / (peak_ops * 1e12)
     if t_bytes >= t_ops:
@@ -364,6 +355,24 @@ def measure(cfg, args, device, want_cpu: bool):
     roof.update({"kernel": f"grouped_gemm {name}", "avg_launch_ms": round(avg_ms, 4), "traffic": traffic,
                  "algorithmic_bytes": a["bytes"], "algorithmic_ops": a["ops"], "experts": a["experts"],
                  "rows": a["rows"]})
+    return roof
+
+
+def measure(cfg, args, device, want_cpu: bool):
+    res = run_gpu(cfg, args.steps, args.warmup, device, keep_host=want_cpu or cfg["kind"] == "w8a8",
+                  graph=args.graph)
+    counts = expert_counts(cfg, res["ids"])
+    layer_bytes, layer_ops, st_alg = algorithmic(cfg, counts)
+    ms = res["ms"]
+    # dominant kernel: largest per-step GPU time among GEMM stages
+    best = None
+    for name, (tot, n) in res["stages"].items():
+        if name in st_alg and (best is None or tot > best[1]):
+            best = (name, tot, n)
+    peak_ops = INT8_PEAK_TOPS if cfg["kind"] == "w8a8" else BF16_PEAK_TFLOPS
+    roof = None
+    if best is not None:  # stage classes outside this model (W8A16 at prefill): no kernel roofline
+        roof = kernel_roofline(args, best, st_alg, peak_ops)
     layer_roof_s = max(layer_bytes / (HBM_PEAK_GBPS * 1e9), layer_ops / (peak_ops * 1e12))
     layer = {
         "bytes": layer_bytes, "ops": layer_ops, "active_experts": int((counts > 0).sum()),

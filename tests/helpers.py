@@ -101,7 +101,8 @@ def gpu_route_build(ids: np.ndarray, experts: int, shared_id: int, device, ids_i
     counts = torch.empty(experts, dtype=torch.int32, device=device)
     offsets = torch.empty(experts + 1, dtype=torch.int32, device=device)
     sorted_routes = torch.full((tokens * kt,), -1, dtype=torch.int32, device=device)
-    invalid = torch.zeros(1, dtype=torch.int32, device=device)
+    # a stale value: the route build writes the count, it does not add to it
+    invalid = torch.full((1,), 12345, dtype=torch.int32, device=device)
     wsb = L.fcmoe_route_workspace_bytes(tokens, top_k, experts, shared_id)
     ws = torch.empty(wsb, dtype=torch.uint8, device=device)
     cabi.check(L.fcmoe_route_build(ids_t.data_ptr(), 1 if ids_i64 else 0, tokens, top_k, experts, shared_id,

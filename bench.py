@@ -155,14 +155,19 @@ def expert_counts(cfg, ids):
     return counts
 
 
-def class_of(c: int, decode: bool) -> int:
-    """Tile class the GPU selector assigns to an expert with c rows (fcmoe_api.hip select_classes)."""
+CLASS_BM_W8 = (16, 32, 128, 256)  # W8A16 tile classes
+
+
+def class_of(c: int, decode: bool, kind: str = "w8a8") -> int:
+    """Tile class (its index in CLASS_BM) the GPU selector assigns to an expert
+    with c rows (fcmoe_api.hip select_classes; W8A16 uses its own class set)."""
     if decode:
         return 0
-    for i, bm in enumerate(CLASS_BM):
+    bms = CLASS_BM_W8 if kind == "w8a16" else CLASS_BM
+    for bm in bms:
         if c <= bm:
-            return i
-    return len(CLASS_BM) - 1
+            return CLASS_BM.index(bm)
+    return CLASS_BM.index(bms[-1])
 
 
 def algorithmic(cfg, counts):
@@ -181,7 +186,7 @@ def algorithmic(cfg, counts):
     stages = {}
     decode = rows <= 8 * len(counts)
     for c in range(len(CLASS_BM)):
-        sel = (counts > 0) & (np.array([class_of(int(x), decode) for x in counts]) == c)
+        sel = (counts > 0) & (np.array([class_of(int(x), decode, cfg["kind"]) for x in counts]) == c)
         n_exp, r = int(sel.sum()), int(counts[sel].sum())
         if n_exp == 0:
             continue

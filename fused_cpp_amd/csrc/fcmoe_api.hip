@@ -28,6 +28,14 @@ constexpr int kNumClasses = 6;
 // L2 / Infinity Cache, not HBM, since its tiles run side by side).
 constexpr int kDecodeRowsPerExpert = 8;
 
+// Stage-timing slot of a class: the index of its BM in kClassBM, so a stage
+// is named by its tile rows whatever class set the forward uses.
+int class_slot(int bm) {
+  for (int i = 0; i < kNumClasses; ++i)
+    if (kClassBM[i] == bm) return i;
+  return kNumClasses - 1;
+}
+
 TileClasses select_classes(int64_t routes, int64_t experts) {
   if (routes <= kDecodeRowsPerExpert * experts) return make_tile_classes(kClassBM, 1, routes, experts);
   return make_tile_classes(kClassBM, kNumClasses, routes, experts);
@@ -101,7 +109,10 @@ W8A8Layout w8a8_layout(const fcmoe_moe_args* a, Arena& ar) {
 
 // BF16 and W8A16 share this layout. K is padded to the GEMM's K chunk: 32
 // bf16 elements (64 bytes) for bf16 weights, 64 elements for int8 weights.
-// W8A16 streams weights on the direct-A kernel only: tile classes 16 / 32.
+// W8A16 tile classes: 16 / 32 rows on the direct-A kernel, 128 / 256 rows on
+// the LDS-staged kernel (no 64- or 192-row W8A16 tile).
+constexpr int kClassBMW8[] = {16, 32, 128, 256};
+constexpr int kNumClassesW8 = 4;
 Bf16Layout bf16_layout(const fcmoe_moe_args* a, Arena& ar, bool w8 = false) {
   Bf16Layout L;
   const int64_t kmul = w8 ? 64 : 32;
@@ -111,7 +122,8 @@ Bf16Layout bf16_layout(const fcmoe_moe_args* a, Arena& ar, bool w8 = false) {
   L.ip = round_up(a->inter, kmul);
   L.gu_ld = 2 * round_up(a->inter, 16);
   if (w8)
-    L.tc = make_tile_classes(kClassBM, L.routes <= kDecodeRowsPerExpert * a->experts ? 1 : 2, L.routes, a->experts);
+    L.tc = make_tile_classes(kClassBMW8, L.routes <= kDecodeRowsPerExpert * a->experts ? 1 : kNumClassesW8, L.routes,
+                             a->experts);
   else
     L.tc = select_classes(L.routes, a->experts);
   route_take(ar, L.rb, L.routes, a->experts, L.tc);
@@ -520,7 +532,7 @@ int bf16_family_forward(const fcmoe_moe_args* a, hipStream_t stream, bool w8) {
     GemmParams p = g13;
     p.tiles = L.rb.tiles + 2 * tile_offset(L.tc, c);
     p.tile_count = L.rb.tile_count + c;
-    Stage st(FCMOE_STAGE_W13_CLASS0 + c, s);
+    Stage st(FCMOE_STAGE_W13_CLASS0 + class_slot(L.tc.bm[c]), s);
     return gemm_launch(epi13, L.tc.bm[c], p, L.tc.bound[c], s);
   });
   if (rc) return rc;
@@ -550,7 +562,7 @@ int bf16_family_forward(const fcmoe_moe_args* a, hipStream_t stream, bool w8) {
     GemmParams p = g2;
     p.tiles = L.rb.tiles + 2 * tile_offset(L.tc, c);
     p.tile_count = L.rb.tile_count + c;
-    Stage st(FCMOE_STAGE_W2_CLASS0 + c, s);
+    Stage st(FCMOE_STAGE_W2_CLASS0 + class_slot(L.tc.bm[c]), s);
     return gemm_launch(w8 ? kEpiW2RouteW8 : kEpiW2RouteBf16, L.tc.bm[c], p, L.tc.bound[c], s);
   });
   if (rc) return rc;

@@ -323,7 +323,8 @@ int launch_bm(int bm, const GemmParams& p, int64_t max_tiles, hipStream_t stream
   }
 }
 
-// W8A16 is a weight-streaming (decode) path: direct-A tiles of 16 or 32 rows.
+// W8A16 on the direct-A kernel: tiles of 16 or 32 rows (decode and the
+// small prefill classes; 128 and 256 rows run on the LDS-staged kernel).
 template <int EPI>
 int launch_bm_w8(int bm, const GemmParams& p, int64_t max_tiles, hipStream_t stream) {
   switch (bm) {
@@ -346,13 +347,14 @@ int launch_bm_w8(int bm, const GemmParams& p, int64_t max_tiles, hipStream_t str
 }  // namespace
 
 int gemm_launch(int epi, int bm, const GemmParams& p, int64_t max_tiles, hipStream_t stream) {
-  if (epi == kEpiW13ActW8) return launch_bm_w8<kEpiW13ActW8>(bm, p, max_tiles, stream);
-  if (epi == kEpiW2RouteW8) return launch_bm_w8<kEpiW2RouteW8>(bm, p, max_tiles, stream);
   static const bool use_lds = [] {
     const char* v = getenv("FCMOE_GEMM_LDS");
     return !(v && v[0] == '0');
   }();
-  if (use_lds && bm >= 128) return gemm_lds_launch(epi, bm, p, max_tiles, stream);
+  // (W8A16 has no register-ring tile above 32 rows)
+  if (bm >= 128 && (use_lds || epi_w8(epi))) return gemm_lds_launch(epi, bm, p, max_tiles, stream);
+  if (epi == kEpiW13ActW8) return launch_bm_w8<kEpiW13ActW8>(bm, p, max_tiles, stream);
+  if (epi == kEpiW2RouteW8) return launch_bm_w8<kEpiW2RouteW8>(bm, p, max_tiles, stream);
   switch (epi) {
     case kEpiRawI32:
       return launch_bm<true, kEpiRawI32>(bm, p, max_tiles, stream);

@@ -63,21 +63,22 @@ __host__ __device__ constexpr bool epi_pair(int epi) {
 __host__ __device__ constexpr bool epi_w8(int epi) { return epi == kEpiW13ActW8 || epi == kEpiW2RouteW8; }
 
 // 16 int8 weights -> two bf16 MFMA operands (bytes 0-7, bytes 8-15), as
-// packed bf16 pairs in 32-bit words. Exact: the bytes are biased to unsigned
-// (x ^ 0x80), converted with v_cvt_f32_ubyteN, un-biased by an exact
-// subtraction of 128, and |q| <= 127 has at most 7 significant bits, so the
-// high 16 bits of the fp32 value are its bf16 value (v_perm packs two).
+// packed bf16 pairs in 32-bit words. Exact: each byte converts to fp32 with
+// one sign-extending byte-select v_cvt_f32_i32 (SDWA), and |q| <= 128 has at
+// most 8 significant bits, so the high 16 bits of the fp32 value are its bf16
+// value (v_perm packs two). Six VALU ops per 4 bytes (a bias-to-unsigned form
+// took twelve).
 __device__ __forceinline__ uint32_t bf16_pair(float lo, float hi) {
   return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
 }
 __device__ __forceinline__ void i8x16_to_bf16(v4i b, v4i& lo, v4i& hi) {
 #pragma unroll
   for (int w = 0; w < 4; ++w) {
-    const uint32_t u = (uint32_t)b[w] ^ 0x80808080u;
-    const float f0 = (float)(u & 0xffu) - 128.0f;
-    const float f1 = (float)((u >> 8) & 0xffu) - 128.0f;
-    const float f2 = (float)((u >> 16) & 0xffu) - 128.0f;
-    const float f3 = (float)(u >> 24) - 128.0f;
+    const uint32_t u = (uint32_t)b[w];
+    const float f0 = (float)(int8_t)u;
+    const float f1 = (float)(int8_t)(u >> 8);
+    const float f2 = (float)(int8_t)(u >> 16);
+    const float f3 = (float)((int32_t)u >> 24);
     const int p0 = (int)bf16_pair(f0, f1), p1 = (int)bf16_pair(f2, f3);
     if (w < 2) {
       lo[2 * w] = p0;

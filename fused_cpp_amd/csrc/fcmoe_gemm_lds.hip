@@ -277,6 +277,13 @@ __global__ __launch_bounds__(WMW * WNW * kWave) void grouped_gemm_lds_kernel(Gem
   // of the time).
   static_assert(AW == 64 || AW == 128, "A stage K width");
   constexpr bool AWIDE = AW == 128;
+  // W8A16: bf16 A rows against int8 weight tiles. A K chunk is 64 elements:
+  // one 128-byte A stage (the AW = 128 layout) per 1 KB weight-tile chunk,
+  // and each chunk runs two bf16 MFMAs per (row fragment, tile) on the
+  // widened weights. With int8 A, an AW = 128 stage holds two chunks.
+  constexpr bool W8 = epi_w8(EPI);
+  static_assert(!W8 || (!I8 && AWIDE), "W8A16 tiles stage 128-byte bf16 A chunks");
+  constexpr bool APAIR = AWIDE && !W8;  // one A stage holds two K chunks
   constexpr int A_BYTES = BM * AW;        // one A stage
   constexpr int B_BYTES = NT * 1024;      // one B stage
   constexpr int LA = BM * AW / 1024;      // A loads (1 KB each) per stage
@@ -293,7 +300,7 @@ __global__ __launch_bounds__(WMW * WNW * kWave) void grouped_gemm_lds_kernel(Gem
   // A c/2 and B c, odd ones for B c (see the loop)
   constexpr int WAIT_EVEN = LPB;
   constexpr int WAIT_ODD = LPA + LPB;
-  static_assert(!AWIDE || (SA == 2 && SB == 3), "wide A runs 2 A stages and 3 B stages");
+  static_assert(!APAIR || (SA == 2 && SB == 3), "paired A stages run 2 A stages and 3 B stages");
   constexpr bool PAIR = epi_pair(EPI);
   constexpr int HP = FN / 2;
   static_assert(SA >= 2 && SB >= SA, "A ring of 2+ stages, B ring at least as deep");
@@ -388,12 +395,12 @@ __global__ __launch_bounds__(WMW * WNW * kWave) void grouped_gemm_lds_kernel(Gem
   // AW = 128: c counts stages (pairs of chunks). With an odd chunk count the
   // last stage's second half lies past K (past the buffer for the last A
   // row): its lanes re-load the first half instead (never read).
-  const int64_t a_stages = AWIDE ? (kc + 1) / 2 : kc;
+  const int64_t a_stages = APAIR ? (kc + 1) / 2 : kc;
   const bool a_hi = AWIDE && ((lane % 8) ^ ((((wave & 1) << 2) | (lane >> 4)) & 7)) >= 4;
   auto issue_a = [&](int64_t c, int stage) {
     const int64_t cc = c < a_stages ? c : a_stages - 1;
     const int soff = (int)(cc * AW);
-    const bool fold = AWIDE && 2 * cc + 1 >= kc;
+    const bool fold = APAIR && 2 * cc + 1 >= kc;
 #pragma unroll
     for (int u = 0; u < LPA; ++u)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_a, (lds_ptr_t)(smem + stage * A_BYTES + lds_a[u]), 16,
@@ -423,8 +430,12 @@ __global__ __launch_bounds__(WMW * WNW * kWave) void grouped_gemm_lds_kernel(Gem
 
   // ---- fragment addresses (bytes within a stage)
   constexpr int A_FRAG = 16 * AW;  // bytes per 16-row fragment in a stage
-  const int a_frag = AWIDE ? (wm * FM * 16 + lane % 16) * 128 + (((lane / 16) ^ ((lane % 16) >> 1)) * 16)
+  // W8A16 reads units 2 g and 2 g + 1 (g = lane / 16) of its row: slots
+  // (2 g) ^ x and ((2 g) ^ x) ^ 1, i.e. a_frag and a_frag + a_dhi.
+  const int a_unit = W8 ? 2 * (lane / 16) : lane / 16;
+  const int a_frag = AWIDE ? (wm * FM * 16 + lane % 16) * 128 + ((a_unit ^ ((lane % 16) >> 1)) * 16)
                            : (wm * FM * 16 + lane % 16) * 64 + (((lane / 16) ^ ((lane % 16) >> 2)) * 16);
+  const int a_dhi = (a_frag ^ 16) - a_frag;
 
   const int b_frag = wn * FN * 1024 + lane * 16;
 
@@ -467,7 +478,7 @@ __global__ __launch_bounds__(WMW * WNW * kWave) void grouped_gemm_lds_kernel(Gem
   // stream from HBM (long latency), A rows are re-read from L2.
   // AW = 128: A stage 0, B 0, B 1; then even iteration c issues A stage
   // c/2 + 1 and B c+2, odd iteration c issues B c+2.
-  if constexpr (AWIDE) {
+  if constexpr (APAIR) {
     issue_a(0, 0);
     issue_b(0, 0);
     issue_b(1, 1);
@@ -521,7 +532,43 @@ __global__ __launch_bounds__(WMW * WNW * kWave) void grouped_gemm_lds_kernel(Gem
     }
     __builtin_amdgcn_sched_barrier(0);
   };
-  if constexpr (AWIDE) {
+  // W8A16 chunk. Lane l's weight bytes are K 16 g .. 16 g + 15 of its column
+  // (g = l / 16); widened, they pair with A units 2 g and 2 g + 1 of its row
+  // (K 16 g .. 16 g + 7 and 16 g + 8 .. 16 g + 15), which sit in adjacent
+  // slots of the swizzled stage (slot (2 g) ^ x and that slot ^ 1). The
+  // weights are widened once per chunk and reused by every row fragment.
+  auto compute_w8 = [&](const uint8_t* sta, const uint8_t* stb) {
+    if constexpr (W8) {
+    v4i bl[FN], bh[FN];
+    v4i af[2][2];
+    {
+      v4i braw[FN];
+#pragma unroll
+      for (int j = 0; j < FN; ++j) braw[j] = *(const v4i*)(stb + b_frag + j * 1024);
+      af[0][0] = *(const v4i*)(sta);
+      af[0][1] = *(const v4i*)(sta + a_dhi);
+      __builtin_amdgcn_sched_group_barrier(0x100, FN + 2, 0);  // the leading LDS reads
+#pragma unroll
+      for (int j = 0; j < FN; ++j) i8x16_to_bf16(braw[j], bl[j], bh[j]);
+    }
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      if (i + 1 < FM) {
+        af[(i + 1) % 2][0] = *(const v4i*)(sta + (i + 1) * A_FRAG);
+        af[(i + 1) % 2][1] = *(const v4i*)(sta + (i + 1) * A_FRAG + a_dhi);
+      }
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        acc[i][j] = mfma(__builtin_bit_cast(v8bf, af[i % 2][0]), __builtin_bit_cast(v8bf, bl[j]), acc[i][j]);
+        acc[i][j] = mfma(__builtin_bit_cast(v8bf, af[i % 2][1]), __builtin_bit_cast(v8bf, bh[j]), acc[i][j]);
+      }
+      if (i + 1 < FM) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // A reads for row i + 1
+      __builtin_amdgcn_sched_group_barrier(0x008, 2 * FN, 0);             // then row i's MFMAs
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  if constexpr (APAIR) {
     int sa = 0, sb = 0;
     for (int64_t c = 0; c < kc; c += 2) {
       wait_vmcnt<WAIT_EVEN>();  // A stage c/2 and B c have landed
@@ -549,7 +596,12 @@ __global__ __launch_bounds__(WMW * WNW * kWave) void grouped_gemm_lds_kernel(Gem
       // everyone is done with chunk c-1: its stages take the next chunks
       issue_a(c + SA - 1, sa == 0 ? SA - 1 : sa - 1);
       issue_b(c + SB - 1, sb == 0 ? SB - 1 : sb - 1);
-      if (wave_live) compute(smem + sa * A_BYTES + a_frag, smem_b + sb * B_BYTES);
+      if (wave_live) {
+        if constexpr (W8)
+          compute_w8(smem + sa * A_BYTES + a_frag, smem_b + sb * B_BYTES);
+        else
+          compute(smem + sa * A_BYTES + a_frag, smem_b + sb * B_BYTES);
+      }
       sa = sa == SA - 1 ? 0 : sa + 1;
       sb = sb == SB - 1 ? 0 : sb + 1;
     }
@@ -642,6 +694,25 @@ int launch_lds_bm(int bm, const GemmParams& p, int64_t max_tiles, hipStream_t st
   }
 }
 
+// W8A16 prefill tiles. The int8 -> bf16 widening is VALU work on the MFMAs'
+// SIMD, done once per chunk and weight tile, so each wave covers 8 row
+// fragments against 4 tiles (two bf16 MFMAs per pair per chunk): the 128-row
+// tile runs 1 x 8 waves, the 256-row tile 2 x 4. As in the int8 classes, the
+// 128-row weights stream nontemporal and the 256-row ones stay cached (their
+// experts' row tiles re-read them).
+template <int EPI>
+int launch_lds_w8(int bm, const GemmParams& p, int64_t max_tiles, hipStream_t stream) {
+  constexpr int kNT = 2;
+  switch (bm) {
+    case 128:
+      return launch_lds_cfg<false, EPI, 8, 4, 2, 3, kNT, 128, 1, 8>(p, max_tiles, stream);
+    case 256:
+      return launch_lds_cfg<false, EPI, 8, 4, 2, 3, 0, 128, 2, 4>(p, max_tiles, stream);
+    default:
+      return fail(FCMOE_EINVAL, "W8A16 LDS tiles are 128 or 256 rows");
+  }
+}
+
 }  // namespace
 
 int gemm_lds_launch(int epi, int bm, const GemmParams& p, int64_t max_tiles, hipStream_t stream) {
@@ -660,6 +731,10 @@ int gemm_lds_launch(int epi, int bm, const GemmParams& p, int64_t max_tiles, hip
       return launch_lds_bm<false, kEpiRawF32Bias>(bm, p, max_tiles, stream);
     case kEpiW2RouteBf16:
       return launch_lds_bm<false, kEpiW2RouteBf16>(bm, p, max_tiles, stream);
+    case kEpiW13ActW8:
+      return launch_lds_w8<kEpiW13ActW8>(bm, p, max_tiles, stream);
+    case kEpiW2RouteW8:
+      return launch_lds_w8<kEpiW2RouteW8>(bm, p, max_tiles, stream);
     default:
       return fail(FCMOE_EINVAL, "unknown epilogue");
   }

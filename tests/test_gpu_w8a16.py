@@ -61,6 +61,24 @@ def test_w8a16_matches_dequantised_fp32_reference(gpu, oracle_lib, activation, l
     _close(out, oracle_lib.bf16_moe_reference(x, deq13, deq2, w, ids, activation=act, round_intermediate=True))
 
 
+@pytest.mark.parametrize("activation", ["silu", "gelu"])
+@pytest.mark.parametrize("T,Hd,F,E,k", [(200, 256, 128, 4, 2), (700, 200, 96, 4, 2), (900, 320, 160, 14, 2)])
+def test_w8a16_prefill_classes(gpu, oracle_lib, activation, T, Hd, F, E, k):
+    """Prefill-sized experts on the LDS-staged W8A16 tiles: ~100 rows per
+    expert (128-row class), ~350 (two 256-row tiles per expert), and a mix of
+    classes with unaligned H (zero-padded K) and a single-chunk W2."""
+    from fused_cpp_amd import moe
+
+    x, _, _, q13, s13, q2, s2, ids, w, deq13, deq2 = _case(oracle_lib, T + 3 * Hd, T, Hd, F, E, k)
+    counts = np.bincount(ids.ravel(), minlength=E)
+    assert counts.max() > 32  # at least one expert beyond the direct-A tiles
+    packed = moe.prepare_fused_moe_w8a16_tiled_quantized_weights(torch.from_numpy(q13), torch.from_numpy(s13),
+                                                                  torch.from_numpy(q2), torch.from_numpy(s2))
+    out = moe.fused_moe_w8a16_tiled(_bf16(x, gpu), packed, torch.from_numpy(w).to(gpu), torch.from_numpy(ids).to(gpu),
+                                    activation=activation)
+    _close(out, oracle_lib.bf16_moe_reference(x, deq13, deq2, w, ids, activation=activation, round_intermediate=True))
+
+
 def test_w8a16_prepare_from_bf16_quantises_like_the_oracle(gpu, oracle_lib):
     from fused_cpp_amd import moe
 

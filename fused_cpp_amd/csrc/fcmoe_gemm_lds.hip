@@ -192,16 +192,24 @@ __device__ __forceinline__ void staged_epilogue(const GemmParams& p, const v4i (
             *(__attribute__((address_space(3))) uint16_t*)(slice + (rq + q0 + b) * RS + (j * 16 + col) * 2) = yb;
             ya[b][j] = rok[b] && fv[j] ? fabsf(bf16_to_f32(yb)) : 0.0f;
           }
+        // Row maxima over the wave's HP gate tiles at once: the lane's own
+        // maximum first, then one 16-lane reduction per row. Each of the
+        // row's HP partial entries gets the group maximum, which leaves the
+        // maximum over all entries, the only thing the requant reads, as is.
+        float ym[QB];
 #pragma unroll
-        for (int b = 0; b < QB; ++b)
+        for (int b = 0; b < QB; ++b) {
+          ym[b] = ya[b][0];
 #pragma unroll
-          for (int j = 0; j < HP; ++j) ya[b][j] = max16(ya[b][j]);
+          for (int j = 1; j < HP; ++j) ym[b] = fmaxf(ym[b], ya[b][j]);
+          ym[b] = max16(ym[b]);
+        }
         if (col == 0) {
 #pragma unroll
           for (int b = 0; b < QB; ++b)
 #pragma unroll
             for (int j = 0; j < HP; ++j)
-              *(__attribute__((address_space(3))) float*)(rp + ((rq + q0 + b) * HP + j) * 4) = ya[b][j];
+              *(__attribute__((address_space(3))) float*)(rp + ((rq + q0 + b) * HP + j) * 4) = ym[b];
         }
       }
 #pragma unroll

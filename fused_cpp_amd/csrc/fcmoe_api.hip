@@ -363,14 +363,17 @@ extern "C" int fcmoe_w8a8_forward(const fcmoe_moe_args* a, hipStream_t stream) {
   if (!ar.ok()) return fail(FCMOE_ESPACE, "W8A8 workspace too small");
   const int64_t H = a->hidden, I = a->inter;
 
+  bool quant_done = false;
   {
+    // At small batch the token rows are quantised in the route launch.
     Stage st(FCMOE_STAGE_ROUTE, stream);
+    const QuantRows qr{a->x, a->tokens, H, 0, L.xq, L.hp, L.xs};
     rc = route_launch(a->topk_ids, a->ids_is_i64, a->topk_weights, a->tokens, a->top_k, a->experts,
                       a->valid_experts, a->shared_expert_id, a->routed_scaling, a->shared_expert_id >= 0, L.rb, L.tc,
-                      a->invalid_count, stream);
+                      a->invalid_count, stream, &qr, &quant_done);
     if (rc) return rc;
   }
-  {
+  if (!quant_done) {
     Stage st(FCMOE_STAGE_QUANT, stream);
     rc = quant_rows_launch(a->x, 0, a->tokens, H, 0, L.xq, L.hp, L.xs, stream);
     if (rc) return rc;

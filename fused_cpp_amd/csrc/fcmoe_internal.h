@@ -56,9 +56,25 @@ struct RouteBuffers {
 };
 constexpr int kRouteChunk = 256;
 void route_take(Arena& a, RouteBuffers& rb, int64_t routes, int64_t experts, const TileClasses& tc);
+// bf16 token rows to quantise (quantize_bf16_row semantics by `rounding`,
+// as quant_rows_launch): at small batch the route kernel takes this job into
+// its own launch.
+struct QuantRows {
+  const uint16_t* x;
+  int64_t rows, cols;
+  int rounding;
+  int8_t* q;
+  int64_t ldq;
+  float* scales;
+};
+// quant / quant_done: optional. When the routing fits the single-workgroup
+// kernel and the rows qualify (cols % 8 == 0, ldq % 8 == 0, cols <= 16384),
+// the rows are quantised in the same launch and *quant_done is set; otherwise
+// *quant_done is false and the caller runs quant_rows_launch.
 int route_launch(const void* ids, int ids_is_i64, const float* topk_w, int64_t tokens, int64_t top_k,
                  int64_t experts, int64_t valid_experts, int64_t shared_id, float routed_scale, bool scale_routed,
-                 const RouteBuffers& rb, const TileClasses& tc, int32_t* invalid_out, hipStream_t stream);
+                 const RouteBuffers& rb, const TileClasses& tc, int32_t* invalid_out, hipStream_t stream,
+                 const QuantRows* quant = nullptr, bool* quant_done = nullptr);
 
 int tiles_from_counts_launch(const int32_t* counts, int64_t experts, const TileClasses& tc, int32_t* tiles,
                              int32_t* tile_count, hipStream_t stream);

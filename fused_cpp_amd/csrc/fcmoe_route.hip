@@ -17,6 +17,7 @@
 //               routes of the same expert gives its stable sorted position.
 #include "fcmoe_device.h"
 #include "fcmoe_internal.h"
+#include "fcmoe_quant_row.h"
 
 namespace fcmoe {
 
@@ -277,11 +278,29 @@ __global__ __launch_bounds__(kRouteChunk) void route_scatter_kernel(RouteArgs a,
 // scatter, where a route's rank is the number of earlier routes of its expert
 // (a scan of the LDS expert list, four entries per read). Produces exactly
 // the outputs of the count / scan / scatter kernels.
-__global__ __launch_bounds__(kScanThreads) void route_small_kernel(RouteArgs a, int routes, int32_t* counts,
-                                                                   int32_t* offsets, ClassArgs cls, int32_t* tiles,
-                                                                   int32_t* tile_count, int32_t* sorted_routes,
-                                                                   int32_t* row_token, int32_t* route_pos,
-                                                                   float* route_weight, int32_t* invalid) {
+struct RouteOut {
+  int32_t* counts;
+  int32_t* offsets;
+  int32_t* tiles;
+  int32_t* tile_count;
+  int32_t* sorted_routes;
+  int32_t* row_token;
+  int32_t* route_pos;
+  float* route_weight;
+  int32_t* invalid;
+};
+
+__device__ __forceinline__ void route_small_body(const RouteArgs& a, int routes, const ClassArgs& cls,
+                                                 const RouteOut& o) {
+  int32_t* counts = o.counts;
+  int32_t* offsets = o.offsets;
+  int32_t* tiles = o.tiles;
+  int32_t* tile_count = o.tile_count;
+  int32_t* sorted_routes = o.sorted_routes;
+  int32_t* row_token = o.row_token;
+  int32_t* route_pos = o.route_pos;
+  float* route_weight = o.route_weight;
+  int32_t* invalid = o.invalid;
   __shared__ int32_t hist[kMaxExperts];
   __shared__ __attribute__((aligned(16))) int32_t ex[kScanThreads];
   __shared__ int32_t n_invalid;
@@ -334,6 +353,32 @@ __global__ __launch_bounds__(kScanThreads) void route_small_kernel(RouteArgs a, 
   sorted_routes[pos] = tid;
   row_token[pos] = tid / a.kt;
   route_pos[tid] = pos;
+}
+
+__global__ __launch_bounds__(kScanThreads) void route_small_kernel(RouteArgs a, int routes, ClassArgs cls,
+                                                                   RouteOut o) {
+  route_small_body(a, routes, cls, o);
+}
+
+// Small-batch front end in one launch: workgroup 0 builds the routes as
+// route_small_kernel; workgroup b >= 1 quantises token rows 4 (b - 1) ..
+// 4 (b - 1) + 3, kRowThreads threads per row (quant_row_wg). The two jobs
+// are independent (the token rows do not depend on the routing), so they
+// share a launch instead of running back to back.
+constexpr int kQuantRowsPerGroup = kScanThreads / kRowThreads;
+
+template <int CAP>
+__global__ __launch_bounds__(kScanThreads) void route_quant_small_kernel(RouteArgs a, int routes, ClassArgs cls,
+                                                                         RouteOut o, QuantRows qr) {
+  if (blockIdx.x == 0) {
+    route_small_body(a, routes, cls, o);
+    return;
+  }
+  __shared__ float wmax[kScanThreads / kWave];
+  const int g = threadIdx.x / kRowThreads;
+  const int64_t row = (int64_t)(blockIdx.x - 1) * kQuantRowsPerGroup + g;
+  quant_row_wg<CAP>(qr.x, qr.cols, qr.rounding, qr.q, qr.ldq, qr.scales, row, row < qr.rows,
+                    (int)threadIdx.x % kRowThreads, wmax + g * (kRowThreads / kWave));
 }
 
 ClassArgs class_args(const TileClasses& tc) {
@@ -391,7 +436,9 @@ void route_take(Arena& ar, RouteBuffers& rb, int64_t routes, int64_t experts, co
 
 int route_launch(const void* ids, int ids_is_i64, const float* topk_w, int64_t tokens, int64_t top_k,
                  int64_t experts, int64_t valid_experts, int64_t shared_id, float routed_scale, bool scale_routed,
-                 const RouteBuffers& rb, const TileClasses& tc, int32_t* invalid_out, hipStream_t stream) {
+                 const RouteBuffers& rb, const TileClasses& tc, int32_t* invalid_out, hipStream_t stream,
+                 const QuantRows* quant, bool* quant_done) {
+  if (quant_done) *quant_done = false;
   if (experts <= 0 || experts > kMaxExperts) return fail(FCMOE_EINVAL, "experts must be in [1, 1024]");
   const int64_t kt = top_k + (shared_id >= 0 ? 1 : 0);
   const int64_t routes = tokens * kt;
@@ -413,9 +460,29 @@ int route_launch(const void* ids, int ids_is_i64, const float* topk_w, int64_t t
   int32_t* invalid = invalid_out ? invalid_out : rb.invalid;
   const ClassArgs ca = class_args(tc);
   if (routes <= kScanThreads) {
-    hipLaunchKernelGGL(route_small_kernel, dim3(1), dim3(kScanThreads), 0, stream, a, (int)routes, rb.counts,
-                       rb.offsets, ca, rb.tiles, rb.tile_count, rb.sorted_routes, rb.row_token, rb.route_pos,
-                       rb.route_weight, invalid);
+    const RouteOut o{rb.counts,    rb.offsets,   rb.tiles,        rb.tile_count, rb.sorted_routes,
+                     rb.row_token, rb.route_pos, rb.route_weight, invalid};
+    if (quant && quant_done && quant->rows > 0 && quant->cols % 8 == 0 && quant->ldq % 8 == 0 &&
+        quant->rows <= (int64_t)INT32_MAX / 2) {
+      const int64_t per_thread = ceil_div(quant->cols / 8, kRowThreads);
+      const dim3 grid((unsigned)(1 + ceil_div(quant->rows, kQuantRowsPerGroup))), block(kScanThreads);
+      bool launched = true;
+      if (per_thread <= 1)
+        hipLaunchKernelGGL(route_quant_small_kernel<1>, grid, block, 0, stream, a, (int)routes, ca, o, *quant);
+      else if (per_thread <= 2)
+        hipLaunchKernelGGL(route_quant_small_kernel<2>, grid, block, 0, stream, a, (int)routes, ca, o, *quant);
+      else if (per_thread <= 4)
+        hipLaunchKernelGGL(route_quant_small_kernel<4>, grid, block, 0, stream, a, (int)routes, ca, o, *quant);
+      else if (per_thread <= 8)
+        hipLaunchKernelGGL(route_quant_small_kernel<8>, grid, block, 0, stream, a, (int)routes, ca, o, *quant);
+      else
+        launched = false;
+      if (launched) {
+        *quant_done = true;
+        return check_launch("route_quant");
+      }
+    }
+    hipLaunchKernelGGL(route_small_kernel, dim3(1), dim3(kScanThreads), 0, stream, a, (int)routes, ca, o);
     return check_launch("route");
   }
   hipLaunchKernelGGL(route_count_kernel, dim3((unsigned)chunks), dim3(kRouteChunk), experts * sizeof(int32_t),

@@ -674,8 +674,6 @@ int launch_lds_bm(int bm, const GemmParams& p, int64_t max_tiles, hipStream_t st
   constexpr int kNT = 2;  // buffer-load cache policy bit: nontemporal
   // A stages are 128 bytes of K (two chunks, full-line loads) where the
   // register budget allows it.
-  // A stages are 128 bytes of K (two chunks, full-line loads) where the
-  // register budget allows it.
   switch (bm) {
     case 128:
       return launch_lds_cfg<I8, EPI, 4, 8, 2, 3, kNT, 128>(p, max_tiles, stream);

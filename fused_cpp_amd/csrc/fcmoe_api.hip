@@ -121,9 +121,13 @@ Bf16Layout bf16_layout(const fcmoe_moe_args* a, Arena& ar, bool w8 = false) {
   L.hp = round_up(a->hidden, kmul);
   L.ip = round_up(a->inter, kmul);
   L.gu_ld = 2 * round_up(a->inter, 16);
+  // W8A16's 128/256-row tiles run on the LDS-staged kernel, whose A must stay
+  // under 2 GiB; beyond that the forward keeps to the 16/32-row tiles.
+  const bool w8_lds = a->tokens * L.hp * 2 < kLdsMaxABytes && L.routes * L.ip * 2 < kLdsMaxABytes;
   if (w8)
-    L.tc = make_tile_classes(kClassBMW8, L.routes <= kDecodeRowsPerExpert * a->experts ? 1 : kNumClassesW8, L.routes,
-                             a->experts);
+    L.tc = make_tile_classes(kClassBMW8,
+                             L.routes <= kDecodeRowsPerExpert * a->experts ? 1 : (w8_lds ? kNumClassesW8 : 2),
+                             L.routes, a->experts);
   else
     L.tc = select_classes(L.routes, a->experts);
   route_take(ar, L.rb, L.routes, a->experts, L.tc);
@@ -382,6 +386,7 @@ extern "C" int fcmoe_w8a8_forward(const fcmoe_moe_args* a, hipStream_t stream) {
   GemmParams g13{};
   g13.a = L.xq;
   g13.lda = L.hp;
+  g13.a_rows = a->tokens;
   g13.row_map = L.rb.row_token;
   g13.offsets = L.rb.offsets;
   g13.counts = L.rb.counts;
@@ -413,6 +418,7 @@ extern "C" int fcmoe_w8a8_forward(const fcmoe_moe_args* a, hipStream_t stream) {
 
   GemmParams g2{};
   g2.a = L.q2;
+  g2.a_rows = L.routes;
   g2.lda = L.ip;
   g2.row_map = nullptr;
   g2.offsets = L.rb.offsets;
@@ -515,6 +521,7 @@ int bf16_family_forward(const fcmoe_moe_args* a, hipStream_t stream, bool w8) {
   GemmParams g13{};
   g13.a = xa;
   g13.lda = L.hp;
+  g13.a_rows = a->tokens;
   g13.row_map = L.rb.row_token;
   g13.offsets = L.rb.offsets;
   g13.counts = L.rb.counts;
@@ -547,6 +554,7 @@ int bf16_family_forward(const fcmoe_moe_args* a, hipStream_t stream, bool w8) {
   GemmParams g2{};
   g2.a = L.y;
   g2.lda = L.ip;
+  g2.a_rows = L.routes;
   g2.offsets = L.rb.offsets;
   g2.counts = L.rb.counts;
   g2.w = a->w2;
@@ -603,6 +611,7 @@ extern "C" int fcmoe_w8a16_forward(const fcmoe_moe_args* a, hipStream_t stream) 
 
 namespace {
 struct I8Layout {
+  int64_t m;
   int64_t kp;
   TileClasses tc;
   int8_t* xq;
@@ -614,6 +623,7 @@ struct I8Layout {
 };
 I8Layout i8_layout(int64_t m, int64_t k, Arena& ar) {
   I8Layout L;
+  L.m = m;
   L.kp = round_up(k, 64);
   L.tc = make_tile_classes(kClassBM, kNumClasses, m, 1);
   L.xq = ar.take<int8_t>(m * L.kp);
@@ -642,6 +652,7 @@ int i8gemm_run(const I8Layout& L, int64_t k, const void* w_packed, const float* 
   GemmParams g{};
   g.a = L.xq;
   g.lda = L.kp;
+  g.a_rows = L.m;
   g.offsets = L.offsets;
   g.counts = L.counts;
   g.w = w_packed;
@@ -742,6 +753,7 @@ extern "C" int fcmoe_grouped_gemm_i8_acc(const int8_t* a, int64_t lda, const int
   GemmParams g{};
   g.a = a;
   g.lda = lda;
+  g.a_rows = row_map ? 0 : total_rows;  // gathered rows: the caller keeps A under 2 GiB
   g.row_map = row_map;
   g.offsets = offsets;
   g.counts = counts;

@@ -106,6 +106,7 @@ enum Epilogue : int {
 struct GemmParams {
   const void* a;             // int8 or bf16 rows
   int64_t lda;               // row stride in elements (a multiple of 64 bytes)
+  int64_t a_rows;            // rows of A the row indices may address (0: unknown, taken as < 2 GiB)
   const int32_t* row_map;    // sorted position -> A row (NULL: identity)
   const int32_t* offsets;    // [experts+1] first sorted position of each expert
   const int32_t* counts;     // [experts]
@@ -134,6 +135,8 @@ int gemm_launch(int epi, int bm, const GemmParams& p, int64_t max_tiles, hipStre
 // LDS-staged kernel for bm in {128, 192, 256} (fcmoe_gemm_lds.hip); gemm_launch
 // dispatches to it unless FCMOE_GEMM_LDS=0.
 int gemm_lds_launch(int epi, int bm, const GemmParams& p, int64_t max_tiles, hipStream_t stream);
+// A bytes the LDS-staged kernel can address (32-bit buffer offsets).
+constexpr int64_t kLdsMaxABytes = 0x7ffffff0;
 
 // ---- combine (fcmoe_combine.hip) ----
 int combine_launch(const float* route_out, const float* route_weight, const int32_t* route_pos, int64_t tokens,

@@ -185,7 +185,8 @@ int fcmoe_i8gemm_pair(const uint16_t* x, int64_t m, int64_t k, const void* w1_pa
 /* Grouped int8 GEMM returning raw int32 accumulators: for each expert e and
  * each j < counts[e], acc[offsets[e] + j, :] = a[row_map ? row_map[pos] : pos]
  * . w[e]^T with w packed (n_groups = 1, [n, k] int8), a int8 with row stride
- * lda (a multiple of 64, zero padded). acc has n columns. Used to show the
+ * lda (a multiple of 64, zero padded). acc has n columns. With a row_map, the
+ * rows it addresses must lie within the first 2 GiB of a. Used to show the
  * int32 accumulators equal an exact integer GEMM bit for bit. */
 int fcmoe_grouped_gemm_i8_acc(const int8_t* a, int64_t lda, const int32_t* row_map, const int32_t* counts,
                               const int32_t* offsets, int64_t experts, int64_t total_rows, const void* w_packed,

@@ -349,6 +349,31 @@ def test_i8gemm_bit_exact(gpu, oracle_lib, m, k, n, out_dtype):
         np.testing.assert_array_equal(got.numpy().view(np.uint32), ref.view(np.uint32))
 
 
+def test_i8gemm_activation_rows_beyond_2gib(gpu, oracle_lib):
+    """Maximum sizes: 320000 x 7168 int8 activation rows (2.29 GB) exceed the
+    2 GiB a 32-bit buffer offset reaches, so the 256-row tiles run on the
+    64-bit-addressed kernel. Rows before, across and after the 2 GiB boundary
+    are checked bit for bit (row quantisation is per row, so the oracle only
+    needs the sampled rows)."""
+    from fused_cpp_amd import i8gemm
+
+    m, k, n = 320000, 7168, 32
+    g = torch.Generator(device=gpu)
+    g.manual_seed(3)
+    x = torch.randn(m, k, dtype=torch.bfloat16, device=gpu, generator=g)
+    torch.manual_seed(4)
+    weight = torch.randint(-127, 128, (n, k), dtype=torch.int8)
+    weight_scale = torch.rand(n, dtype=torch.float32) * 0.05 + 0.01
+    out = i8gemm.dynamic_scaled_mm(x, i8gemm.prepare(weight, weight_scale), out_dtype=torch.bfloat16)
+    boundary = (1 << 31) // k
+    rows = np.r_[0:8, boundary - 8:boundary + 8, m - 8:m]
+    idx = torch.from_numpy(rows).to(gpu)
+    xs = x.index_select(0, idx).cpu().view(torch.int16).numpy().view(np.uint16)
+    ref = oracle_lib.i8gemm(xs, weight.numpy(), weight_scale.numpy(), None, True)
+    got = out.index_select(0, idx).cpu().view(torch.int16).numpy().view(np.uint16)
+    np.testing.assert_array_equal(got, ref)
+
+
 def test_i8gemm_batched_scalar_scale_and_ties(gpu, oracle_lib):
     from fused_cpp_amd import i8gemm
 

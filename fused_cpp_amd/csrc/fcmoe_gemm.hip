@@ -351,13 +351,15 @@ int gemm_launch(int epi, int bm, const GemmParams& p, int64_t max_tiles, hipStre
     const char* v = getenv("FCMOE_GEMM_LDS");
     return !(v && v[0] == '0');
   }();
-  // The LDS-staged kernel addresses A through a buffer resource with 32-bit
-  // offsets: an A of 2 GiB or more runs on the register-ring kernel (64-bit
-  // addresses). W8A16 has no register-ring tile above 32 rows; its forward
+  // The LDS-staged kernel addresses A and one expert's weights through
+  // buffer resources with 32-bit offsets: 2 GiB or more of either runs on
+  // the register-ring kernel (64-bit addresses). W8A16 has no register-ring tile above 32 rows; its forward
   // keeps to the 16/32-row classes for such an A.
   const bool a_int8 = epi == kEpiRawI32 || epi == kEpiW13SwigluI8 || epi == kEpiW2RouteI8 || epi == kEpiI8Gemm;
-  const bool a_fits = p.a_rows <= 0 || p.a_rows * p.lda * (a_int8 ? 1 : 2) < kLdsMaxABytes;
-  if (bm >= 128 && epi_w8(epi) && !a_fits) return fail(FCMOE_EINVAL, "W8A16 LDS tiles need A under 2 GiB");
+  const bool a_fits = (p.a_rows <= 0 || p.a_rows * p.lda * (a_int8 ? 1 : 2) < kLdsMaxABytes) &&
+                      p.w_expert_bytes < kLdsMaxABytes;  // one expert's weights: one buffer resource too
+  if (bm >= 128 && epi_w8(epi) && !a_fits)
+    return fail(FCMOE_EINVAL, "W8A16 LDS tiles need A and each expert's weights under 2 GiB");
   if (bm >= 128 && a_fits && (use_lds || epi_w8(epi))) return gemm_lds_launch(epi, bm, p, max_tiles, stream);
   if (epi == kEpiW13ActW8) return launch_bm_w8<kEpiW13ActW8>(bm, p, max_tiles, stream);
   if (epi == kEpiW2RouteW8) return launch_bm_w8<kEpiW2RouteW8>(bm, p, max_tiles, stream);

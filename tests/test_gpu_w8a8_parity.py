@@ -213,6 +213,16 @@ def test_w8a8_forward_bit_exact_odd_chunk_counts(gpu, oracle_lib):
             np.testing.assert_array_equal(acc[lo:hi], oracle_lib.gemm_i8_rows(a, row_map[lo:hi].astype(np.int64), w[e]))
 
 
+@pytest.mark.parametrize("tokens", [128, 129])
+def test_w8a8_forward_bit_exact_route_path_boundary(gpu, oracle_lib, tokens):
+    """1024 routes (128 tokens x top-8) is the largest routing the single-
+    workgroup route kernel takes, and there the token rows are quantised in
+    the same launch (32 groups of 4 rows); 129 tokens (1032 routes) take the
+    count / scan / scatter kernels and the separate row quantisation."""
+    case = H.w8a8_case(900 + tokens, tokens, 512, 256, 16, 8)
+    _check_w8a8(gpu, oracle_lib, case, shared=False)
+
+
 @pytest.mark.parametrize("tokens", [1, 2, 5])
 def test_w8a8_forward_bit_exact_small_batch(gpu, oracle_lib, tokens):
     """Small-batch decode (1-5 tokens, 4 routed experts each plus the shared

@@ -155,6 +155,7 @@ def expert_counts(cfg, ids):
     return counts
 
 
+CLASS_BM_PREFILL = (16, 128, 192, 256)  # W8A8 / BF16 prefill tile classes
 CLASS_BM_W8 = (16, 32, 128, 256)  # W8A16 tile classes
 
 
@@ -163,7 +164,7 @@ def class_of(c: int, decode: bool, kind: str = "w8a8") -> int:
     with c rows (fcmoe_api.hip select_classes; W8A16 uses its own class set)."""
     if decode:
         return 0
-    bms = CLASS_BM_W8 if kind == "w8a16" else CLASS_BM
+    bms = CLASS_BM_W8 if kind == "w8a16" else CLASS_BM_PREFILL
     for bm in bms:
         if c <= bm:
             return CLASS_BM.index(bm)

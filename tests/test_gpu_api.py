@@ -399,9 +399,10 @@ def test_i8gemm_batched_scalar_scale_and_ties(gpu, oracle_lib):
 
 @pytest.mark.parametrize("activation", ["silu", "swigluoai"])
 def test_bf16_prefill_every_tile_class_within_tolerance(gpu, oracle_lib, activation):
-    """Per-expert counts 3..420 reach every tile class (16..256 rows), i.e. the bf16
-    instantiations of the register-ring kernel and of the LDS-staged prefill kernel,
-    with biases, against the fp32 reference."""
+    """Per-expert counts 3..420 reach every prefill tile class (16, 128, 192 and
+    256 rows, the last with a two-tile expert), i.e. the bf16 instantiations of
+    the register-ring kernel and of the LDS-staged prefill kernel, with biases,
+    against the fp32 reference."""
     from fused_cpp_amd import moe
 
     rng = np.random.default_rng(17)

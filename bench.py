@@ -9,13 +9,15 @@ activations. A step is one call of ``fused_moe_w8a8_tiled_with_shared`` on
 inputs resident in HBM. Prints ONE JSON line.
 
 ``--config c3`` / ``c4`` run the prefill configs, ``c1`` / ``c0`` the BF16
-ones (for the tables in DESIGN.md); ``--prefill`` adds the C3 prefill figures
-to the default line as ``secondary``.
+ones and ``c1w8`` the W8A16 one; ``--tokens`` overrides a config's token
+count; ``--prefill`` adds the C3 prefill figures to the default line as
+``secondary``.
 
 roofline: the dominant kernel (largest GPU time per step among the grouped
 GEMM tile-class launches) is timed live with hipEvents recorded by libfcmoe
 on the launch stream (fcmoe_stage_timing_*); its algorithmic bytes/ops come
-from the realised routing ("Measurement").
+from the realised routing: active experts' weight and scale bytes plus the
+stage's activation rows in and out (ops: 2 x MACs).
 cpu_baseline: the CPU oracle (oracle/, a restatement of the reference
 arithmetic, OpenMP) timed on this host on the same layer.
 """
@@ -461,7 +463,7 @@ def main() -> int:
         return 0
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only: every box has one MI355X; "
-                                   "run with --gpus 1 (multi-GPU sharding is described in DESIGN.md)"}))
+                                   "run with --gpus 1"}))
         return 2
     os.environ.setdefault("FUSED_CPP_AMD_VALIDATE_IDS", "0")  # no host read inside the timed loop
     import torch

@@ -250,7 +250,7 @@ __global__ __launch_bounds__(kRouteChunk) void route_scatter_kernel(RouteArgs a,
                                                                      const int32_t* chunk_hist,
                                                                      const int32_t* offsets, int32_t* sorted_routes,
                                                                      int32_t* row_token, int32_t* route_pos) {
-  __shared__ int32_t ex[kRouteChunk];
+  __shared__ __attribute__((aligned(16))) int32_t ex[kRouteChunk];
   const int tid = threadIdx.x;
   const int64_t r = (int64_t)blockIdx.x * kRouteChunk + tid;
   int e = -1;
@@ -265,8 +265,16 @@ __global__ __launch_bounds__(kRouteChunk) void route_scatter_kernel(RouteArgs a,
     route_pos[r] = -1;
     return;
   }
+  // stable rank within the chunk: earlier routes of the same expert, four
+  // list entries per LDS read
   int rank = 0;
-  for (int j = 0; j < tid; ++j) rank += (ex[j] == e) ? 1 : 0;
+  const int4* ex4 = (const int4*)ex;
+  int j = 0;
+  for (; j + 4 <= tid; j += 4) {
+    const int4 q = ex4[j / 4];
+    rank += (q.x == e) + (q.y == e) + (q.z == e) + (q.w == e);
+  }
+  for (; j < tid; ++j) rank += ex[j] == e;
   const int pos = offsets[e] + chunk_hist[(int64_t)blockIdx.x * a.experts + e] + rank;
   sorted_routes[pos] = (int32_t)r;
   row_token[pos] = (int32_t)(r / a.kt);

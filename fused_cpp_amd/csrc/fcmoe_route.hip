@@ -15,6 +15,8 @@
 //               for the grouped GEMMs (the tokens-per-expert tile selector).
 //   3. scatter: per chunk, the in-chunk rank of each route among earlier
 //               routes of the same expert gives its stable sorted position.
+#include <utility>
+
 #include "fcmoe_device.h"
 #include "fcmoe_internal.h"
 #include "fcmoe_quant_row.h"
@@ -172,11 +174,9 @@ __global__ __launch_bounds__(kScanThreads) void tiles_from_counts_kernel(const i
 // instead of one per chunk.
 constexpr int kScanBatch = 16;
 
-__global__ __launch_bounds__(kScanThreads) void route_scan_kernel(int experts, int64_t chunks, int32_t* chunk_hist,
-                                                                   int32_t* counts, int32_t* offsets,
-                                                                   ClassArgs cls, int32_t* tiles,
-                                                                   int32_t* tile_count, const int32_t* chunk_invalid,
-                                                                   int32_t* invalid) {
+__device__ __forceinline__ void route_scan_body(int experts, int64_t chunks, int32_t* chunk_hist, int32_t* counts,
+                                                int32_t* offsets, const ClassArgs& cls, int32_t* tiles,
+                                                int32_t* tile_count, const int32_t* chunk_invalid, int32_t* invalid) {
   __shared__ int seg_sum[kScanThreads];
   const int tid = threadIdx.x;
   {
@@ -244,6 +244,14 @@ __global__ __launch_bounds__(kScanThreads) void route_scan_kernel(int experts, i
   if (owner) offsets[e] = off;
   if (tid == 0) offsets[experts] = total;
   emit_tiles(owner ? count : 0, tid, cls, tiles, tile_count);
+}
+
+__global__ __launch_bounds__(kScanThreads) void route_scan_kernel(int experts, int64_t chunks, int32_t* chunk_hist,
+                                                                   int32_t* counts, int32_t* offsets,
+                                                                   ClassArgs cls, int32_t* tiles,
+                                                                   int32_t* tile_count, const int32_t* chunk_invalid,
+                                                                   int32_t* invalid) {
+  route_scan_body(experts, chunks, chunk_hist, counts, offsets, cls, tiles, tile_count, chunk_invalid, invalid);
 }
 
 __global__ __launch_bounds__(kRouteChunk) void route_scatter_kernel(RouteArgs a, int64_t routes,
@@ -375,6 +383,16 @@ __global__ __launch_bounds__(kScanThreads) void route_small_kernel(RouteArgs a, 
 // share a launch instead of running back to back.
 constexpr int kQuantRowsPerGroup = kScanThreads / kRowThreads;
 
+// Workgroup b >= 1 of a shared launch: token rows 4 (b - 1) .. 4 (b - 1) + 3.
+template <int CAP>
+__device__ __forceinline__ void quant_row_group(const QuantRows& qr) {
+  __shared__ float wmax[kScanThreads / kWave];
+  const int g = threadIdx.x / kRowThreads;
+  const int64_t row = (int64_t)(blockIdx.x - 1) * kQuantRowsPerGroup + g;
+  quant_row_wg<CAP>(qr.x, qr.cols, qr.rounding, qr.q, qr.ldq, qr.scales, row, row < qr.rows,
+                    (int)threadIdx.x % kRowThreads, wmax + g * (kRowThreads / kWave));
+}
+
 template <int CAP>
 __global__ __launch_bounds__(kScanThreads) void route_quant_small_kernel(RouteArgs a, int routes, ClassArgs cls,
                                                                          RouteOut o, QuantRows qr) {
@@ -382,11 +400,45 @@ __global__ __launch_bounds__(kScanThreads) void route_quant_small_kernel(RouteAr
     route_small_body(a, routes, cls, o);
     return;
   }
-  __shared__ float wmax[kScanThreads / kWave];
-  const int g = threadIdx.x / kRowThreads;
-  const int64_t row = (int64_t)(blockIdx.x - 1) * kQuantRowsPerGroup + g;
-  quant_row_wg<CAP>(qr.x, qr.cols, qr.rounding, qr.q, qr.ldq, qr.scales, row, row < qr.rows,
-                    (int)threadIdx.x % kRowThreads, wmax + g * (kRowThreads / kWave));
+  quant_row_group<CAP>(qr);
+}
+
+// Larger routings: the column scan is one workgroup that leaves the rest of
+// the GPU idle for its whole duration (22-33 us at C3/C4), so the token rows
+// are quantised by the same launch's other workgroups.
+template <int CAP>
+__global__ __launch_bounds__(kScanThreads) void route_scan_quant_kernel(int experts, int64_t chunks,
+                                                                        int32_t* chunk_hist, int32_t* counts,
+                                                                        int32_t* offsets, ClassArgs cls,
+                                                                        int32_t* tiles, int32_t* tile_count,
+                                                                        const int32_t* chunk_invalid,
+                                                                        int32_t* invalid, QuantRows qr) {
+  if (blockIdx.x == 0) {
+    route_scan_body(experts, chunks, chunk_hist, counts, offsets, cls, tiles, tile_count, chunk_invalid, invalid);
+    return;
+  }
+  quant_row_group<CAP>(qr);
+}
+
+// 16-byte units per thread when kRowThreads threads quantise one row of
+// `quant` (1, 2, 4 or 8), or 0 when the rows do not qualify for a shared
+// launch (the caller then runs quant_rows_launch).
+int quant_cap(const QuantRows* quant) {
+  if (!quant || quant->rows <= 0 || quant->cols % 8 || quant->ldq % 8 || quant->rows > (int64_t)INT32_MAX / 2)
+    return 0;
+  const int64_t pt = ceil_div(quant->cols / 8, kRowThreads);
+  return pt <= 1 ? 1 : pt <= 2 ? 2 : pt <= 4 ? 4 : pt <= 8 ? 8 : 0;
+}
+
+// Calls launch(std::integral_constant<int, cap>) for cap in {1, 2, 4, 8}.
+template <typename F>
+void with_cap(int cap, F&& launch) {
+  switch (cap) {
+    case 1: launch(std::integral_constant<int, 1>{}); break;
+    case 2: launch(std::integral_constant<int, 2>{}); break;
+    case 4: launch(std::integral_constant<int, 4>{}); break;
+    default: launch(std::integral_constant<int, 8>{}); break;
+  }
 }
 
 ClassArgs class_args(const TileClasses& tc) {
@@ -470,33 +522,32 @@ int route_launch(const void* ids, int ids_is_i64, const float* topk_w, int64_t t
   if (routes <= kScanThreads) {
     const RouteOut o{rb.counts,    rb.offsets,   rb.tiles,        rb.tile_count, rb.sorted_routes,
                      rb.row_token, rb.route_pos, rb.route_weight, invalid};
-    if (quant && quant_done && quant->rows > 0 && quant->cols % 8 == 0 && quant->ldq % 8 == 0 &&
-        quant->rows <= (int64_t)INT32_MAX / 2) {
-      const int64_t per_thread = ceil_div(quant->cols / 8, kRowThreads);
+    if (const int cap = quant_done ? quant_cap(quant) : 0) {
       const dim3 grid((unsigned)(1 + ceil_div(quant->rows, kQuantRowsPerGroup))), block(kScanThreads);
-      bool launched = true;
-      if (per_thread <= 1)
-        hipLaunchKernelGGL(route_quant_small_kernel<1>, grid, block, 0, stream, a, (int)routes, ca, o, *quant);
-      else if (per_thread <= 2)
-        hipLaunchKernelGGL(route_quant_small_kernel<2>, grid, block, 0, stream, a, (int)routes, ca, o, *quant);
-      else if (per_thread <= 4)
-        hipLaunchKernelGGL(route_quant_small_kernel<4>, grid, block, 0, stream, a, (int)routes, ca, o, *quant);
-      else if (per_thread <= 8)
-        hipLaunchKernelGGL(route_quant_small_kernel<8>, grid, block, 0, stream, a, (int)routes, ca, o, *quant);
-      else
-        launched = false;
-      if (launched) {
-        *quant_done = true;
-        return check_launch("route_quant");
-      }
+      with_cap(cap, [&](auto c) {
+        hipLaunchKernelGGL(route_quant_small_kernel<decltype(c)::value>, grid, block, 0, stream, a, (int)routes, ca,
+                           o, *quant);
+      });
+      *quant_done = true;
+      return check_launch("route_quant");
     }
     hipLaunchKernelGGL(route_small_kernel, dim3(1), dim3(kScanThreads), 0, stream, a, (int)routes, ca, o);
     return check_launch("route");
   }
   hipLaunchKernelGGL(route_count_kernel, dim3((unsigned)chunks), dim3(kRouteChunk), experts * sizeof(int32_t),
                      stream, a, routes, rb.chunk_hist, rb.route_weight, rb.chunk_invalid);
-  hipLaunchKernelGGL(route_scan_kernel, dim3(1), dim3(kScanThreads), 0, stream, (int)experts, chunks,
-                     rb.chunk_hist, rb.counts, rb.offsets, ca, rb.tiles, rb.tile_count, rb.chunk_invalid, invalid);
+  if (const int cap = quant_done ? quant_cap(quant) : 0) {
+    const dim3 grid((unsigned)(1 + ceil_div(quant->rows, kQuantRowsPerGroup))), block(kScanThreads);
+    with_cap(cap, [&](auto c) {
+      hipLaunchKernelGGL(route_scan_quant_kernel<decltype(c)::value>, grid, block, 0, stream, (int)experts, chunks,
+                         rb.chunk_hist, rb.counts, rb.offsets, ca, rb.tiles, rb.tile_count, rb.chunk_invalid,
+                         invalid, *quant);
+    });
+    *quant_done = true;
+  } else {
+    hipLaunchKernelGGL(route_scan_kernel, dim3(1), dim3(kScanThreads), 0, stream, (int)experts, chunks,
+                       rb.chunk_hist, rb.counts, rb.offsets, ca, rb.tiles, rb.tile_count, rb.chunk_invalid, invalid);
+  }
   hipLaunchKernelGGL(route_scatter_kernel, dim3((unsigned)chunks), dim3(kRouteChunk), 0, stream, a, routes,
                      rb.chunk_hist, rb.offsets, rb.sorted_routes, rb.row_token, rb.route_pos);
   return check_launch("route");

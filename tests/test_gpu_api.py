@@ -349,6 +349,52 @@ def test_i8gemm_bit_exact(gpu, oracle_lib, m, k, n, out_dtype):
         np.testing.assert_array_equal(got.numpy().view(np.uint32), ref.view(np.uint32))
 
 
+@pytest.mark.parametrize("kind", ["bf16", "w8a16"])
+def test_forward_activation_rows_beyond_2gib(gpu, oracle_lib, kind):
+    """Maximum sizes: 150000 x 7168 bf16 token rows (2.15 GB) exceed the 2 GiB a
+    32-bit buffer offset reaches. BF16's W13 then runs its 128-256-row tiles on
+    the 64-bit-addressed register kernel, and W8A16 keeps to its 16/32-row
+    classes. Tokens before, across and after the boundary are checked against
+    the fp32 reference (tokens are independent, so the reference only needs
+    the sampled ones), within max-abs 2e-2 and cosine 0.9999."""
+    from fused_cpp_amd import moe
+
+    T, Hd, F, E = 150000, 7168, 64, 2
+    g = torch.Generator(device=gpu)
+    g.manual_seed(5)
+    x = torch.randn(T, Hd, dtype=torch.bfloat16, device=gpu, generator=g)
+    rng = np.random.default_rng(6)
+    w13 = H.bf16_bits((rng.standard_normal((E, 2 * F, Hd)) * 0.02).astype(np.float32))
+    w2 = H.bf16_bits((rng.standard_normal((E, Hd, F)) * 0.02).astype(np.float32))
+    ids = rng.integers(0, E, size=(T, 1)).astype(np.int64)
+    w = np.ones((T, 1), np.float32)
+    wt, it = torch.from_numpy(w).to(gpu), torch.from_numpy(ids).to(gpu)
+    tb = lambda b: torch.from_numpy(b.view(np.int16)).to(gpu).view(torch.bfloat16)  # noqa: E731
+    if kind == "bf16":
+        packed = moe.prepare_fused_moe_bf16_tiled_weights(tb(w13), tb(w2))
+        out = moe.fused_moe_bf16_tiled(x, packed, wt, it)
+        d13, d2, rnd = H.bits_to_f32(w13), H.bits_to_f32(w2), False
+    else:
+        q13, s13 = oracle_lib.quant_weight_rows(w13)
+        q2, s2 = oracle_lib.quant_weight_rows(w2)
+        packed = moe.prepare_fused_moe_w8a16_tiled_quantized_weights(torch.from_numpy(q13), torch.from_numpy(s13),
+                                                                      torch.from_numpy(q2), torch.from_numpy(s2))
+        out = moe.fused_moe_w8a16_tiled(x, packed, wt, it)
+        d13 = q13.astype(np.float32) * s13[..., None]
+        d2 = q2.astype(np.float32) * s2[..., None]
+        rnd = True
+    boundary = (1 << 31) // (Hd * 2)
+    rows = np.r_[0:4, boundary - 4:boundary + 4, T - 4:T]
+    idx = torch.from_numpy(rows).to(gpu)
+    xs = x.index_select(0, idx).float().cpu().numpy()
+    ref = oracle_lib.bf16_moe_reference(xs, d13, d2, w[rows], ids[rows], round_intermediate=rnd).astype(np.float64)
+    o = out.index_select(0, idx).float().cpu().numpy().astype(np.float64)
+    err = float(np.abs(o - ref).max())
+    cos = float((o * ref).sum() / np.sqrt((o * o).sum() * (ref * ref).sum()))
+    assert err <= 2e-2 * max(1.0, float(np.abs(ref).max())), err
+    assert cos >= 0.9999, cos
+
+
 def test_i8gemm_activation_rows_beyond_2gib(gpu, oracle_lib):
     """Maximum sizes: 320000 x 7168 int8 activation rows (2.29 GB) exceed the
     2 GiB a 32-bit buffer offset reaches, so the 256-row tiles run on the

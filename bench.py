@@ -10,16 +10,20 @@ inputs resident in HBM. Prints ONE JSON line.
 
 ``--config c3`` / ``c4`` run the prefill configs, ``c1`` / ``c0`` the BF16
 ones and ``c1w8`` the W8A16 one; ``--tokens`` overrides a config's token
-count; ``--prefill`` adds the C3 prefill figures to the default line as
-``secondary``.
+count. The default C2 line also carries, as ``secondary`` entries, C3 and
+C4 prefill, decode at T=1 and T=2 on the C2 layer, and C1 (BF16), each with
+its own kernel roofline, layer roofline and sampled bit-exact parity check.
 
 roofline: the dominant kernel (largest GPU time per step among the grouped
 GEMM tile-class launches) is timed live with hipEvents recorded by libfcmoe
 on the launch stream (fcmoe_stage_timing_*); its algorithmic bytes/ops come
 from the realised routing: active experts' weight and scale bytes plus the
 stage's activation rows in and out (ops: 2 x MACs).
-cpu_baseline: the CPU oracle (oracle/, a restatement of the reference
-arithmetic, OpenMP) timed on this host on the same layer.
+cpu_baseline: the repo tests' PyTorch eager reference (tests/test_moe_w8a8.py:
+40-69, restated grouped per expert with float64 GEMMs) on this host's torch
+threads, timed on a seeded uniform sample of the active experts and scaled to
+the layer; cpu_baseline_oracle: the C oracle (oracle/, OpenMP) on the same
+sample.
 """
 
 from __future__ import annotations
@@ -88,8 +92,19 @@ def make_routing(cfg, seed: int = 0):
     return ids.astype(np.int64), w.astype(np.float32), tau
 
 
-def build_layer(cfg, device, keep_host_int8: bool):
-    """Random N(0, 0.02) bf16 experts (+shared), quantised per channel and packed on the GPU."""
+def make_x(cfg, device):
+    """Token rows x ~ N(0, 1) as bf16 on the device (seed 7)."""
+    import torch
+
+    rng = np.random.default_rng(7)
+    return torch.from_numpy(rng.standard_normal((cfg["T"], cfg["H"])).astype(np.float32)).to(device).to(torch.bfloat16)
+
+
+def build_layer(cfg, device, keep_host_int8: bool, keep_device_int8: bool = False):
+    """Random N(0, 0.02) bf16 experts (+shared), quantised per channel and packed on the GPU.
+
+    Returns (prepared weights, host int8 copy or None); with keep_device_int8 a
+    third item holds the unpacked device tensors (q13, s13, q2, s2)."""
     import torch
 
     from fused_cpp_amd import cabi
@@ -120,6 +135,7 @@ def build_layer(cfg, device, keep_host_int8: bool):
     host = None
     if keep_host_int8:
         host = (q13.cpu().numpy(), s13.cpu().numpy(), q2.cpu().numpy(), s2.cpu().numpy())
+    dev_int8 = (q13, s13, q2, s2) if keep_device_int8 else None
     del q13, q2
     torch.cuda.empty_cache()
     if cfg["shared"]:
@@ -127,10 +143,14 @@ def build_layer(cfg, device, keep_host_int8: bool):
                                                           shared_expert_id=cfg["E"])
     else:
         weights = packed
+    if keep_device_int8:
+        return weights, host, dev_int8
     return weights, host
 
 
-def build_bf16_layer(cfg, device):
+def build_bf16_layer(cfg, device, keep_device: bool = False):
+    """Random N(0, 0.02) bf16 experts (+shared), packed on the GPU; with
+    keep_device the unpacked (w13, w2) device tensors are returned as well."""
     import torch
 
     from fused_cpp_amd.moe import (PreparedBF16TiledRoutedSharedMoEWeights, prepare_fused_moe_bf16_tiled_weights)
@@ -141,12 +161,13 @@ def build_bf16_layer(cfg, device):
     w13 = (torch.randn((E, 2 * I, H), generator=g, device=device) * 0.02).to(torch.bfloat16)
     w2 = (torch.randn((E, H, I), generator=g, device=device) * 0.02).to(torch.bfloat16)
     packed = prepare_fused_moe_bf16_tiled_weights(w13, w2, fuse_silu=True)
+    kept = (w13, w2) if keep_device else None
     del w13, w2
     torch.cuda.empty_cache()
     if cfg["shared"]:
-        return PreparedBF16TiledRoutedSharedMoEWeights(packed=packed, routed_experts=cfg["E"],
-                                                       shared_expert_id=cfg["E"])
-    return packed
+        packed = PreparedBF16TiledRoutedSharedMoEWeights(packed=packed, routed_experts=cfg["E"],
+                                                         shared_expert_id=cfg["E"])
+    return (packed, kept) if keep_device else packed
 
 
 def expert_counts(cfg, ids):
@@ -201,7 +222,37 @@ def algorithmic(cfg, counts):
     return layer_bytes, layer_ops, stages
 
 
-def run_gpu(cfg, steps: int, warmup: int, device, keep_host: bool, graph: bool = False):
+_LAYERS: dict = {}
+
+
+def get_layer(cfg, device):
+    """Prepared weights for cfg's shape, built once per (kind, shape) and shared
+    by every workload of that shape (C2, C3 and the small-batch decode lines
+    use the same seeded E=256 layer). W8A8 / W8A16 entries also hold the
+    unpacked int8 device tensors, from which parity checks and the CPU
+    baselines copy the experts they touch."""
+    kind = "w8" if cfg["kind"] in ("w8a8", "w8a16") else "bf16"
+    key = (kind, cfg["E"], cfg["H"], cfg["I"], cfg["shared"])
+    if key not in _LAYERS:
+        import gc
+
+        import torch
+
+        for k in list(_LAYERS):  # one layer resident at a time
+            del _LAYERS[k]
+        gc.collect()
+        torch.cuda.empty_cache()
+        t0 = time.time()
+        if kind == "w8":
+            weights, _, dev = build_layer(cfg, device, False, keep_device_int8=True)
+        else:
+            weights, dev = build_bf16_layer(cfg, device), None
+        log(f"[bench] {cfg['desc']}: weights ready in {time.time() - t0:.1f}s")
+        _LAYERS[key] = (weights, dev)
+    return _LAYERS[key]
+
+
+def run_gpu(cfg, steps: int, warmup: int, device, graph: bool = False):
     import torch
 
     from fused_cpp_amd import cabi
@@ -209,14 +260,11 @@ def run_gpu(cfg, steps: int, warmup: int, device, keep_host: bool, graph: bool =
     from fused_cpp_amd.moe import fused_moe_bf16_tiled_with_shared, fused_moe_tiled, fused_moe_w8a8_tiled_with_shared
 
     ids, w, tau = make_routing(cfg)
-    rng = np.random.default_rng(7)
-    x = torch.from_numpy(rng.standard_normal((cfg["T"], cfg["H"])).astype(np.float32)).to(device).to(torch.bfloat16)
+    x = make_x(cfg, device)
     ids_d = torch.from_numpy(ids).to(device)
     w_d = torch.from_numpy(w).to(device)
-    t0 = time.time()
-    host = None
+    weights, dev_int8 = get_layer(cfg, device)
     if cfg["kind"] == "w8a8":
-        weights, host = build_layer(cfg, device, keep_host)
         if cfg["shared"]:
             def step(out):
                 return fused_moe_w8a8_tiled_with_shared(x, weights, w_d, ids_d, routed_scaling_factor=cfg["scale"],
@@ -225,17 +273,15 @@ def run_gpu(cfg, steps: int, warmup: int, device, keep_host: bool, graph: bool =
             def step(out):
                 return fused_moe_tiled(x, weights, w_d, ids_d, swiglu_limit=10.0, out=out)
     elif cfg["kind"] == "w8a16":
-        w8, _ = build_layer(cfg, device, False)
-        p = w8.packed
-        weights = moe.PreparedW8A16TiledRoutedSharedMoEWeights(
-            packed=moe.PreparedW8A16TiledFusedMoEWeights(w13=p.w13, w2=p.w2), routed_experts=w8.routed_experts,
-            shared_expert_id=w8.shared_expert_id)
+        p = weights.packed
+        w16 = moe.PreparedW8A16TiledRoutedSharedMoEWeights(
+            packed=moe.PreparedW8A16TiledFusedMoEWeights(w13=p.w13, w2=p.w2), routed_experts=weights.routed_experts,
+            shared_expert_id=weights.shared_expert_id)
 
         def step(out):
-            return moe.fused_moe_w8a16_tiled_with_shared(x, weights, w_d, ids_d, routed_scaling_factor=cfg["scale"],
+            return moe.fused_moe_w8a16_tiled_with_shared(x, w16, w_d, ids_d, routed_scaling_factor=cfg["scale"],
                                                          out=out)
     else:
-        weights = build_bf16_layer(cfg, device)
         if cfg["shared"]:
             def step(out):
                 return fused_moe_bf16_tiled_with_shared(x, weights, w_d, ids_d, routed_scaling_factor=cfg["scale"],
@@ -243,7 +289,6 @@ def run_gpu(cfg, steps: int, warmup: int, device, keep_host: bool, graph: bool =
         else:
             def step(out):
                 return fused_moe_tiled(x, weights, w_d, ids_d, out=out)
-    log(f"[bench] weights ready in {time.time() - t0:.1f}s")
     out = torch.empty_like(x)
     for _ in range(max(warmup, 1)):
         step(out)
@@ -275,59 +320,169 @@ def run_gpu(cfg, steps: int, warmup: int, device, keep_host: bool, graph: bool =
     torch.cuda.synchronize()
     stages = cabi.stage_timing_read()
     cabi.stage_timing_enable(False)
-    return dict(ms=ms, stages=stages, ids=ids, w=w, tau=tau, x=x, out=out, host=host, weights=weights)
+    return dict(ms=ms, stages=stages, ids=ids, w=w, tau=tau, x=x, out=out, dev_int8=dev_int8)
 
 
-def cpu_baseline(cfg, res, max_routes: int | None):
-    """Time the oracle's grouped per-expert W8A8 layer (OpenMP) on this host."""
-    import oracle
+def _host_experts(dev_int8, experts: np.ndarray):
+    """Host copies (numpy) of the given experts' int8 weights and scales."""
+    import torch
 
-    q13, s13, q2, s2 = res["host"]
-    x_bits = res["x"].cpu().view(__import__("torch").int16).numpy().view(np.uint16)
-    counts_routes = oracle.route_build(res["ids"], q13.shape[0], cfg["E"] if cfg["shared"] else -1)
-    counts, offsets, sorted_routes, _ = counts_routes
+    q13, s13, q2, s2 = dev_int8
+    sel = torch.from_numpy(np.ascontiguousarray(experts, np.int64)).to(q13.device)
+    return tuple(t.index_select(0, sel).cpu().numpy() for t in (q13, s13, q2, s2))
+
+
+def _expert_sample(cfg, ids, budget_experts: int, seed: int = 5):
+    """A seeded uniform sample of the active experts (shared one included with
+    its share of probability): timing a uniform subset of experts and scaling
+    by active/sampled estimates the whole layer without bias."""
+    counts = expert_counts(cfg, ids)
+    active = np.nonzero(counts > 0)[0]
+    rng = np.random.default_rng(seed)
+    n = min(budget_experts, len(active))
+    return np.sort(rng.choice(active, n, replace=False)), len(active), counts
+
+
+def _expert_routes(cfg, ids, experts: np.ndarray):
+    """For each expert: its flat routes (t*kt + s) in ascending order."""
     kt = cfg["k"] + (1 if cfg["shared"] else 0)
-    R = cfg["T"] * kt
-    # bounded sample: whole experts in sorted order until max_routes
-    e_end = len(counts)
-    if max_routes is not None:
-        csum = np.cumsum(counts)
-        e_end = int(np.searchsorted(csum, max_routes) + 1)
-        e_end = min(e_end, len(counts))
-    route_out = np.zeros((R, cfg["H"]), np.float32)
-    threads = os.cpu_count() or 1
-    oracle.w8a8_expert_range(x_bits, sorted_routes, offsets, kt, q13, s13, q2, s2, 0, min(e_end, 2), route_out)
+    T = cfg["T"]
+    routes = []
+    for e in experts:
+        if cfg["shared"] and e == cfg["E"]:
+            r = np.arange(T, dtype=np.int64) * kt + cfg["k"]
+        else:
+            t, s = np.nonzero(ids == e)
+            r = np.sort(t.astype(np.int64) * kt + s)
+        routes.append(r)
+    return routes, kt
+
+
+def torch_eager_expert_layer(x_bf16, ids, w, cfg, experts, host, routes):
+    """Grouped per-expert restatement, in PyTorch eager on the CPU, of the
+    reference test's W8A8 reference (tests/test_moe_w8a8.py:40-69): per-token
+    quantisation (round half to even, as torch.round), int8 GEMMs accumulated
+    exactly in float64, fp32 dequantisation, clamped SiLU-mul to bf16,
+    requantisation, the down GEMM, and the routing-weighted sum over slots in
+    fp32. Returns the fp32 [T, H] partial output of the given experts."""
+    import torch
+
+    q13, s13, q2, s2 = (torch.from_numpy(a) for a in host)
+    T, Hd = x_bf16.shape
+    I = q2.shape[2]
+    kt = cfg["k"] + (1 if cfg["shared"] else 0)
+    xf = x_bf16.float()
+    xs = (xf.abs().amax(1) / 127.0).clamp_min(1.0e-30)
+    xq = (xf / xs[:, None]).round().clamp(-127, 127).double()
+    wt = torch.from_numpy(w)
+    out = torch.zeros((T, Hd), dtype=torch.float32)
+    for j, e in enumerate(experts):
+        r = torch.from_numpy(routes[j])
+        if r.numel() == 0:
+            continue
+        tok, slot = r // kt, r % kt
+        if cfg["shared"] and e == cfg["E"]:
+            rw = torch.ones(r.numel(), dtype=torch.float32)
+        else:
+            rw = wt[tok, slot] * cfg["scale"] if cfg["shared"] else wt[tok, slot]
+        acc = (xq[tok] @ q13[j].double().T).float() * xs[tok][:, None] * s13[j]
+        gate = acc[:, :I].clamp(max=10.0)
+        up = acc[:, I:].clamp(-10.0, 10.0)
+        act = (gate * up / (1.0 + torch.exp(-gate))).to(torch.bfloat16).float()
+        s_act = (act.abs().amax(1) / 127.0).clamp_min(1.0e-30)
+        aq = (act / s_act[:, None]).round().clamp(-127, 127).double()
+        route = (aq @ q2[j].double().T).float() * s_act[:, None] * s2[j]
+        out.index_add_(0, tok, route * rw[:, None])
+    return out
+
+
+def cpu_baseline_torch(cfg, res, budget_experts: int):
+    """The north-star CPU baseline: the repo tests' PyTorch eager reference
+    (grouped per expert, float64 accumulation) on this host's cores, timed on
+    a seeded uniform sample of the active experts and scaled to the layer;
+    median of 3 after 1 warmup."""
+    import torch
+
+    experts, n_active, _ = _expert_sample(cfg, res["ids"], budget_experts)
+    host = _host_experts(res["dev_int8"], experts)
+    routes, _ = _expert_routes(cfg, res["ids"], experts)
+    x = res["x"].cpu()
+    torch.set_num_threads(torch.get_num_threads())
+    torch_eager_expert_layer(x, res["ids"], res["w"], cfg, experts[:2], tuple(a[:2] for a in host), routes[:2])
     times = []
-    done = 0
     for _ in range(3):
         t0 = time.perf_counter()
-        done = oracle.w8a8_expert_range(x_bits, sorted_routes, offsets, kt, q13, s13, q2, s2, 0, e_end, route_out)
+        torch_eager_expert_layer(x, res["ids"], res["w"], cfg, experts, host, routes)
         times.append(time.perf_counter() - t0)
     t = float(np.median(times))
-    routes_per_s = done / t
-    layer_s = R / routes_per_s
+    layer_s = t * n_active / len(experts)
+    rows = sum(len(r) for r in routes)
+    return {
+        "value": round(cfg["T"] / layer_s, 2),
+        "unit": "tokens/s",
+        "cores": torch.get_num_threads(),
+        "kind": "torch_eager",
+        "sample": f"PyTorch eager grouped restatement of tests/test_moe_w8a8.py:40-69 (float64 GEMMs, "
+                  f"{torch.get_num_threads()} threads) on a seeded uniform sample of {len(experts)} of the "
+                  f"{n_active} active experts ({rows} routes), median of 3 = {t:.2f}s after 1 warmup, "
+                  f"scaled by {n_active}/{len(experts)} to the full layer ({layer_s:.2f}s/layer)",
+    }
+
+
+def cpu_baseline_oracle(cfg, res, budget_experts: int):
+    """The C oracle (oracle/, OpenMP), grouped per expert, on the same kind of
+    expert sample as cpu_baseline_torch, scaled to the layer."""
+    import oracle
+
+    experts, n_active, _ = _expert_sample(cfg, res["ids"], budget_experts)
+    host = _host_experts(res["dev_int8"], experts)
+    routes, kt = _expert_routes(cfg, res["ids"], experts)
+    offsets = np.zeros(len(experts) + 1, np.int64)
+    offsets[1:] = np.cumsum([len(r) for r in routes])
+    sorted_routes = np.concatenate(routes).astype(np.int64)
+    x_bits = res["x"].cpu().view(__import__("torch").int16).numpy().view(np.uint16)
+    route_out = np.zeros((cfg["T"] * kt, cfg["H"]), np.float32)
+    q13, s13, q2, s2 = host
+    oracle.w8a8_expert_range(x_bits, sorted_routes, offsets, kt, q13, s13, q2, s2, 0, min(2, len(experts)),
+                             route_out)
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        oracle.w8a8_expert_range(x_bits, sorted_routes, offsets, kt, q13, s13, q2, s2, 0, len(experts), route_out)
+        times.append(time.perf_counter() - t0)
+    t = float(np.median(times))
+    layer_s = t * n_active / len(experts)
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
     return {
         "value": round(cfg["T"] / layer_s, 2),
         "unit": "tokens/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"oracle grouped W8A8 layer (OpenMP, {threads} threads), experts 0..{e_end - 1} = {done} of {R} "
-                  f"routes, median of 3 = {t:.2f}s, scaled to the full layer ({layer_s:.2f}s/layer)",
+        "sample": f"C oracle grouped W8A8 (OpenMP, {threads} threads) on the same {len(experts)}-of-{n_active} "
+                  f"expert sample, median of 3 = {t:.2f}s, scaled to the layer ({layer_s:.2f}s/layer)",
     }
 
 
-def parity_check(cfg, res) -> dict:
-    """Bit-exact check of a few tokens against the oracle (same routing, same weights)."""
+def parity_check(cfg, res, n: int = 4) -> dict:
+    """Bit-exact check of n tokens (the first n-1 and the last) against the
+    oracle, on host copies of only the experts they touch."""
     import oracle
 
-    q13, s13, q2, s2 = res["host"]
-    n = min(4, cfg["T"])
-    x_bits = res["x"][:n].cpu().view(__import__("torch").int16).numpy().view(np.uint16)
+    T = cfg["T"]
+    tok = np.unique(np.array(list(range(min(n - 1, T))) + [T - 1]))
     sid = cfg["E"] if cfg["shared"] else -1
-    ref = oracle.w8a8_forward(x_bits, res["ids"][:n], res["w"][:n], q13, s13, q2, s2, shared_id=sid,
-                              routed_scale=cfg["scale"])
-    got = res["out"][:n].cpu().view(__import__("torch").int16).numpy().view(np.uint16)
-    return {"tokens_checked": n, "bit_exact": bool(np.array_equal(ref, got))}
+    touched = np.unique(res["ids"][tok])
+    local = np.searchsorted(touched, res["ids"][tok])
+    experts = np.append(touched, sid) if sid >= 0 else touched
+    q13, s13, q2, s2 = _host_experts(res["dev_int8"], experts)
+    import torch
+
+    tk = torch.from_numpy(tok).to(res["x"].device)
+    x_bits = res["x"][tk].cpu().view(torch.int16).numpy().view(np.uint16)
+    ref = oracle.w8a8_forward(x_bits, local, res["w"][tok], q13, s13, q2, s2,
+                              shared_id=len(experts) - 1 if sid >= 0 else -1, routed_scale=cfg["scale"])
+    got = res["out"][tk].cpu().view(torch.int16).numpy().view(np.uint16)
+    return {"tokens_checked": int(len(tok)), "bit_exact": bool(np.array_equal(ref, got))}
 
 
 def measured_traffic(config: str, stage: str):
@@ -343,7 +498,7 @@ def measured_traffic(config: str, stage: str):
         return None
 
 
-def kernel_roofline(args, best, st_alg, peak_ops):
+def kernel_roofline(workload: str, best, st_alg, peak_ops):
     """Roofline of the dominant GEMM stage: its algorithmic bytes or ops over its
     average launch time (library hipEvents on the launch stream)."""
     name, tot, n = best
@@ -359,16 +514,15 @@ def kernel_roofline(args, best, st_alg, peak_ops):
         achieved = a["ops"] / (avg_ms * 1e-3) / 1e12
         roof = {"bound": "mfma", "achieved": round(achieved, 1), "peak": peak_ops, "unit": "TFLOP/s",
                 "frac": round(achieved / peak_ops, 4)}
-    traffic = measured_traffic(args.config, name)
+    traffic = measured_traffic(workload, name)
     roof.update({"kernel": f"grouped_gemm {name}", "avg_launch_ms": round(avg_ms, 4), "traffic": traffic,
                  "algorithmic_bytes": a["bytes"], "algorithmic_ops": a["ops"], "experts": a["experts"],
                  "rows": a["rows"]})
     return roof
 
 
-def measure(cfg, args, device, want_cpu: bool):
-    res = run_gpu(cfg, args.steps, args.warmup, device, keep_host=want_cpu or cfg["kind"] == "w8a8",
-                  graph=args.graph)
+def measure(cfg, workload: str, args, device, want_cpu: bool):
+    res = run_gpu(cfg, args.steps, args.warmup, device, graph=args.graph)
     counts = expert_counts(cfg, res["ids"])
     layer_bytes, layer_ops, st_alg = algorithmic(cfg, counts)
     ms = res["ms"]
@@ -380,26 +534,35 @@ def measure(cfg, args, device, want_cpu: bool):
     peak_ops = INT8_PEAK_TOPS if cfg["kind"] == "w8a8" else BF16_PEAK_TFLOPS
     roof = None
     if best is not None:  # stage classes outside this model (W8A16 at prefill): no kernel roofline
-        roof = kernel_roofline(args, best, st_alg, peak_ops)
+        roof = kernel_roofline(workload, best, st_alg, peak_ops)
     layer_roof_s = max(layer_bytes / (HBM_PEAK_GBPS * 1e9), layer_ops / (peak_ops * 1e12))
     layer = {
         "bytes": layer_bytes, "ops": layer_ops, "active_experts": int((counts > 0).sum()),
         "zero_token_experts": int((counts[: cfg["E"]] == 0).sum()),
         "hbm_TBps": round(layer_bytes / (ms * 1e-3) / 1e12, 3),
         "ops_TOPS": round(layer_ops / (ms * 1e-3) / 1e12, 2),
+        "int8_mfma_frac": round(layer_ops / (ms * 1e-3) / 1e12 / peak_ops, 4),
         "roofline_ms": round(layer_roof_s * 1e3, 4),
         "roofline_frac": round(layer_roof_s * 1e3 / ms, 4),
         "stage_ms_per_step": {k: round(v[0] / args.steps, 4) for k, v in res["stages"].items()},
     }
+    if cfg["kind"] != "w8a8":
+        layer["bf16_mfma_frac"] = layer.pop("int8_mfma_frac")
     if res.get("tau") is not None:
         layer["zipf_tau"] = res["tau"]
     out = {"ms": ms, "tokens_per_s": cfg["T"] / (ms * 1e-3), "roofline": roof, "layer": layer}
-    if cfg["kind"] == "w8a8" and res["host"] is not None:
+    if cfg["kind"] == "w8a8":
         out["parity"] = parity_check(cfg, res)
     if want_cpu and cfg["kind"] == "w8a8":
-        max_routes = None if cfg["T"] * (cfg["k"] + 1) <= 1024 else args.cpu_routes
-        out["cpu_baseline"] = cpu_baseline(cfg, res, max_routes)
+        out["cpu_baseline"] = cpu_baseline_torch(cfg, res, args.cpu_experts)
+        out["cpu_baseline_oracle"] = cpu_baseline_oracle(cfg, res, args.cpu_experts)
+    del res
     return out
+
+
+# Extra workloads measured by default after the headline one, each on its own
+# layer: the prefill configs and decode at its smallest batches.
+SECONDARY = [("c3", "c3", 0), ("c4", "c4", 0), ("c2_t1", "c2", 1), ("c2_t2", "c2", 2), ("c1", "c1", 0)]
 
 
 def int_mm_reference() -> int:
@@ -436,11 +599,14 @@ def main() -> int:
     ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
     ap.add_argument("--tokens", type=int, default=0,
                     help="override the config's token count (e.g. small-batch decode on the C2 shape)")
-    ap.add_argument("--prefill", action="store_true", help="also measure C3 prefill as 'secondary'")
+    ap.add_argument("--no-secondary", action="store_true",
+                    help="measure only the selected config (by default the C2 line also carries C3, C4, decode "
+                         "at T=1 and T=2, and C1 as 'secondary' entries)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--graph", action="store_true",
                     help="time replays of one forward captured into a HIP graph (removes per-launch host cost)")
-    ap.add_argument("--cpu-routes", type=int, default=2048, help="route sample of the CPU baseline at prefill")
+    ap.add_argument("--cpu-experts", type=int, default=24,
+                    help="active experts in the seeded sample the CPU baselines are timed on")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 256 MiB device copy 5 times (scale reference for rocprofv3 "
                          "FETCH_SIZE / WRITE_SIZE counters)")
@@ -472,7 +638,8 @@ def main() -> int:
     cfg = CONFIGS[args.config]
     if args.tokens > 0:
         cfg = dict(cfg, T=args.tokens, desc=f"{cfg['desc']} (T overridden to {args.tokens})")
-    res = measure(cfg, args, device, want_cpu=not args.no_cpu_baseline)
+    workload = args.config if args.tokens <= 0 else f"{args.config}_t{args.tokens}"
+    res = measure(cfg, workload, args, device, want_cpu=not args.no_cpu_baseline)
     line = {
         "metric": {"w8a8": "W8A8", "w8a16": "W8A16", "bf16": "BF16"}[cfg["kind"]] + " MoE-layer tokens/s",
         "value": round(res["tokens_per_s"], 1),
@@ -497,15 +664,20 @@ def main() -> int:
         line["parity"] = res["parity"]
     if "cpu_baseline" in res:
         line["cpu_baseline"] = res["cpu_baseline"]
-    if args.prefill and args.config == "c2":
-        import gc
-
-        gc.collect()
-        torch.cuda.empty_cache()
-        sec = measure(CONFIGS["c3"], args, device, want_cpu=False)
-        line["secondary"] = {"workload": CONFIGS["c3"]["desc"], "tokens_per_s": round(sec["tokens_per_s"], 1),
-                             "ms_per_step": round(sec["ms"], 4), "roofline": sec["roofline"],
-                             "layer": sec["layer"], "parity": sec.get("parity")}
+        line["cpu_baseline_oracle"] = res["cpu_baseline_oracle"]
+    if args.config == "c2" and args.tokens <= 0 and not args.no_secondary:
+        line["secondary"] = []
+        for wl, name, tokens in SECONDARY:
+            c = CONFIGS[name] if tokens <= 0 else dict(CONFIGS[name], T=tokens,
+                                                       desc=f"{CONFIGS[name]['desc']}, run at T={tokens}")
+            log(f"[bench] secondary {wl}: {c['desc']}")
+            sec = measure(c, wl, args, device, want_cpu=False)
+            entry = {"workload": c["desc"], "dtype": "int8" if c["kind"] == "w8a8" else "bf16",
+                     "tokens_per_s": round(sec["tokens_per_s"], 1), "ms_per_step": round(sec["ms"], 4),
+                     "roofline": sec["roofline"], "layer": sec["layer"]}
+            if "parity" in sec:
+                entry["parity"] = sec["parity"]
+            line["secondary"].append(entry)
     print(json.dumps(line), flush=True)
     return 0
 

@@ -134,9 +134,12 @@ Bf16Layout bf16_layout(const fcmoe_moe_args* a, Arena& ar, bool w8 = false) {
   L.hp = round_up(a->hidden, kmul);
   L.ip = round_up(a->inter, kmul);
   L.gu_ld = 2 * round_up(a->inter, 16);
-  // W8A16's 128/256-row tiles run on the LDS-staged kernel, whose A must stay
-  // under 2 GiB; beyond that the forward keeps to the 16/32-row tiles.
-  const bool w8_lds = a->tokens * L.hp * 2 < kLdsMaxABytes && L.routes * L.ip * 2 < kLdsMaxABytes;
+  // W8A16's 128/256-row tiles run on the LDS-staged kernel, whose buffer
+  // offsets are 32-bit: A and one expert's packed weights must stay under
+  // 2 GiB; beyond that the forward keeps to the 16/32-row tiles.
+  const bool w8_lds = a->tokens * L.hp * 2 < kLdsMaxABytes && L.routes * L.ip * 2 < kLdsMaxABytes &&
+                      fcmoe_packed_expert_bytes(1, 2 * a->inter, a->hidden, 2) < kLdsMaxABytes &&
+                      fcmoe_packed_expert_bytes(1, a->hidden, a->inter, 1) < kLdsMaxABytes;
   if (w8)
     L.tc = make_tile_classes(kClassBMW8,
                              L.routes <= kDecodeRowsPerExpert * a->experts ? 1 : (w8_lds ? kNumClassesW8 : 2),
@@ -618,6 +621,21 @@ extern "C" size_t fcmoe_w8a16_workspace_bytes(const fcmoe_moe_args* a) {
 
 extern "C" int fcmoe_w8a16_forward(const fcmoe_moe_args* a, hipStream_t stream) {
   return bf16_family_forward(a, stream, true);
+}
+
+extern "C" int fcmoe_bf16_stage_views(const fcmoe_moe_args* a, int w8a16, const int32_t** route_pos,
+                                      const float** route_weight, const float** route_out) {
+  int rc = check_common(a);
+  if (rc) return rc;
+  Arena ar;
+  ar.base = (char*)a->workspace;
+  ar.cap = a->workspace_bytes;
+  Bf16Layout L = bf16_layout(a, ar, w8a16 != 0);
+  if (!ar.ok() || !ar.base) return fail(FCMOE_ESPACE, "workspace too small");
+  if (route_pos) *route_pos = L.rb.route_pos;
+  if (route_weight) *route_weight = L.rb.route_weight;
+  if (route_out) *route_out = L.route_out;
+  return FCMOE_OK;
 }
 
 // ---------------------------------------------------------------- i8gemm --

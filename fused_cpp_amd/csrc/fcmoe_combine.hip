@@ -33,12 +33,17 @@ struct TreeSum<Begin, 1> {
   __device__ __forceinline__ static float run(const float* v) { return v[Begin]; }
 };
 
+// A dropped (invalid) route's row was never written: its leaf is 0 by a
+// select, so whatever the row holds (NaN included) cannot reach the sum.
 template <int K>
-__device__ __forceinline__ float tree_merge(const float* route_out, const float* w, int64_t r0, int64_t hidden,
-                                            int64_t h) {
+__device__ __forceinline__ float tree_merge(const float* route_out, const float* w, const int32_t* route_pos,
+                                            int64_t r0, int64_t hidden, int64_t h) {
   float v[K];
 #pragma unroll
-  for (int s = 0; s < K; ++s) v[s] = route_out[(r0 + s) * hidden + h] * w[r0 + s];
+  for (int s = 0; s < K; ++s) {
+    const float prod = route_out[(r0 + s) * hidden + h] * w[r0 + s];
+    v[s] = route_pos[r0 + s] >= 0 ? prod : 0.0f;
+  }
   return TreeSum<0, K>::run(v);
 }
 
@@ -84,16 +89,16 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* route_out, co
     for (int v = 0; v < VW; ++v) {
       switch (kt) {
         case 2:
-          acc[v] = tree_merge<2>(route_out, route_weight, r0, hidden, h0 + v);
+          acc[v] = tree_merge<2>(route_out, route_weight, route_pos, r0, hidden, h0 + v);
           break;
         case 4:
-          acc[v] = tree_merge<4>(route_out, route_weight, r0, hidden, h0 + v);
+          acc[v] = tree_merge<4>(route_out, route_weight, route_pos, r0, hidden, h0 + v);
           break;
         case 6:
-          acc[v] = tree_merge<6>(route_out, route_weight, r0, hidden, h0 + v);
+          acc[v] = tree_merge<6>(route_out, route_weight, route_pos, r0, hidden, h0 + v);
           break;
         default:
-          acc[v] = tree_merge<8>(route_out, route_weight, r0, hidden, h0 + v);
+          acc[v] = tree_merge<8>(route_out, route_weight, route_pos, r0, hidden, h0 + v);
           break;
       }
     }

@@ -49,20 +49,27 @@ __global__ __launch_bounds__(kRouterWaves * kWave) void router_topk_kernel(const
   }
   s = wave_sum(s);
 
-  // k rounds of argmax; the winner's slot is knocked out with -inf (NaN
-  // logits never win: every comparison with NaN is false)
+  // k rounds of argmax over the experts not chosen yet (a per-lane bit per
+  // value slot). NaN logits never win: every comparison with NaN is false.
+  // When no candidate is left (the rest are NaN), the lowest unchosen id is
+  // taken, so the k ids of a row are always distinct.
   float psel = 0.0f;  // lane s of the wave keeps winner s's probability
   int esel = 0;
   float psum = 0.0f;
+  uint32_t chosen = 0;
   for (int r = 0; r < top_k; ++r) {
     float bv = -INFINITY;
     int be = 0x7fffffff;
+    int first_free = 0x7fffffff;
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
       const int e = lane + i * kWave;
-      if (e < experts && (v[i] > bv || (v[i] == bv && e < be))) {
-        bv = v[i];
-        be = e;
+      if (e < experts && !((chosen >> i) & 1u)) {
+        if (e < first_free) first_free = e;
+        if (v[i] > bv || (v[i] == bv && e < be)) {
+          bv = v[i];
+          be = e;
+        }
       }
     }
 #pragma unroll
@@ -73,11 +80,15 @@ __global__ __launch_bounds__(kRouterWaves * kWave) void router_topk_kernel(const
         bv = ov;
         be = oe;
       }
+      first_free = min(first_free, __shfl_xor(first_free, off));
     }
-    if (be == 0x7fffffff) be = r;  // fewer finite logits than k: fill in id order
+    if (be == 0x7fffffff) {  // only NaN logits left
+      be = first_free;
+      bv = -INFINITY;
+    }
 #pragma unroll
     for (int i = 0; i < VPL; ++i)
-      if (lane + i * kWave == be) v[i] = -INFINITY;
+      if (lane + i * kWave == be) chosen |= 1u << i;
     const float p = expf(bv - m) / s;
     psum += p;
     if (lane == r) {

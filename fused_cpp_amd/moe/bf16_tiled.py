@@ -193,11 +193,18 @@ def _weights_f32(topk_weights: torch.Tensor, scaling: float = 1.0) -> tuple[torc
     return scaled.to(torch.float32).contiguous(), 1.0
 
 
-def _check_routed_range(topk_ids: torch.Tensor, routed_experts: int) -> None:
-    if topk_ids.numel() > 0 and _native.validate_ids_default():
-        lo, hi = int(topk_ids.min().item()), int(topk_ids.max().item())
-        if lo < 0 or hi >= routed_experts:
-            raise ValueError(f"routed topk_ids must be in [0, {routed_experts}), got [{lo}, {hi}]")
+def _routed_range_checked(routed_experts: int, call):
+    """Run a routed+shared forward. The route kernel counts ids outside
+    [0, routed_experts) on the device and the extension reads that count once
+    after the launch (when id validation is on); an out-of-range id is raised
+    as the reference's ValueError (bf16_tiled.py routed+shared wrappers), with
+    no host synchronisation before the launch."""
+    try:
+        return call()
+    except RuntimeError as exc:
+        if "topk_ids out of range" in str(exc):
+            raise ValueError(f"routed topk_ids must be in [0, {routed_experts}): {exc}") from None
+        raise
 
 
 def _to_device(t: torch.Tensor) -> torch.Tensor:
@@ -490,13 +497,13 @@ def fused_moe_bf16_tiled_with_shared(
     if _activation_name(activation) != "silu":
         raise ValueError("routed+shared BF16 scheduling currently requires activation='silu'")
     _validate_output_buffer(input, out)
-    _check_routed_range(topk_ids, weights.routed_experts)
     if int(input.shape[0]) == 0:
         return out if out is not None else torch.empty_like(input)
     w, scale = _weights_f32(topk_weights, scaling)
-    return _bf16_call(input, weights.packed, w, _ids(topk_ids), w13_bias=None, w2_bias=None, activation=native_act,
-                      global_num_experts=weights.routed_experts, skip_weighted=False,
-                      shared_id=weights.shared_expert_id, scaling=scale, out=out)
+    return _routed_range_checked(weights.routed_experts, lambda: _bf16_call(
+        input, weights.packed, w, _ids(topk_ids), w13_bias=None, w2_bias=None, activation=native_act,
+        global_num_experts=weights.routed_experts, skip_weighted=False, shared_id=weights.shared_expert_id,
+        scaling=scale, out=out))
 
 
 def shared_mlp_bf16_tiled(
@@ -705,12 +712,12 @@ def fused_moe_w8a8_tiled_with_shared(
     if _activation_name(activation) != "silu" or float(swiglu_limit) != 10.0:
         raise ValueError("routed+shared W8A8 requires activation='silu' with swiglu_limit=10.0")
     _validate_output_buffer(input, out)
-    _check_routed_range(topk_ids, weights.routed_experts)
     if int(input.shape[0]) == 0:
         return out if out is not None else torch.empty_like(input)
     w, scale = _weights_f32(topk_weights, scaling)
-    return _w8a8_call(input, weights.packed, w, _ids(topk_ids), shared_id=weights.shared_expert_id, scaling=scale,
-                      out=out, valid_experts=weights.routed_experts)
+    return _routed_range_checked(weights.routed_experts, lambda: _w8a8_call(
+        input, weights.packed, w, _ids(topk_ids), shared_id=weights.shared_expert_id, scaling=scale, out=out,
+        valid_experts=weights.routed_experts))
 
 
 # --------------------------------------------------------------- W8A16 ops --
@@ -849,13 +856,12 @@ def fused_moe_w8a16_tiled_with_shared(
     if _activation_name(activation) != "silu":
         raise ValueError("routed+shared W8A16 scheduling currently requires activation='silu'")
     _validate_output_buffer(input, out)
-    _check_routed_range(topk_ids, weights.routed_experts)
     if int(input.shape[0]) == 0:
         return out if out is not None else torch.empty_like(input)
     w, scale = _weights_f32(topk_weights, scaling)
-    return _w8a16_call(input, weights.packed, w, _ids(topk_ids), activation=native_act,
-                       global_num_experts=weights.routed_experts, skip_weighted=False,
-                       shared_id=weights.shared_expert_id, scaling=scale, out=out)
+    return _routed_range_checked(weights.routed_experts, lambda: _w8a16_call(
+        input, weights.packed, w, _ids(topk_ids), activation=native_act, global_num_experts=weights.routed_experts,
+        skip_weighted=False, shared_id=weights.shared_expert_id, scaling=scale, out=out))
 
 
 # ------------------------------------------------------------- dispatcher --

@@ -202,6 +202,15 @@ int fcmoe_w8a8_stage_views(const fcmoe_moe_args* args, const int32_t** sorted_ro
                            int64_t* ldy, const int8_t** q2, int64_t* ldq, const float** s2row,
                            const float** route_out);
 
+/* The same for the last fcmoe_bf16_forward (w8a16 = 0) or fcmoe_w8a16_forward
+ * (w8a16 = 1) that used `workspace`: route_pos [R] (flat route -> sorted
+ * position, -1 for a dropped route), route_weight [R] (the combined weight
+ * each route row is merged with: routed weight x routed_scaling, 1.0 for the
+ * shared slot) and route_out [R, hidden] fp32 (the W2 rows the top-k merge of
+ * csrc/moe/arm/sve_bf16/route_merge.cpp:47-126 reads). */
+int fcmoe_bf16_stage_views(const fcmoe_moe_args* args, int w8a16, const int32_t** route_pos,
+                           const float** route_weight, const float** route_out);
+
 /* ---- stage timing ------------------------------------------------------ */
 
 /* Stage ids for fcmoe_stage_timing_read. W13 / W2 class stages are per tile

@@ -67,6 +67,7 @@ def lib() -> ctypes.CDLL:
         l.orc_gemm_i8_rows.argtypes = [_P, _I64, _P, _I64, _P, _I64, _I64, _P]
         l.orc_i8gemm.argtypes = [_P, _I, _I64, _I64, _P, _P, _I64, _P, _I, _P]
         l.orc_bf16_activation.argtypes = [_P, _I64, _I64, _I, _P]
+        l.orc_bf16_route_merge.argtypes = [_P, _P, _I64, _I64, _I64, _P]
         _lib = l
     return _lib
 
@@ -242,6 +243,20 @@ def bf16_activation(gate_up: np.ndarray, mode: str) -> np.ndarray:
     y = np.empty((rows, two_f // 2), np.uint16)
     lib().orc_bf16_activation(_ptr(gate_up), rows, two_f // 2, _ACT_MODES[mode], _ptr(y))
     return y
+
+
+def bf16_route_merge(route_out: np.ndarray, weights: np.ndarray, kt: int) -> np.ndarray:
+    """BF16 executor's top-k merge (csrc/moe/arm/sve_bf16/route_merge.cpp:38-126):
+    route_out [T*kt, H] fp32 rows by flat route, weights [T*kt] fp32 -> bf16
+    bits [T, H]. kt in {2,4,6,8}: weighted leaves summed as a power-of-two
+    split tree; otherwise an ordered fused multiply-add chain."""
+    route_out = _c(route_out, np.float32)
+    weights = _c(weights, np.float32).reshape(-1)
+    rows, hidden = route_out.shape
+    tokens = rows // kt
+    out = np.empty((tokens, hidden), np.uint16)
+    lib().orc_bf16_route_merge(_ptr(route_out), _ptr(weights), tokens, kt, hidden, _ptr(out))
+    return out
 
 
 # ---- BF16 fused MoE fp32 reference -----------------------------------------

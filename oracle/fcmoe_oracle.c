@@ -385,3 +385,43 @@ void orc_bf16_activation(const float* gate_up, int64_t rows, int64_t f, int mode
     }
   }
 }
+
+/* ---- BF16 top-k merge (csrc/moe/arm/sve_bf16/route_merge.cpp:38-126) ----
+ * route_out rows are indexed by flat route t*kt + s. For kt in {2, 4, 6, 8}
+ * the SVE merge multiplies each row by its weight (weighted_leaf, :47-52) and
+ * adds the products as a tree that splits every range at the largest power of
+ * two below its length (reduce_fixed, :54-69): ((0+1)+(2+3))+(4+5) for 6.
+ * Other kt: acc = 0, then acc = fma(row_s, w_s, acc) for s = 0..kt-1
+ * (merge_dynamic_block, :78-86; svmla is a fused multiply-add). The fp32 sum
+ * is rounded to bf16 to nearest even. */
+static int orc_pow2_below(int n) {
+  int p = 1;
+  while ((p << 1) < n) p <<= 1;
+  return p;
+}
+
+static float orc_tree(const float* leaf, int begin, int count) {
+  if (count == 1) return leaf[begin];
+  const int left = orc_pow2_below(count);
+  const float a = orc_tree(leaf, begin, left);
+  const float b = orc_tree(leaf, begin + left, count - left);
+  return a + b;
+}
+
+void orc_bf16_route_merge(const float* route_out, const float* weights, int64_t tokens, int64_t kt, int64_t hidden,
+                          uint16_t* out) {
+  const int tree = kt == 2 || kt == 4 || kt == 6 || kt == 8;
+  for (int64_t t = 0; t < tokens; ++t) {
+    for (int64_t h = 0; h < hidden; ++h) {
+      float acc = 0.0f;
+      if (tree) {
+        float leaf[8];
+        for (int64_t s = 0; s < kt; ++s) leaf[s] = route_out[(t * kt + s) * hidden + h] * weights[t * kt + s];
+        acc = orc_tree(leaf, 0, (int)kt);
+      } else {
+        for (int64_t s = 0; s < kt; ++s) acc = fmaf(route_out[(t * kt + s) * hidden + h], weights[t * kt + s], acc);
+      }
+      out[t * hidden + h] = orc_f32_to_bf16(acc);
+    }
+  }
+}

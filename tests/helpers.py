@@ -236,3 +236,56 @@ def gpu_grouped_gemm_acc(a: np.ndarray, row_map, counts: np.ndarray, w: np.ndarr
                "grouped_gemm_i8_acc")
     torch.cuda.synchronize()
     return acc.cpu().numpy()[:total], offsets
+
+
+def gpu_bf16_forward(x, ids, w, w13, w2, device, *, shared_id: int = -1, scale: float = 1.0,
+                     activation: int = 0, valid_experts: int | None = None):
+    """Run fcmoe_bf16_forward through the C ABI on bf16-valued float32 inputs.
+    Returns (out bf16 bits [T, H], route_pos [R], route_weight [R], route_out [R, H])."""
+    import torch
+
+    from fused_cpp_amd import cabi
+
+    L = cabi.lib()
+    tokens, hidden = x.shape
+    experts, two_i, _ = w13.shape
+    inter = two_i // 2
+    p13 = pack_gpu(bf16_bits(w13).reshape(w13.shape), 2, device)
+    p2 = pack_gpu(bf16_bits(w2).reshape(w2.shape), 1, device)
+    xt = _t(bf16_bits(x).view(np.int16).reshape(x.shape), device)
+    top_k = ids.shape[1]
+    idt = _t(ids.astype(np.int64), device) if top_k else None
+    wt = _t(w.astype(np.float32), device) if top_k else None
+    out = torch.empty((tokens, hidden), dtype=torch.int16, device=device)
+    a = cabi.MoeArgs()
+    a.x = xt.data_ptr()
+    a.tokens, a.hidden, a.inter = tokens, hidden, inter
+    a.topk_ids = idt.data_ptr() if idt is not None else None
+    a.ids_is_i64 = 1
+    a.topk_weights = wt.data_ptr() if wt is not None else None
+    a.top_k = top_k
+    a.experts = experts
+    a.valid_experts = valid_experts or experts
+    a.shared_expert_id = shared_id
+    a.routed_scaling = scale
+    a.w13, a.w2 = p13.data_ptr(), p2.data_ptr()
+    a.activation = activation
+    a.out = out.data_ptr()
+    wsb = L.fcmoe_bf16_workspace_bytes(ctypes.byref(a))
+    ws = torch.empty(wsb, dtype=torch.uint8, device=device)
+    a.workspace, a.workspace_bytes = ws.data_ptr(), wsb
+    cabi.check(L.fcmoe_bf16_forward(ctypes.byref(a), cabi.stream_handle()), "bf16_forward")
+    torch.cuda.synchronize()
+    views = [ctypes.c_void_p() for _ in range(3)]
+    cabi.check(L.fcmoe_bf16_stage_views(ctypes.byref(a), 0, ctypes.byref(views[0]), ctypes.byref(views[1]),
+                                        ctypes.byref(views[2])), "bf16_stage_views")
+    kt = top_k + (1 if shared_id >= 0 else 0)
+    R = tokens * kt
+
+    def grab(p, n, dtype):
+        t = torch.empty(n, dtype=dtype, device=device)
+        cabi_copy(t, p.value, n * t.element_size())
+        return t.cpu().numpy()
+
+    return (out.cpu().numpy().view(np.uint16), grab(views[0], R, torch.int32), grab(views[1], R, torch.float32),
+            grab(views[2], R * hidden, torch.float32).reshape(R, hidden))

@@ -56,10 +56,30 @@ def test_router_ties_and_infinities(gpu, oracle_lib):
     ids, w = _run(x, 3)
     assert ids[0].tolist() == [0, 1, 2]
     assert ids[1].tolist() == [3, 9, 66]
-    assert ids[2][:2].tolist() == [5, 40]
+    # fewer finite logits than k: the rest in id order, never a repeated id
+    assert ids[2].tolist() == [5, 40, 0]
     assert ids[3].tolist() == [0, 1, 2]
+    np.testing.assert_array_equal(ids, oracle_lib.router_topk(x, 3)[0])
+    for row in ids:
+        assert len(set(row.tolist())) == 3
     np.testing.assert_allclose(w[[0, 1, 3]], oracle_lib.router_topk(x[[0, 1, 3]], 3)[1], rtol=RTOL)
     np.testing.assert_allclose(w[2].sum(), 1.0, rtol=1e-6)
+
+
+def test_router_ids_distinct_with_infinities_and_nans(gpu, oracle_lib):
+    """One finite logit and k = 2, or NaNs only: ids stay distinct (an expert
+    already chosen never wins a later round) and follow the oracle's order
+    (NaN logits rank last, lower id first)."""
+    x = np.full((3, 4), -np.inf, np.float32)
+    x[0, 0] = 1.0                      # [1, -inf, -inf, -inf], k = 2
+    x[1, :] = np.nan
+    x[2, :] = [np.nan, 0.5, np.nan, -np.inf]
+    ids, w = _run(x, 2)
+    assert ids[0].tolist() == [0, 1]
+    assert ids[1].tolist() == [0, 1]
+    assert ids[2].tolist() == [1, 3]
+    np.testing.assert_array_equal(ids, oracle_lib.router_topk(x, 2)[0])
+    np.testing.assert_allclose(w[0], [1.0, 0.0], rtol=1e-6)
 
 
 def test_router_feeds_w8a8_forward(gpu):

@@ -248,3 +248,32 @@ def test_deepseek_v4_w8a8_surface_matches_reference_names():
     if not ds._HAS_DEEPSEEK_V4_W8A8:
         with pytest.raises(RuntimeError):
             ds.prepare_deepseek_v4_w8a8_linear_weight(torch.zeros((4, 8), dtype=torch.bfloat16))
+
+
+def test_bench_torch_eager_baseline_matches_oracle():
+    """bench.py's CPU baseline (the reference test's eager formula, grouped per
+    expert) computes the same layer as the oracle: within a few bf16 ulps (it
+    rounds ties to even and uses torch.exp where the reference kernel rounds
+    half away and uses its FEXPA exp)."""
+    import numpy as np
+    import torch
+
+    import bench
+    import oracle
+    from tests import helpers as H
+
+    cfg = dict(kind="w8a8", T=40, H=256, I=128, E=6, k=3, shared=True, scale=2.5, skew=None)
+    x, ids, w, q13, s13, q2, s2 = H.w8a8_case(3, 40, 256, 128, 7, 3)
+    ids = ids % 6
+    experts = np.arange(7)
+    routes, _ = bench._expert_routes(cfg, ids, experts)
+    xb = torch.from_numpy(x.view(np.int16)).view(torch.bfloat16)
+    got = bench.torch_eager_expert_layer(xb, ids, w, cfg, experts, (q13, s13, q2, s2), routes)
+    ref = H.bits_to_f32(oracle.w8a8_forward(x, ids, w, q13, s13, q2, s2, shared_id=6, routed_scale=2.5))
+    got = got.to(torch.bfloat16).float().numpy()
+    assert np.abs(got - ref).max() <= 2e-2 * max(1.0, np.abs(ref).max())
+    # a uniform expert sample and its complement add up to the whole layer
+    a = bench.torch_eager_expert_layer(xb, ids, w, cfg, experts[:3], (q13[:3], s13[:3], q2[:3], s2[:3]), routes[:3])
+    b = bench.torch_eager_expert_layer(xb, ids, w, cfg, experts[3:], (q13[3:], s13[3:], q2[3:], s2[3:]), routes[3:])
+    full = bench.torch_eager_expert_layer(xb, ids, w, cfg, experts, (q13, s13, q2, s2), routes)
+    np.testing.assert_allclose((a + b).numpy(), full.numpy(), rtol=1e-5, atol=1e-5)

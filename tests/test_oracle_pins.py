@@ -343,3 +343,69 @@ def test_bf16_reference_matches_per_token_brute_force(oracle_lib):
             y = gu[:F] / (1 + np.exp(-gu[:F])) * gu[F:]
             ref[t] += w[t, s] * (w2[e].astype(np.float64) @ y + b2[e])
     np.testing.assert_allclose(got, ref, rtol=1e-4, atol=1e-4)
+
+
+def _f32(x):
+    return np.float32(x)
+
+
+@pytest.mark.parametrize("kt", [2, 4, 6, 8])
+def test_bf16_merge_tree_follows_reference_comment(oracle_lib, kt):
+    """route_merge.cpp:54-55 states the tree: split each range at its largest
+    power of two, so TopK=6 is ((0+1)+(2+3))+(4+5). Products are rounded
+    first (weighted_leaf, :47-52). Inputs mix magnitudes so a left fold, a
+    fused chain or another pairing round differently; the test shows that for
+    each alternative on some element, and that the oracle follows the stated
+    tree on every element."""
+    rng = np.random.default_rng(kt)
+    tokens, hidden = 3, 512
+    mag = np.array([1e7, 1.0, -1e7, 3.0, 1e-3, 7.0, -5.0, 2.0], np.float32)[:kt]
+    rows = (rng.standard_normal((tokens * kt, hidden)).astype(np.float32) * np.tile(mag, tokens)[:, None])
+    w = rng.uniform(0.1, 2.0, tokens * kt).astype(np.float32)
+    got = oracle_lib.bf16_route_merge(rows, w, kt)
+
+    def tree(p, b, c):
+        if c == 1:
+            return p[b]
+        left = 1
+        while left * 2 < c:
+            left *= 2
+        return _f32(tree(p, b, left) + tree(p, b + left, c - left))
+
+    prods = (rows.reshape(tokens, kt, hidden) * w.reshape(tokens, kt, 1)).astype(np.float32)
+    want = np.empty((tokens, hidden), np.float32)
+    fold = np.zeros((tokens, hidden), np.float32)
+    chain = np.zeros((tokens, hidden), np.float32)
+    for t in range(tokens):
+        for h in range(hidden):
+            want[t, h] = tree(prods[t, :, h], 0, kt)
+        for s in range(kt):
+            fold[t] = (fold[t] + prods[t, s]).astype(np.float32)
+            chain[t] = (rows.reshape(tokens, kt, hidden)[t, s].astype(np.float64) * np.float64(w[t * kt + s])
+                        + chain[t]).astype(np.float32)
+    np.testing.assert_array_equal(got, oracle_lib.f32_to_bf16_bits(want))
+    if kt > 2:  # for two leaves every order is the same sum
+        assert not np.array_equal(want, fold)
+        assert not np.array_equal(want, chain)
+
+
+@pytest.mark.parametrize("kt", [1, 3, 5, 9])
+def test_bf16_merge_ordered_chain_is_fused(oracle_lib, kt):
+    """Other top-k: acc = fma(row, w, acc) in slot order (merge_dynamic_block,
+    route_merge.cpp:78-86): equal to an exact-product float64 chain rounded
+    to float32 each step, and (for kt > 1) not to the unfused form."""
+    rng = np.random.default_rng(40 + kt)
+    tokens, hidden = 4, 777
+    rows = rng.standard_normal((tokens * kt, hidden)).astype(np.float32) * 100
+    w = rng.uniform(0.1, 2.0, tokens * kt).astype(np.float32)
+    got = oracle_lib.bf16_route_merge(rows, w, kt)
+    r3 = rows.reshape(tokens, kt, hidden)
+    acc = np.zeros((tokens, hidden), np.float32)
+    unfused = np.zeros((tokens, hidden), np.float32)
+    for s in range(kt):
+        ws = w.reshape(tokens, kt)[:, s:s + 1]
+        acc = (r3[:, s].astype(np.float64) * ws.astype(np.float64) + acc).astype(np.float32)
+        unfused = ((r3[:, s] * ws).astype(np.float32) + unfused).astype(np.float32)
+    np.testing.assert_array_equal(got, oracle_lib.f32_to_bf16_bits(acc))
+    if kt > 1:
+        assert not np.array_equal(acc, unfused)

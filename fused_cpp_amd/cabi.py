@@ -68,6 +68,7 @@ SIGNATURES = {
     "fcmoe_router_topk": (_I, [_P, _I64, _I64, _I64, _I, ctypes.c_float, _P, _I, _P, _P]),
     "fcmoe_w8a8_workspace_bytes": (_SZ, [ctypes.POINTER(MoeArgs)]),
     "fcmoe_w8a8_forward": (_I, [ctypes.POINTER(MoeArgs), _P]),
+    "fcmoe_w8a8_forward_noalloc": (_I, [ctypes.POINTER(MoeArgs), _P]),
     "fcmoe_bf16_workspace_bytes": (_SZ, [ctypes.POINTER(MoeArgs)]),
     "fcmoe_bf16_forward": (_I, [ctypes.POINTER(MoeArgs), _P]),
     "fcmoe_w8a16_workspace_bytes": (_SZ, [ctypes.POINTER(MoeArgs)]),
@@ -84,6 +85,7 @@ SIGNATURES = {
 }
 
 FCMOE_STAGE_COUNT = 24
+FCMOE_NOALLOC_SCRATCH_BYTES = 64 << 20
 STAGE_NAMES = {0: "route", 1: "quant", 2: "requant", 3: "act", 4: "combine",
                **{8 + c: f"w13_bm{bm}" for c, bm in enumerate((16, 32, 64, 128, 192, 256))},
                **{16 + c: f"w2_bm{bm}" for c, bm in enumerate((16, 32, 64, 128, 192, 256))}}

@@ -246,10 +246,11 @@ int side_streams(SideStreams** out) {
 bool timing_on();
 
 template <typename F>
-int run_classes(const TileClasses& tc, hipStream_t stream, F&& gemm) {
+int run_classes(const TileClasses& tc, hipStream_t stream, F&& gemm, bool serial = false) {
   // Stage timing brackets each launch with events on its stream, so it runs
   // the classes one after another: each event pair then times one kernel.
-  if (tc.n <= 1 || timing_on()) {
+  // `serial` does the same for callers that must not create streams.
+  if (tc.n <= 1 || serial || timing_on()) {
     for (int c = 0; c < tc.n; ++c) {
       const int rc = gemm(c, stream);
       if (rc) return rc;
@@ -365,7 +366,11 @@ extern "C" size_t fcmoe_w8a8_workspace_bytes(const fcmoe_moe_args* a) {
   return ar.used + 256;
 }
 
-extern "C" int fcmoe_w8a8_forward(const fcmoe_moe_args* a, hipStream_t stream) {
+namespace {
+
+// The W8A8 forward over a given workspace. serial_classes runs the class
+// launches of a GEMM stage on `stream` one after another (no side streams).
+int w8a8_run(const fcmoe_moe_args* a, char* ws_base, size_t ws_bytes, bool serial_classes, hipStream_t stream) {
   int rc = check_shapes(a);
   if (rc) return rc;
   if (a->activation != FCMOE_ACT_SILU_CLAMP10)
@@ -376,8 +381,8 @@ extern "C" int fcmoe_w8a8_forward(const fcmoe_moe_args* a, hipStream_t stream) {
   if (!a->w13_scale || !a->w2_scale) return fail(FCMOE_EINVAL, "W8A8 scales are NULL");
   if (a->tokens == 0) return FCMOE_OK;
   Arena ar;
-  ar.base = (char*)a->workspace;
-  ar.cap = a->workspace_bytes;
+  ar.base = ws_base;
+  ar.cap = ws_bytes;
   if (!ar.base) return fail(FCMOE_ESPACE, "workspace is NULL");
   W8A8Layout L = w8a8_layout(a, ar);
   if (!ar.ok()) return fail(FCMOE_ESPACE, "W8A8 workspace too small");
@@ -424,7 +429,7 @@ extern "C" int fcmoe_w8a8_forward(const fcmoe_moe_args* a, hipStream_t stream) {
     p.tile_count = L.rb.tile_count + c;
     Stage st(FCMOE_STAGE_W13_CLASS0 + class_slot(L.tc.bm[c]), s);
     return gemm_launch(kEpiW13SwigluI8, L.tc.bm[c], p, L.tc.bound[c], s);
-  });
+  }, serial_classes);
   if (rc) return rc;
   {
     Stage st(FCMOE_STAGE_REQUANT, stream);
@@ -457,10 +462,55 @@ extern "C" int fcmoe_w8a8_forward(const fcmoe_moe_args* a, hipStream_t stream) {
     p.tile_count = L.rb.tile_count + c;
     Stage st(FCMOE_STAGE_W2_CLASS0 + class_slot(L.tc.bm[c]), s);
     return gemm_launch(kEpiW2RouteI8, L.tc.bm[c], p, L.tc.bound[c], s);
-  });
+  }, serial_classes);
   if (rc) return rc;
   Stage st(FCMOE_STAGE_COMBINE, stream);
   return combine_launch(L.route_out, L.rb.route_weight, L.rb.route_pos, a->tokens, L.kt, H, 0, 0, a->out, stream);
+}
+
+// Scratch of fcmoe_w8a8_forward_noalloc: one copy per GPU, held until the
+// process ends. Host code never passes `scratch` itself (on the host the name
+// is a stand-in, not a device address): each device's address comes from
+// hipGetSymbolAddress, looked up once per device with that device current.
+__device__ __align__(256) char scratch[FCMOE_NOALLOC_SCRATCH_BYTES];
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+int scratch_ptr(void** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return fail(FCMOE_EDEVICE, "hipGetDevice failed");
+  std::lock_guard<std::mutex> g(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(FCMOE_EDEVICE, std::string("hipGetSymbolAddress(scratch) failed: ") + hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return FCMOE_OK;
+}
+
+}  // namespace
+
+extern "C" int fcmoe_w8a8_forward(const fcmoe_moe_args* a, hipStream_t stream) {
+  if (!a) return fail(FCMOE_EINVAL, "args is NULL");
+  return w8a8_run(a, (char*)a->workspace, a->workspace_bytes, false, stream);
+}
+
+extern "C" int fcmoe_w8a8_forward_noalloc(const fcmoe_moe_args* a, hipStream_t stream) {
+  int rc = check_shapes(a);
+  if (rc) return rc;
+  const size_t need = fcmoe_w8a8_workspace_bytes(a);
+  if (need > (size_t)FCMOE_NOALLOC_SCRATCH_BYTES)
+    return fail(FCMOE_ESPACE, "w8a8_forward_noalloc: this call needs " + std::to_string(need) +
+                                  " bytes of scratch, more than the fixed " +
+                                  std::to_string((size_t)FCMOE_NOALLOC_SCRATCH_BYTES) + " bytes");
+  void* ws = nullptr;
+  if ((rc = scratch_ptr(&ws))) return rc;
+  return w8a8_run(a, (char*)ws, FCMOE_NOALLOC_SCRATCH_BYTES, true, stream);
 }
 
 extern "C" int fcmoe_w8a8_stage_views(const fcmoe_moe_args* a, const int32_t** sorted_routes, const uint16_t** y,

@@ -138,6 +138,21 @@ typedef struct fcmoe_moe_args {
 size_t fcmoe_w8a8_workspace_bytes(const fcmoe_moe_args* args);
 int fcmoe_w8a8_forward(const fcmoe_moe_args* args, hipStream_t stream);
 
+/* W8A8 forward that allocates nothing. No counterpart in the reference: it is
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). Same
+ * arguments and results as fcmoe_w8a8_forward; args->workspace and
+ * args->workspace_bytes are ignored. Its workspace is a fixed per-GPU device
+ * array of FCMOE_NOALLOC_SCRATCH_BYTES bytes (held until the process ends),
+ * so calls with fcmoe_w8a8_workspace_bytes(args) above that size fail with
+ * FCMOE_ESPACE (at H = 7168, F = 2048, top-8 + shared: up to ~200 tokens).
+ * Every call on one GPU shares that array: calls that overlap on one GPU
+ * (different streams, or host threads) race and must be serialised by the
+ * caller. Tile classes of a GEMM stage run in order on `stream`; no side
+ * streams or events are created. */
+#define FCMOE_NOALLOC_SCRATCH_BYTES (64ll << 20)
+int fcmoe_w8a8_forward_noalloc(const fcmoe_moe_args* args, hipStream_t stream);
+
 /* BF16 fused MoE (bf16 MFMA, fp32 accumulation, bf16 intermediate, fp32 route
  * rows, top-k merge). Replaces fused_moe_bf16_tiled
  * (csrc/moe/arm/common/fused_moe_bf16_tiled.cpp:6376-7218) behind

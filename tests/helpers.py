@@ -130,8 +130,10 @@ def gpu_quant_rows(x: np.ndarray, rounding: int, device, ldq: int | None = None)
 
 
 def gpu_w8a8_forward(x, ids, w, q13, s13, q2, s2, device, *, shared_id: int = -1, scale: float = 1.0,
-                     ids_i64: bool = True, packed=None, stages: bool = False, valid_experts: int | None = None):
-    """Run fcmoe_w8a8_forward; returns out bf16 bits (and stage buffers)."""
+                     ids_i64: bool = True, packed=None, stages: bool = False, valid_experts: int | None = None,
+                     noalloc: bool = False):
+    """Run fcmoe_w8a8_forward (fcmoe_w8a8_forward_noalloc with noalloc=True);
+    returns out bf16 bits (and stage buffers)."""
     import torch
 
     from fused_cpp_amd import cabi
@@ -165,6 +167,12 @@ def gpu_w8a8_forward(x, ids, w, q13, s13, q2, s2, device, *, shared_id: int = -1
     a.activation = cabi.FCMOE_ACT_SILU_CLAMP10
     a.out = out.data_ptr()
     a.invalid_count = inv.data_ptr()
+    if noalloc:
+        if stages:
+            raise ValueError("stage views need a caller workspace")
+        cabi.check(L.fcmoe_w8a8_forward_noalloc(ctypes.byref(a), cabi.stream_handle()), "w8a8_forward_noalloc")
+        torch.cuda.synchronize()
+        return out.cpu().numpy().view(np.uint16)
     wsb = L.fcmoe_w8a8_workspace_bytes(ctypes.byref(a))
     ws = torch.empty(wsb, dtype=torch.uint8, device=device)
     a.workspace, a.workspace_bytes = ws.data_ptr(), wsb

@@ -277,3 +277,24 @@ def test_bench_torch_eager_baseline_matches_oracle():
     b = bench.torch_eager_expert_layer(xb, ids, w, cfg, experts[3:], (q13[3:], s13[3:], q2[3:], s2[3:]), routes[3:])
     full = bench.torch_eager_expert_layer(xb, ids, w, cfg, experts, (q13, s13, q2, s2), routes)
     np.testing.assert_allclose((a + b).numpy(), full.numpy(), rtol=1e-5, atol=1e-5)
+
+
+def test_noalloc_rejects_calls_beyond_its_scratch():
+    """The fixed-scratch W8A8 entry point refuses a call whose workspace would
+    exceed the array, before touching the device (so this runs without a GPU)."""
+    import ctypes
+
+    from fused_cpp_amd import cabi
+
+    L = cabi.lib()
+    a = cabi.MoeArgs()
+    a.tokens, a.hidden, a.inter = 4096, 7168, 2048
+    a.top_k, a.experts, a.valid_experts, a.shared_expert_id = 8, 257, 257, 256
+    a.routed_scaling = 2.5
+    a.activation = cabi.FCMOE_ACT_SILU_CLAMP10
+    assert L.fcmoe_w8a8_workspace_bytes(ctypes.byref(a)) > cabi.FCMOE_NOALLOC_SCRATCH_BYTES
+    rc = L.fcmoe_w8a8_forward_noalloc(ctypes.byref(a), None)
+    assert rc == -2  # FCMOE_ESPACE
+    assert "scratch" in L.fcmoe_last_error().decode()
+    a.tokens = 64  # C2's decode batch fits the array
+    assert L.fcmoe_w8a8_workspace_bytes(ctypes.byref(a)) <= cabi.FCMOE_NOALLOC_SCRATCH_BYTES

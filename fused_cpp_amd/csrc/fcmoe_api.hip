@@ -244,6 +244,7 @@ int side_streams(SideStreams** out) {
 // classes, the largest class (last) stays on the caller's stream and is
 // launched first; the others are forked.
 bool timing_on();
+int persistent_wgs();
 
 template <typename F>
 int run_classes(const TileClasses& tc, hipStream_t stream, F&& gemm, bool serial = false) {
@@ -270,6 +271,21 @@ int run_classes(const TileClasses& tc, hipStream_t stream, F&& gemm, bool serial
   for (int c = tc.n - 2; c >= 0; --c)
     if (hipStreamWaitEvent(stream, ss->join[c], 0) != hipSuccess) return fail(FCMOE_EDEVICE, "stream wait failed");
   return FCMOE_OK;
+}
+
+// Workgroups of a persistent launch: the device's CU count, rounded down to
+// a multiple of the XCD count (the LDS kernel's item order keeps each item on
+// the XCD of the workgroup that runs it). Cached per device.
+int persistent_wgs() {
+  static int cache[kMaxDevices] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 256;
+  if (!cache[dev]) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 8) cus = 256;
+    cache[dev] = cus / 8 * 8;
+  }
+  return cache[dev];
 }
 
 bool timing_on() {
@@ -368,6 +384,117 @@ extern "C" size_t fcmoe_w8a8_workspace_bytes(const fcmoe_moe_args* a) {
 
 namespace {
 
+// ---- W8A8 prefill: two launch plans per GEMM stage, chosen on the device.
+//
+// Classic plan: one launch per tile class (16 / 128 / 192 / 256 rows), the
+// classes side by side on forked streams. Mixed plan: two persistent
+// launches that share every CU -- the 16-row class streams its experts'
+// weights from HBM on a 4-wave workgroup per CU while a persistent
+// 256-row-tile launch (2 x 4 waves, at most 216 VGPRs) runs every larger
+// expert's MFMA work; row fragments past an expert's rows skip their MFMAs,
+// so the 128/192-row experts cost their own rows. With many experts of at
+// most 16 rows beside MFMA-bound ones (skewed routing, C3: 149 such experts)
+// the HBM stream hides under the MFMA work (C3 3.12 -> 2.81 ms); with few of
+// them the classic plan is faster (uniform routing at T = 1024: 2.15 vs 2.30
+// ms, C4 4.30 vs 5.10 ms). The route scan's count of 16-row tiles picks the
+// plan: every launch of the other plan exits at once (no host round trip).
+constexpr int kPrefillMixedMinTiles = 32;
+
+// FCMOE_PREFILL_MIXED_MIN_TILES overrides the threshold (0: always the mixed
+// plan; a large value: never); read on every call so that tests can run both
+// plans on one input.
+int mixed_min_tiles() {
+  const char* v = getenv("FCMOE_PREFILL_MIXED_MIN_TILES");
+  return v && v[0] ? atoi(v) : kPrefillMixedMinTiles;
+}
+
+// One W8A8 GEMM stage (epilogue epi, stage-timing base id stage0) over the
+// prefill class set {16, 128, 192, 256}, or over any other class set with the
+// classic launches only.
+int run_w8a8_stage(const TileClasses& tc, const RouteBuffers& rb, int epi, const GemmParams& base, int stage0,
+                   bool serial, hipStream_t stream) {
+  const bool prefill = tc.n == 4 && tc.bm[0] == 16 && tc.bm[3] == 256;
+  GemmParams gate = base;
+  if (prefill) {
+    gate.plan_tiles = rb.tile_count;  // class 0: the 16-row tiles
+    gate.plan_min = mixed_min_tiles();
+    // Mixed plan. The persistent MFMA launch takes classes 256, 192, 128 (in
+    // that order) as one item space; the 16-row class streams beside it.
+    GemmParams pm = gate;
+    pm.plan_mixed = 1;
+    pm.persist = persistent_wgs();
+    pm.u_n = 3;
+    int64_t big_bound = 0;
+    for (int u = 0; u < 3; ++u) {
+      const int c = 3 - u;
+      pm.u_tiles[u] = rb.tiles + 2 * tile_offset(tc, c);
+      pm.u_count[u] = rb.tile_count + c;
+      big_bound += tc.bound[c];
+    }
+    GemmParams ps = gate;
+    ps.plan_mixed = 1;
+    ps.persist = persistent_wgs();
+    ps.stream_role = 1;
+    ps.tiles = rb.tiles;
+    ps.tile_count = rb.tile_count;
+    // Classic-plan launch of class c.
+    auto classic = [&](int c, hipStream_t s) {
+      GemmParams p = gate;
+      p.plan_mixed = 0;
+      p.tiles = rb.tiles + 2 * tile_offset(tc, c);
+      p.tile_count = rb.tile_count + c;
+      // The 16-row class loops over its items on one workgroup per CU: a
+      // class with few or no tiles then dispatches 256 workgroups, not the
+      // thousands its host-side bound allows (C4, whose 16-row class is
+      // empty: 4.67 -> 4.30 ms with the classes side by side).
+      if (c == 0) p.persist = persistent_wgs();
+      Stage st(stage0 + class_slot(tc.bm[c]), s);
+      return gemm_launch(epi, tc.bm[c], p, tc.bound[c], s);
+    };
+    int rc;
+    if (serial || timing_on()) {
+      {
+        Stage st(stage0 + class_slot(256), stream);
+        if ((rc = gemm_launch(epi, 256, pm, big_bound, stream))) return rc;
+      }
+      {
+        Stage st(stage0 + class_slot(16), stream);
+        if ((rc = gemm_launch(epi, 16, ps, tc.bound[0], stream))) return rc;
+      }
+      for (int c = 0; c < tc.n; ++c)
+        if ((rc = classic(c, stream))) return rc;
+      return FCMOE_OK;
+    }
+    // Every launch of both plans under one fork: the mixed plan's MFMA launch
+    // on the caller's stream (first, so its workgroups hold every CU before
+    // the streaming ones arrive), its 16-row launch and the classic classes
+    // (largest first) on side streams; the plan not taken exits at once,
+    // beside the one that runs.
+    SideStreams* ss = nullptr;
+    if ((rc = side_streams(&ss))) return rc;
+    if (hipEventRecord(ss->fork, stream) != hipSuccess) return fail(FCMOE_EDEVICE, "hipEventRecord failed");
+    if ((rc = gemm_launch(epi, 256, pm, big_bound, stream))) return rc;
+    for (int k = 0; k <= tc.n; ++k) {
+      hipStream_t s = ss->s[k];
+      if (hipStreamWaitEvent(s, ss->fork, 0) != hipSuccess) return fail(FCMOE_EDEVICE, "stream wait failed");
+      rc = k == 0 ? gemm_launch(epi, 16, ps, tc.bound[0], s) : classic(tc.n - k, s);
+      if (rc) return rc;
+      if (hipEventRecord(ss->join[k], s) != hipSuccess) return fail(FCMOE_EDEVICE, "hipEventRecord failed");
+    }
+    for (int k = 0; k <= tc.n; ++k)
+      if (hipStreamWaitEvent(stream, ss->join[k], 0) != hipSuccess) return fail(FCMOE_EDEVICE, "stream wait failed");
+    return FCMOE_OK;
+  }
+  // Outside the prefill class set: the classic launches only.
+  return run_classes(tc, stream, [&](int c, hipStream_t s) {
+    GemmParams p = base;
+    p.tiles = rb.tiles + 2 * tile_offset(tc, c);
+    p.tile_count = rb.tile_count + c;
+    Stage st(stage0 + class_slot(tc.bm[c]), s);
+    return gemm_launch(epi, tc.bm[c], p, tc.bound[c], s);
+  }, serial);
+}
+
 // The W8A8 forward over a given workspace. serial_classes runs the class
 // launches of a GEMM stage on `stream` one after another (no side streams).
 int w8a8_run(const fcmoe_moe_args* a, char* ws_base, size_t ws_bytes, bool serial_classes, hipStream_t stream) {
@@ -423,13 +550,7 @@ int w8a8_run(const fcmoe_moe_args* a, char* ws_base, size_t ws_bytes, bool seria
   g13.scale_row = L.xs;
   g13.scale_col = a->w13_scale;
   g13.rowpart = L.rowpart;
-  rc = run_classes(L.tc, stream, [&](int c, hipStream_t s) {
-    GemmParams p = g13;
-    p.tiles = L.rb.tiles + 2 * tile_offset(L.tc, c);
-    p.tile_count = L.rb.tile_count + c;
-    Stage st(FCMOE_STAGE_W13_CLASS0 + class_slot(L.tc.bm[c]), s);
-    return gemm_launch(kEpiW13SwigluI8, L.tc.bm[c], p, L.tc.bound[c], s);
-  }, serial_classes);
+  rc = run_w8a8_stage(L.tc, L.rb, kEpiW13SwigluI8, g13, FCMOE_STAGE_W13_CLASS0, serial_classes, stream);
   if (rc) return rc;
   {
     Stage st(FCMOE_STAGE_REQUANT, stream);
@@ -456,13 +577,7 @@ int w8a8_run(const fcmoe_moe_args* a, char* ws_base, size_t ws_bytes, bool seria
   g2.scale_row = L.s2row;
   g2.scale_col = a->w2_scale;
   g2.sorted_routes = L.rb.sorted_routes;
-  rc = run_classes(L.tc, stream, [&](int c, hipStream_t s) {
-    GemmParams p = g2;
-    p.tiles = L.rb.tiles + 2 * tile_offset(L.tc, c);
-    p.tile_count = L.rb.tile_count + c;
-    Stage st(FCMOE_STAGE_W2_CLASS0 + class_slot(L.tc.bm[c]), s);
-    return gemm_launch(kEpiW2RouteI8, L.tc.bm[c], p, L.tc.bound[c], s);
-  }, serial_classes);
+  rc = run_w8a8_stage(L.tc, L.rb, kEpiW2RouteI8, g2, FCMOE_STAGE_W2_CLASS0, serial_classes, stream);
   if (rc) return rc;
   Stage st(FCMOE_STAGE_COMBINE, stream);
   return combine_launch(L.route_out, L.rb.route_weight, L.rb.route_pos, a->tokens, L.kt, H, 0, 0, a->out, stream);

@@ -33,7 +33,7 @@ namespace {
 
 
 template <bool I8, int EPI, int WM, int WN, int FM, int FN, int NB, bool ADIRECT>
-__global__ __launch_bounds__(WM * WN * kWave) void grouped_gemm_kernel(GemmParams p, int n_blocks) {
+__device__ __forceinline__ void grouped_gemm_body(const GemmParams& p, int n_blocks) {
   constexpr int kThreads = WM * WN * kWave;
   constexpr int BM = WM * FM * 16;
   constexpr int ROWB = 64 + 16;                    // LDS row stride (bytes): 16 rows hit distinct banks
@@ -52,10 +52,16 @@ __global__ __launch_bounds__(WM * WN * kWave) void grouped_gemm_kernel(GemmParam
 
   // Tiles run last-first: the route kernel lists experts in id order and the
   // appended shared expert (the largest) is last, so it starts first.
+  if (!plan_open(p)) return;
   const int count = *p.tile_count;
-  const int tile = count - 1 - (int)(blockIdx.x / n_blocks);
-  if (tile < 0) return;
-  const int nb = blockIdx.x % n_blocks;
+  const int total_items = count * n_blocks;
+  // Persistent launches (p.persist > 0, direct-A tiles only) run a fixed
+  // grid whose workgroups stride over the items; otherwise each workgroup
+  // runs item blockIdx.x once.
+  const int item_step = (ADIRECT && p.persist > 0) ? (int)gridDim.x : total_items;
+  for (int item = (int)blockIdx.x; item < total_items; item += item_step) {
+  const int tile = count - 1 - item / n_blocks;
+  const int nb = item % n_blocks;
   const int expert = p.tiles[2 * tile];
   const int m0 = p.tiles[2 * tile + 1];
   const int rows_left = p.counts[expert] - m0;
@@ -280,21 +286,46 @@ __global__ __launch_bounds__(WM * WN * kWave) void grouped_gemm_kernel(GemmParam
   }(std::make_integer_sequence<int, U - 1>{});
 
   gemm_epilogue<I8, EPI, FM, FN>(p, acc, gtile, tvalid, wm * FM * 16, rows, pos0, expert, lane);
+  }
 }
 
 template <bool I8, int EPI, int WM, int WN, int FM, int FN, int NB, bool ADIRECT>
+__global__ __launch_bounds__(WM * WN * kWave) void grouped_gemm_kernel(GemmParams p, int n_blocks) {
+  grouped_gemm_body<I8, EPI, WM, WN, FM, FN, NB, ADIRECT>(p, n_blocks);
+}
+
+// Persistent streaming form (16-row tiles beside the persistent LDS-kernel
+// launch): at most 80 VGPRs (6 waves per SIMD), so one of its waves fits on
+// each SIMD next to two waves of that kernel.
+template <bool I8, int EPI, int WM, int WN, int FM, int FN, int NB, bool ADIRECT>
+__global__ __launch_bounds__(WM * WN * kWave) __attribute__((amdgpu_waves_per_eu(6))) void
+grouped_gemm_stream_kernel(GemmParams p, int n_blocks) {
+  grouped_gemm_body<I8, EPI, WM, WN, FM, FN, NB, ADIRECT>(p, n_blocks);
+}
+
+template <bool I8, int EPI, int WM, int WN, int FM, int FN, int NB, bool ADIRECT, bool STREAM = false>
 int launch_cfg(const GemmParams& p, int64_t max_tiles, hipStream_t stream) {
   constexpr bool PAIR = epi_pair(EPI);
   const int64_t per_block = PAIR ? FN / 2 * WN : FN * WN;
   const int64_t units = PAIR ? p.n_tiles : (int64_t)p.n_groups * p.n_tiles;
   const int64_t n_blocks = ceil_div(units, per_block);
-  const int64_t grid = max_tiles * n_blocks;
+  int64_t grid = max_tiles * n_blocks;
   if (grid <= 0) return FCMOE_OK;
+  if (ADIRECT && p.persist > 0 && grid > p.persist) grid = p.persist;
   if (grid > INT32_MAX) return fail(FCMOE_EINVAL, "grouped gemm grid too large");
-  hipLaunchKernelGGL((grouped_gemm_kernel<I8, EPI, WM, WN, FM, FN, NB, ADIRECT>), dim3((unsigned)grid), dim3(WM * WN * kWave), 0,
-                     stream, p, (int)n_blocks);
+  if constexpr (STREAM) {
+    hipLaunchKernelGGL((grouped_gemm_stream_kernel<I8, EPI, WM, WN, FM, FN, NB, ADIRECT>), dim3((unsigned)grid),
+                       dim3(WM * WN * kWave), 0, stream, p, (int)n_blocks);
+  } else {
+    hipLaunchKernelGGL((grouped_gemm_kernel<I8, EPI, WM, WN, FM, FN, NB, ADIRECT>), dim3((unsigned)grid),
+                       dim3(WM * WN * kWave), 0, stream, p, (int)n_blocks);
+  }
   return check_launch("grouped_gemm");
 }
+
+// Tile bound (the host's upper limit on a launch's tiles) up to which the
+// 16-row class runs one-wave workgroups.
+constexpr int64_t kDecodeFewTiles = 80;
 
 template <bool I8, int EPI>
 int launch_bm(int bm, const GemmParams& p, int64_t max_tiles, hipStream_t stream) {
@@ -304,6 +335,24 @@ int launch_bm(int bm, const GemmParams& p, int64_t max_tiles, hipStream_t stream
       // and one up tile per wave; W2 (short K) streams one tile per wave.
       // Measured on the DSv3 C2 layer against 4 waves (W13 2+2 tiles with a
       // 4-deep ring, W2 2 tiles): W2 0.527 -> 0.506 ms, W13 0.964 -> 0.961 ms.
+      // Small decode batches (a few dozen tiles at most): one wave per
+      // workgroup. A CU streams at most ~40 GB/s, so the bytes must spread
+      // evenly over all 256 CUs; 8-wave workgroups leave CUs idle at T=1
+      // (144 workgroups) or doubled up at T=2 (272 workgroups, W13
+      // 0.108 -> 0.083 ms with one-wave workgroups; T=8 0.243 -> 0.233 ms).
+      // At C2 (T=64) the 8-wave form is faster (0.929 vs 0.944 ms).
+      if (p.stream_role) {
+        if constexpr (epi_pair(EPI))
+          return launch_cfg<I8, EPI, 1, 4, 1, 2, 2, true, true>(p, max_tiles, stream);
+        else
+          return launch_cfg<I8, EPI, 1, 4, 1, 1, 4, true, true>(p, max_tiles, stream);
+      }
+      if (max_tiles <= kDecodeFewTiles) {
+        if constexpr (epi_pair(EPI))
+          return launch_cfg<I8, EPI, 1, 1, 1, 2, 8, true>(p, max_tiles, stream);
+        else
+          return launch_cfg<I8, EPI, 1, 1, 1, 1, 8, true>(p, max_tiles, stream);
+      }
       if constexpr (epi_pair(EPI))
         return launch_cfg<I8, EPI, 1, 8, 1, 2, 8, true>(p, max_tiles, stream);
       else

@@ -268,8 +268,8 @@ __device__ __forceinline__ void staged_epilogue(const GemmParams& p, const v4i (
   (void)expert;
 }
 
-template <bool I8, int EPI, int FM, int FN, int SA, int SB, int BPOL, int AW, int WMW, int WNW>
-__global__ __launch_bounds__(WMW * WNW * kWave) void grouped_gemm_lds_kernel(GemmParams p, int n_blocks, int partial, int gm) {
+template <bool I8, int EPI, int FM, int FN, int SA, int SB, int BPOL, int AW, int WMW, int WNW, bool PERSIST>
+__device__ __forceinline__ void lds_gemm_body(const GemmParams& p, int n_blocks, int partial, int gm, int grid_items) {
   // The body is device-only: the buffer-resource type does not exist for the
   // host target, and the host pass needs only the kernel's signature.
 #if __HIP_DEVICE_COMPILE__
@@ -329,12 +329,39 @@ __global__ __launch_bounds__(WMW * WNW * kWave) void grouped_gemm_lds_kernel(Gem
   float* const meta_cs = (float*)(smem + META + 8 * BM);
   uint8_t* const smem_b = smem + SA * A_BYTES;
 
-  const int count = *p.tile_count;
+  if (!plan_open(p)) return;
+  // Item space: one class's tile list, or (u_n > 0) several lists back to back.
+  int ucount[3] = {0, 0, 0};
+  int count;
+  if constexpr (PERSIST) {
+    count = 0;
+    for (int u = 0; u < p.u_n; ++u) {
+      ucount[u] = *p.u_count[u];
+      count += ucount[u];
+    }
+    if (p.u_n == 0) count = *p.tile_count;
+  } else {
+    count = *p.tile_count;
+  }
+  // Persistent launches (p.persist > 0): gridDim.x workgroups (a multiple of
+  // the XCD count, so an item keeps its XCD) stride over the `grid_items`
+  // item slots; otherwise each workgroup runs slot blockIdx.x.
+  const int slot_step = PERSIST ? (int)gridDim.x : grid_items;
+  for (int it = 0, slot = (int)blockIdx.x; PERSIST ? slot < grid_items : it < 1; ++it, slot += slot_step) {
   int tile_idx, nb;
-  if (!lds_work_item((int)blockIdx.x, count, n_blocks, partial != 0, gm, tile_idx, nb)) return;
-  const int tile = count - 1 - tile_idx;  // last-first, as the register kernel
-  const int expert = p.tiles[2 * tile];
-  const int m0 = p.tiles[2 * tile + 1];
+  if (!lds_work_item(slot, count, n_blocks, partial != 0, gm, tile_idx, nb)) continue;
+  if (PERSIST && slot != (int)blockIdx.x) __syncthreads();  // the previous item's epilogue is done with the stages
+  // last-first within a list, as the register kernel
+  const int32_t* tpair = p.tiles + 2 * (count - 1 - tile_idx);
+  if constexpr (PERSIST) {
+    if (p.u_n > 0) {
+      int t = tile_idx, u = 0;
+      while (u + 1 < p.u_n && t >= ucount[u]) t -= ucount[u++];
+      tpair = p.u_tiles[u] + 2 * (ucount[u] - 1 - t);
+    }
+  }
+  const int expert = tpair[0];
+  const int m0 = tpair[1];
   const int rows_left = p.counts[expert] - m0;
   const int rows = rows_left < BM ? rows_left : BM;
   const int pos0 = p.offsets[expert] + m0;
@@ -435,6 +462,11 @@ __global__ __launch_bounds__(WMW * WNW * kWave) void grouped_gemm_lds_kernel(Gem
     (void)tile_of(wn, j, &v);
     wave_live = wave_live || v;
   }
+  // Persistent launches also take experts of fewer rows than the tile: a
+  // wave whose row fragments all lie past the expert's rows skips its MFMAs.
+  if constexpr (PERSIST) wave_live = wave_live && wm * FM * 16 < rows;
+  // row fragments of this wave that hold rows of the expert (the rest are clamped re-reads of its last row)
+  const int live_frags = __builtin_amdgcn_readfirstlane((rows - wm * FM * 16 + 15) / 16);
 
   // ---- fragment addresses (bytes within a stage)
   constexpr int A_FRAG = 16 * AW;  // bytes per 16-row fragment in a stage
@@ -527,6 +559,8 @@ __global__ __launch_bounds__(WMW * WNW * kWave) void grouped_gemm_lds_kernel(Gem
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
       if (i + 2 < FM) af[(i + 2) % 3] = *(const v4i*)(sta + (i + 2) * A_FRAG);
+      // persistent launches: row fragments past the expert's rows skip their MFMAs
+      if (PERSIST && i >= live_frags) continue;
 #pragma unroll
       for (int j = 0; j < FN; ++j) {
         if constexpr (I8) {
@@ -630,7 +664,21 @@ __global__ __launch_bounds__(WMW * WNW * kWave) void grouped_gemm_lds_kernel(Gem
   } else {
     gemm_epilogue<I8, EPI, FM, FN, true>(p, acc, gtile, tvalid, wm * FM * 16, rows, pos0, expert, lane, meta);
   }
+  }
 #endif
+}
+
+template <bool I8, int EPI, int FM, int FN, int SA, int SB, int BPOL, int AW, int WMW, int WNW>
+__global__ __launch_bounds__(WMW * WNW * kWave) void grouped_gemm_lds_kernel(GemmParams p, int n_blocks, int partial,
+                                                                            int gm, int grid_items) {
+  lds_gemm_body<I8, EPI, FM, FN, SA, SB, BPOL, AW, WMW, WNW, false>(p, n_blocks, partial, gm, grid_items);
+}
+
+// Persistent form: gridDim.x workgroups loop over the items.
+template <bool I8, int EPI, int FM, int FN, int SA, int SB, int BPOL, int AW, int WMW, int WNW>
+__global__ __launch_bounds__(WMW * WNW * kWave) void
+grouped_gemm_lds_persist_kernel(GemmParams p, int n_blocks, int partial, int gm, int grid_items) {
+  lds_gemm_body<I8, EPI, FM, FN, SA, SB, BPOL, AW, WMW, WNW, true>(p, n_blocks, partial, gm, grid_items);
 }
 
 // Channel blocks per row tile of a workgroup whose waves hold FN 16-channel
@@ -643,23 +691,30 @@ int64_t lds_blocks(int wn, int fn, const GemmParams& p) {
   return ceil_div(units, per_block);
 }
 
-template <bool I8, int EPI, int FM, int FN, int SA, int SB, int BPOL, int AW, int WMW = kWM, int WNW = kWN>
+template <bool I8, int EPI, int FM, int FN, int SA, int SB, int BPOL, int AW, int WMW = kWM, int WNW = kWN,
+          bool PERSIST = false>
 int launch_lds_cfg(const GemmParams& p, int64_t max_tiles, hipStream_t stream) {
   const int64_t n_blocks = lds_blocks<EPI>(WNW, FN, p);
   if (max_tiles * n_blocks <= 0) return FCMOE_OK;
   constexpr bool PAIR = epi_pair(EPI);
   const int64_t units = PAIR ? p.n_tiles : (int64_t)p.n_groups * p.n_tiles;
   const int partial = n_blocks * (PAIR ? WNW * (FN / 2) : WNW * FN) > units ? 1 : 0;
-  const int64_t grid = max_tiles * n_blocks + (partial ? kXcds : 0);
-  if (grid > INT32_MAX) return fail(FCMOE_EINVAL, "grouped gemm grid too large");
+  const int64_t items = max_tiles * n_blocks + (partial ? kXcds : 0);
+  if (items > INT32_MAX) return fail(FCMOE_EINVAL, "grouped gemm grid too large");
+  const int64_t grid = PERSIST && items > p.persist ? p.persist : items;
   // 32-bit buffer offsets: A rows and one expert's packed weights
   if (p.w_expert_bytes >= 0x7ffffff0) return fail(FCMOE_EINVAL, "expert weights exceed 2 GiB");
   static const int gm = [] {
     const char* v = getenv("FCMOE_LDS_GROUP");
     return v ? atoi(v) : kLdsGroupTiles;
   }();
-  hipLaunchKernelGGL((grouped_gemm_lds_kernel<I8, EPI, FM, FN, SA, SB, BPOL, AW, WMW, WNW>), dim3((unsigned)grid),
-                     dim3(WMW * WNW * kWave), 0, stream, p, (int)n_blocks, partial, gm);
+  if constexpr (PERSIST)
+    hipLaunchKernelGGL((grouped_gemm_lds_persist_kernel<I8, EPI, FM, FN, SA, SB, BPOL, AW, WMW, WNW>),
+                       dim3((unsigned)grid), dim3(WMW * WNW * kWave), 0, stream, p, (int)n_blocks, partial, gm,
+                       (int)items);
+  else
+    hipLaunchKernelGGL((grouped_gemm_lds_kernel<I8, EPI, FM, FN, SA, SB, BPOL, AW, WMW, WNW>), dim3((unsigned)grid),
+                       dim3(WMW * WNW * kWave), 0, stream, p, (int)n_blocks, partial, gm, (int)items);
   return check_launch("grouped_gemm_lds");
 }
 
@@ -687,6 +742,10 @@ int launch_lds_bm(int bm, const GemmParams& p, int64_t max_tiles, hipStream_t st
       else
         return launch_lds_cfg<I8, EPI, 6, 8, 3, 3, kNT, 64>(p, max_tiles, stream);
     case 256:
+      // The mixed plan's persistent launch: 2 x 4 waves of 128 x 64 (at most
+      // 216 VGPRs, 115 KB of LDS), so that the 16-row streaming launch's
+      // waves (64 VGPRs) fit on every SIMD beside two of its waves.
+      if (p.persist > 0) return launch_lds_cfg<I8, EPI, 8, 4, 2, 3, 0, 128, 2, 4, true>(p, max_tiles, stream);
       // W13 (gate/up pairs) on 4-wave workgroups, two per CU (2 x 2 waves of
       // 128 x 96, 72 KB of LDS): another workgroup's K loop overlaps each
       // item's epilogue (C3 W13 0.938 -> 0.927 ms, C4 0.455 -> 0.417 ms). W2

@@ -133,7 +133,30 @@ struct GemmParams {
   const int32_t* sorted_routes;  // W2: sorted position -> flat route
   int activation;            // bf16 W13
   int out_bf16;              // i8gemm output dtype
+  // Persistent launch: > 0 = this many workgroups (a multiple of the XCD
+  // count) loop over the items; 0 = one workgroup per item slot.
+  int persist;
+  // Streaming role of the 16-row class beside a persistent LDS-kernel launch
+  // (4 waves per workgroup, few enough VGPRs to share each SIMD with it).
+  int stream_role;
+  // Launch-plan gate (W8A8 prefill; see the forward): when plan_tiles is set
+  // the launch does its work only if (*plan_tiles >= plan_min) == plan_mixed,
+  // and otherwise every workgroup exits at once.
+  const int32_t* plan_tiles;
+  int plan_min;
+  int plan_mixed;
+  // Several classes' tile lists as one item space (the persistent LDS launch
+  // of the mixed plan): u_n > 0 replaces tiles / tile_count by lists
+  // u_tiles[0..u_n) (largest tile class first), each run last-first.
+  int u_n;
+  const int32_t* u_tiles[3];
+  const int32_t* u_count[3];
 };
+
+// Whether a launch's plan gate lets it run (device side).
+__device__ __forceinline__ bool plan_open(const GemmParams& p) {
+  return !p.plan_tiles || ((*p.plan_tiles >= p.plan_min) == (p.plan_mixed != 0));
+}
 
 int gemm_launch(int epi, int bm, const GemmParams& p, int64_t max_tiles, hipStream_t stream);
 // LDS-staged kernel for bm in {128, 192, 256} (fcmoe_gemm_lds.hip); gemm_launch

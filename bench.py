@@ -219,6 +219,19 @@ def algorithmic(cfg, counts):
             experts=n_exp, rows=r)
         stages[f"w2_bm{CLASS_BM[c]}"] = dict(
             bytes=n_exp * (H * I * eb + H * sb) + r * I * eb + r * H * 4, ops=r * 2 * H * I, experts=n_exp, rows=r)
+    if cfg["kind"] == "w8a8" and not decode:
+        # The mixed prefill plan's two launches: the persistent MFMA launch
+        # (every expert above 16 rows) and the 16-row streaming launch.
+        for name, sel in (("mixed_mfma", counts > 16), ("mixed_stream", (counts > 0) & (counts <= 16))):
+            n_exp, r = int(sel.sum()), int(counts[sel].sum())
+            if n_exp == 0:
+                continue
+            stages[f"w13_{name}"] = dict(
+                bytes=n_exp * (2 * I * H * eb + 2 * I * sb) + r * H * eb + r * I * 2, ops=r * 2 * (2 * I) * H,
+                experts=n_exp, rows=r)
+            stages[f"w2_{name}"] = dict(
+                bytes=n_exp * (H * I * eb + H * sb) + r * I * eb + r * H * 4, ops=r * 2 * H * I, experts=n_exp,
+                rows=r)
     return layer_bytes, layer_ops, stages
 
 

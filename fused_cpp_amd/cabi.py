@@ -88,7 +88,8 @@ FCMOE_STAGE_COUNT = 24
 FCMOE_NOALLOC_SCRATCH_BYTES = 64 << 20
 STAGE_NAMES = {0: "route", 1: "quant", 2: "requant", 3: "act", 4: "combine",
                **{8 + c: f"w13_bm{bm}" for c, bm in enumerate((16, 32, 64, 128, 192, 256))},
-               **{16 + c: f"w2_bm{bm}" for c, bm in enumerate((16, 32, 64, 128, 192, 256))}}
+               **{16 + c: f"w2_bm{bm}" for c, bm in enumerate((16, 32, 64, 128, 192, 256))},
+               14: "w13_mixed_mfma", 15: "w13_mixed_stream", 22: "w2_mixed_mfma", 23: "w2_mixed_stream"}
 
 
 def stage_timing_enable(on: bool = True) -> None:

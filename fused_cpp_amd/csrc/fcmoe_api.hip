@@ -412,7 +412,7 @@ int mixed_min_tiles() {
 // prefill class set {16, 128, 192, 256}, or over any other class set with the
 // classic launches only.
 int run_w8a8_stage(const TileClasses& tc, const RouteBuffers& rb, int epi, const GemmParams& base, int stage0,
-                   bool serial, hipStream_t stream) {
+                   int stage_mixed, bool serial, hipStream_t stream) {
   const bool prefill = tc.n == 4 && tc.bm[0] == 16 && tc.bm[3] == 256;
   GemmParams gate = base;
   if (prefill) {
@@ -454,11 +454,11 @@ int run_w8a8_stage(const TileClasses& tc, const RouteBuffers& rb, int epi, const
     int rc;
     if (serial || timing_on()) {
       {
-        Stage st(stage0 + class_slot(256), stream);
+        Stage st(stage_mixed, stream);
         if ((rc = gemm_launch(epi, 256, pm, big_bound, stream))) return rc;
       }
       {
-        Stage st(stage0 + class_slot(16), stream);
+        Stage st(stage_mixed + 1, stream);
         if ((rc = gemm_launch(epi, 16, ps, tc.bound[0], stream))) return rc;
       }
       for (int c = 0; c < tc.n; ++c)
@@ -474,14 +474,15 @@ int run_w8a8_stage(const TileClasses& tc, const RouteBuffers& rb, int epi, const
     if ((rc = side_streams(&ss))) return rc;
     if (hipEventRecord(ss->fork, stream) != hipSuccess) return fail(FCMOE_EDEVICE, "hipEventRecord failed");
     if ((rc = gemm_launch(epi, 256, pm, big_bound, stream))) return rc;
-    for (int k = 0; k <= tc.n; ++k) {
+    const int nk = gate.plan_min <= 0 ? 0 : tc.n;  // forced mixed plan: no classic launches
+    for (int k = 0; k <= nk; ++k) {
       hipStream_t s = ss->s[k];
       if (hipStreamWaitEvent(s, ss->fork, 0) != hipSuccess) return fail(FCMOE_EDEVICE, "stream wait failed");
       rc = k == 0 ? gemm_launch(epi, 16, ps, tc.bound[0], s) : classic(tc.n - k, s);
       if (rc) return rc;
       if (hipEventRecord(ss->join[k], s) != hipSuccess) return fail(FCMOE_EDEVICE, "hipEventRecord failed");
     }
-    for (int k = 0; k <= tc.n; ++k)
+    for (int k = 0; k <= nk; ++k)
       if (hipStreamWaitEvent(stream, ss->join[k], 0) != hipSuccess) return fail(FCMOE_EDEVICE, "stream wait failed");
     return FCMOE_OK;
   }
@@ -550,7 +551,8 @@ int w8a8_run(const fcmoe_moe_args* a, char* ws_base, size_t ws_bytes, bool seria
   g13.scale_row = L.xs;
   g13.scale_col = a->w13_scale;
   g13.rowpart = L.rowpart;
-  rc = run_w8a8_stage(L.tc, L.rb, kEpiW13SwigluI8, g13, FCMOE_STAGE_W13_CLASS0, serial_classes, stream);
+  rc = run_w8a8_stage(L.tc, L.rb, kEpiW13SwigluI8, g13, FCMOE_STAGE_W13_CLASS0, FCMOE_STAGE_W13_MIXED_MFMA,
+                      serial_classes, stream);
   if (rc) return rc;
   {
     Stage st(FCMOE_STAGE_REQUANT, stream);
@@ -577,7 +579,8 @@ int w8a8_run(const fcmoe_moe_args* a, char* ws_base, size_t ws_bytes, bool seria
   g2.scale_row = L.s2row;
   g2.scale_col = a->w2_scale;
   g2.sorted_routes = L.rb.sorted_routes;
-  rc = run_w8a8_stage(L.tc, L.rb, kEpiW2RouteI8, g2, FCMOE_STAGE_W2_CLASS0, serial_classes, stream);
+  rc = run_w8a8_stage(L.tc, L.rb, kEpiW2RouteI8, g2, FCMOE_STAGE_W2_CLASS0, FCMOE_STAGE_W2_MIXED_MFMA,
+                      serial_classes, stream);
   if (rc) return rc;
   Stage st(FCMOE_STAGE_COMBINE, stream);
   return combine_launch(L.route_out, L.rb.route_weight, L.rb.route_pos, a->tokens, L.kt, H, 0, 0, a->out, stream);

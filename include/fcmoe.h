@@ -229,14 +229,22 @@ int fcmoe_bf16_stage_views(const fcmoe_moe_args* args, int w8a16, const int32_t*
 /* ---- stage timing ------------------------------------------------------ */
 
 /* Stage ids for fcmoe_stage_timing_read. W13 / W2 class stages are per tile
- * class c (BM = 16, 32, 64, 128, 192, 256 for c = 0..5). */
+ * class c (BM = 16, 32, 64, 128, 192, 256 for c = 0..5). W8A8 prefill
+ * records the launches of both launch plans (the classic per-class launches
+ * and the mixed plan's persistent MFMA and 16-row streaming launches); the
+ * plan not chosen on the device exits at once and records a few
+ * microseconds. */
 #define FCMOE_STAGE_ROUTE 0
 #define FCMOE_STAGE_QUANT 1
 #define FCMOE_STAGE_REQUANT 2
 #define FCMOE_STAGE_ACT 3
 #define FCMOE_STAGE_COMBINE 4
 #define FCMOE_STAGE_W13_CLASS0 8
+#define FCMOE_STAGE_W13_MIXED_MFMA 14
+#define FCMOE_STAGE_W13_MIXED_STREAM 15
 #define FCMOE_STAGE_W2_CLASS0 16
+#define FCMOE_STAGE_W2_MIXED_MFMA 22
+#define FCMOE_STAGE_W2_MIXED_STREAM 23
 #define FCMOE_STAGE_COUNT 24
 
 /* Per-stage GPU timing with hipEvents recorded on the launch stream around

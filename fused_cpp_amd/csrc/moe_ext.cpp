@@ -10,6 +10,7 @@
 #include <c10/hip/HIPStream.h>
 #include <torch/extension.h>
 
+#include <algorithm>
 #include <string>
 #include <tuple>
 
@@ -53,6 +54,55 @@ at::Tensor pack(const at::Tensor& w, int n_groups) {
   return dst;
 }
 
+// Packs source experts `w` ([e, n, k] int8 or bf16, host or device) into rows
+// [first, first + e) of `dst` ([E, per] int8 on the device). Host experts are
+// staged through the device a chunk at a time (at most 256 MB and 1/16 of
+// the source, at least one expert), so the device never holds a full second
+// copy of them.
+void pack_into(at::Tensor& dst, int64_t first, const at::Tensor& w, int n_groups) {
+  const int eb = w.scalar_type() == at::kChar ? 1 : 2;
+  const int64_t e = w.size(0), n = w.size(1), k = w.size(2);
+  const int64_t per = dst.size(1);
+  TORCH_CHECK(per == fcmoe_packed_expert_bytes(eb, n, k, n_groups), "packed expert size mismatch");
+  const int64_t expert_bytes = n * k * eb;
+  const int64_t stage_bytes = std::min<int64_t>(int64_t(256) << 20, e * expert_bytes / 16);
+  const int64_t chunk = w.is_cuda() ? e : std::max<int64_t>(1, stage_bytes / std::max<int64_t>(expert_bytes, 1));
+  for (int64_t i = 0; i < e; i += chunk) {
+    const int64_t m = std::min(chunk, e - i);
+    at::Tensor src = w.slice(0, i, i + m);
+    src = src.is_cuda() ? src.contiguous() : src.to(dst.device()).contiguous();
+    check_rc(fcmoe_pack_experts(src.data_ptr(), eb, m, n, k, n_groups, (int8_t*)dst.data_ptr() + (first + i) * per,
+                                current_stream()),
+             "pack");
+  }
+}
+
+// Routed experts [E, n, k] plus one shared expert [n, k] packed as experts
+// 0..E-1 and E of one buffer, without concatenating the sources first: the
+// routed+shared prepare of src/fused_cpp/moe/bf16_tiled.py:541-570 (native
+// fused_moe_bf16_tiled.cpp:6276-6288), which packs "without a full source copy".
+at::Tensor pack_routed_shared(const at::Tensor& routed, const at::Tensor& shared, int n_groups,
+                              const at::Device& dev) {
+  TORCH_CHECK(routed.dim() == 3 && routed.size(0) > 0, "routed weights must be [E, N, K] with E > 0");
+  at::Tensor sh = shared.dim() == 3 ? shared.squeeze(0) : shared;
+  TORCH_CHECK(sh.dim() == 2 && sh.size(0) == routed.size(1) && sh.size(1) == routed.size(2),
+              "the shared expert must match one routed expert's shape");
+  TORCH_CHECK(sh.scalar_type() == routed.scalar_type(), "routed and shared weights must share a dtype");
+  const int eb = routed.scalar_type() == at::kChar ? 1 : 2;
+  const int64_t e = routed.size(0);
+  const int64_t per = fcmoe_packed_expert_bytes(eb, routed.size(1), routed.size(2), n_groups);
+  TORCH_CHECK(per > 0, "invalid weight shape for packing");
+  at::Tensor dst = at::empty({e + 1, per}, at::TensorOptions().dtype(at::kChar).device(dev));
+  pack_into(dst, 0, routed, n_groups);
+  pack_into(dst, e, sh.unsqueeze(0), n_groups);
+  return dst;
+}
+
+at::Device target_device(const at::Tensor& t) {
+  if (t.is_cuda()) return t.device();
+  return at::Device(at::kCUDA, c10::hip::current_device());
+}
+
 using W8A8Tuple =
     std::tuple<at::Tensor, int64_t, int64_t, at::Tensor, at::Tensor, int64_t, int64_t, at::Tensor, int64_t, int64_t>;
 
@@ -82,6 +132,39 @@ W8A8Tuple pack_int8_experts(at::Tensor w13, at::Tensor s13, at::Tensor w2, at::T
   at::Tensor p2 = pack(w2.contiguous(), 1);
   return {p13, h, 2 * f, s13.to(w13.device()).reshape({e, 2 * f}).contiguous(), p2, f, h,
           s2.to(w13.device()).reshape({e, h}).contiguous(), kBackendId, 16};
+}
+
+// Routed + shared checkpoint int8 experts (W8A8: bf16_tiled.py:573-609;
+// W8A16: bf16_tiled.py:541-570): the shared expert is packed as expert E
+// straight into the routed experts' buffer; only the fp32 scales (one value
+// per channel) are concatenated.
+W8A8Tuple int8_prepare_routed_shared(at::Tensor rw13, at::Tensor rs13, at::Tensor rw2, at::Tensor rs2,
+                                     at::Tensor sw13, at::Tensor ss13, at::Tensor sw2, at::Tensor ss2, bool w8a16) {
+  const char* what = w8a16 ? "W8A16" : "W8A8";
+  TORCH_CHECK(rw13.scalar_type() == at::kChar && rw2.scalar_type() == at::kChar, what,
+              " weights must have dtype torch.int8");
+  TORCH_CHECK(rw13.dim() == 3 && rw2.dim() == 3, what, " weights must be [E, 2F, H] and [E, H, F]");
+  TORCH_CHECK(rw13.size(0) > 0 && rw13.size(0) == rw2.size(0), what, " expert counts must match and be positive");
+  TORCH_CHECK(rw13.size(1) % 2 == 0, what, " W13 output dimension must be even");
+  const int64_t e = rw13.size(0), f = rw13.size(1) / 2, h = rw13.size(2);
+  TORCH_CHECK(rw2.size(1) == h && rw2.size(2) == f, what, " W2 shape mismatch");
+  if (w8a16) {
+    TORCH_CHECK(f % 8 == 0, "W8A16 fused W13 requires F % 8 == 0, got ", f);
+  } else {
+    TORCH_CHECK(h % 16 == 0 && f % 16 == 0, what, " requires H and F to be multiples of 16");
+  }
+  TORCH_CHECK(rs13.numel() == e * 2 * f && ss13.numel() == 2 * f, what,
+              " W13 scales must contain one value per output channel");
+  TORCH_CHECK(rs2.numel() == e * h && ss2.numel() == h, what, " W2 scales must contain one value per output channel");
+  const at::Device dev = target_device(rw13);
+  at::Tensor p13 = pack_routed_shared(rw13, sw13, 2, dev);
+  at::Tensor p2 = pack_routed_shared(rw2, sw2, 1, dev);
+  auto f32 = [&](const at::Tensor& t, int64_t rows, int64_t cols) {
+    return t.to(dev, at::kFloat).reshape({rows, cols});
+  };
+  at::Tensor s13 = at::cat({f32(rs13, e, 2 * f), f32(ss13, 1, 2 * f)}, 0).contiguous();
+  at::Tensor s2 = at::cat({f32(rs2, e, h), f32(ss2, 1, h)}, 0).contiguous();
+  return {p13, h, 2 * f, s13, p2, f, h, s2, kBackendId, 16};
 }
 
 // Packs checkpoint int8 experts (csrc/moe/arm/i8mm_w8a8/kernels.cpp:424-444).
@@ -246,6 +329,21 @@ Bf16Tuple bf16_prepare(at::Tensor w13, at::Tensor w2) {
   at::Tensor p13 = pack(w13.contiguous(), 2);
   at::Tensor p2 = pack(w2.contiguous(), 1);
   return {p13, w13.size(2), w13.size(1), p2, w2.size(2), w2.size(1), kBackendId, 16, std::string(kBackendName)};
+}
+
+// Routed + shared BF16 experts packed into one buffer (shared expert E)
+// without concatenating the sources (bf16_tiled.py:573-609).
+Bf16Tuple bf16_prepare_routed_shared(at::Tensor rw13, at::Tensor rw2, at::Tensor sw13, at::Tensor sw2) {
+  TORCH_CHECK(rw13.scalar_type() == at::kBFloat16 && rw2.scalar_type() == at::kBFloat16,
+              "BF16 tiled fused MoE weights must be torch.bfloat16");
+  TORCH_CHECK(rw13.dim() == 3 && rw2.dim() == 3, "weights must be [E, 2F, H] and [E, H, F]");
+  TORCH_CHECK(rw13.size(0) == rw2.size(0) && rw13.size(1) % 2 == 0 && rw2.size(1) == rw13.size(2) &&
+                  rw2.size(2) == rw13.size(1) / 2,
+              "w13/w2 shape mismatch");
+  const at::Device dev = target_device(rw13);
+  at::Tensor p13 = pack_routed_shared(rw13, sw13, 2, dev);
+  at::Tensor p2 = pack_routed_shared(rw2, sw2, 1, dev);
+  return {p13, rw13.size(2), rw13.size(1), p2, rw2.size(2), rw2.size(1), kBackendId, 16, std::string(kBackendName)};
 }
 
 at::Tensor bias_f32(c10::optional<at::Tensor> b, int64_t e, int64_t n, const at::Tensor& like) {
@@ -424,6 +522,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("fused_moe_w8a16_prepare_quantized_weights", &w8a16_prepare_quantized);
   m.def("fused_moe_w8a16_forward", &w8a16_forward);
   m.def("fused_moe_bf16_prepare_weights", &bf16_prepare);
+  m.def("fused_moe_bf16_prepare_routed_shared_weights", &bf16_prepare_routed_shared);
+  m.def("fused_moe_int8_prepare_routed_shared_weights", &int8_prepare_routed_shared);
   m.def("fused_moe_bf16_forward", &bf16_forward);
   m.def("i8gemm_prepare", &i8gemm_prepare);
   m.def("i8gemm_dynamic_scaled_mm", &i8gemm_dynamic_scaled_mm);

@@ -297,14 +297,12 @@ def prepare_routed_shared_moe_w8a8_tiled_quantized_weights(
     """Append the shared expert as packed expert E (bf16_tiled.py:573-609)."""
     if shared_w13_weight.dim() != 2 or shared_w2_weight.dim() != 2:
         raise ValueError("shared W8A8 weights must be [2F, H] and [H, F]")
+    _require_backend()
     e = int(routed_w13_weight.shape[0])
-    dev = lambda t: _to_device(t)  # noqa: E731
-    packed = prepare_fused_moe_w8a8_tiled_quantized_weights(
-        torch.cat((dev(routed_w13_weight), dev(shared_w13_weight).unsqueeze(0)), dim=0),
-        torch.cat((dev(routed_w13_scale).reshape(e, -1), dev(shared_w13_scale).reshape(1, -1)), dim=0),
-        torch.cat((dev(routed_w2_weight), dev(shared_w2_weight).unsqueeze(0)), dim=0),
-        torch.cat((dev(routed_w2_scale).reshape(e, -1), dev(shared_w2_scale).reshape(1, -1)), dim=0),
-    )
+    # Packed straight into one buffer (no concatenated copy of the sources).
+    packed = _prepared_w8a8(_native.moe_C.fused_moe_int8_prepare_routed_shared_weights(
+        routed_w13_weight, routed_w13_scale.float(), routed_w2_weight, routed_w2_scale.float(), shared_w13_weight,
+        shared_w13_scale.float(), shared_w2_weight, shared_w2_scale.float(), False))
     return PreparedW8A8TiledRoutedSharedMoEWeights(packed=packed, routed_experts=e, shared_expert_id=e)
 
 
@@ -339,9 +337,22 @@ def prepare_routed_shared_moe_bf16_tiled_weights(
         shared_w13_weight = shared_w13_weight.squeeze(0)
     if shared_w2_weight.dim() == 3:
         shared_w2_weight = shared_w2_weight.squeeze(0)
-    w13 = torch.cat((_to_device(routed_w13_weight), _to_device(shared_w13_weight).unsqueeze(0)), dim=0)
-    w2 = torch.cat((_to_device(routed_w2_weight), _to_device(shared_w2_weight).unsqueeze(0)), dim=0)
-    combined = prepare_fused_moe_bf16_tiled_weights(w13, w2, fuse_silu=True, backend=backend)
+    if backend not in ("auto", _BACKEND_NAME, "arm_sve_bf16", "arm_neon_bf16"):
+        raise ValueError(f"unknown MoE backend {backend!r}; available: {_BACKEND_NAME}")
+    if any(t.dtype != torch.bfloat16 for t in (routed_w13_weight, routed_w2_weight, shared_w13_weight,
+                                                shared_w2_weight)):
+        raise TypeError("BF16 tiled fused MoE weights must be torch.bfloat16")
+    # Packed straight into one buffer (no concatenated copy of the sources).
+    packed = _native.moe_C.fused_moe_bf16_prepare_routed_shared_weights(routed_w13_weight, routed_w2_weight,
+                                                                        shared_w13_weight, shared_w2_weight)
+    combined = PreparedBF16TiledFusedMoEWeights(
+        w13=(packed[0], int(packed[1]), int(packed[2])),
+        w2=(packed[3], int(packed[4]), int(packed[5])),
+        fused_silu=True,
+        gemm_backend=int(packed[6]),
+        backend_n_tile=int(packed[7]),
+        backend_name=str(packed[8]),
+    )
     e = int(routed_w13_weight.shape[0])
     return PreparedBF16TiledRoutedSharedMoEWeights(packed=combined, routed_experts=e, shared_expert_id=e)
 
@@ -398,14 +409,12 @@ def prepare_routed_shared_moe_w8a16_tiled_quantized_weights(
     (bf16_tiled.py:541-570; native fused_moe_bf16_tiled.cpp:6276-6288)."""
     if shared_w13_weight.dim() != 2 or shared_w2_weight.dim() != 2:
         raise ValueError("shared W8A16 weights must be [2F, H] and [H, F]")
+    _require_backend()
     e = int(routed_w13_weight.shape[0])
-    dev = lambda t: _to_device(t)  # noqa: E731
-    packed = prepare_fused_moe_w8a16_tiled_quantized_weights(
-        torch.cat((dev(routed_w13_weight), dev(shared_w13_weight).unsqueeze(0)), dim=0),
-        torch.cat((dev(routed_w13_scale).reshape(e, -1), dev(shared_w13_scale).reshape(1, -1)), dim=0),
-        torch.cat((dev(routed_w2_weight), dev(shared_w2_weight).unsqueeze(0)), dim=0),
-        torch.cat((dev(routed_w2_scale).reshape(e, -1), dev(shared_w2_scale).reshape(1, -1)), dim=0),
-    )
+    # Packed straight into one buffer (no concatenated copy of the sources).
+    packed = _prepared_w8a16(_native.moe_C.fused_moe_int8_prepare_routed_shared_weights(
+        routed_w13_weight, routed_w13_scale.float(), routed_w2_weight, routed_w2_scale.float(), shared_w13_weight,
+        shared_w13_scale.float(), shared_w2_weight, shared_w2_scale.float(), True))
     return PreparedW8A16TiledRoutedSharedMoEWeights(packed=packed, routed_experts=e, shared_expert_id=e)
 
 

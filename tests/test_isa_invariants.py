@@ -10,7 +10,12 @@ silently and that each cost a large share of the kernel's speed when lost:
   object once made the compiler insert one per iteration (the K loop of a C4-sized
   launch went from 151 to 228 us per workgroup);
 * no flat memory instructions: LDS reads typed as generic pointers become flat loads,
-  which wait on vector-memory stores as well.
+  which wait on vector-memory stores as well;
+* the staged counts are exact: inside a K loop the only vector-memory instructions
+  are the loop's own ``buffer_load ... lds`` stage loads (no scratch spill or
+  reload, no other load or store), so ``vmcnt(N)`` counts exactly the loads the
+  pipeline comment assigns to it; and no kernel uses scratch at all. (A spilling
+  harness variant put spill/reload pairs with ``vmcnt(0)`` waits into its K loop.)
 """
 
 from __future__ import annotations
@@ -22,7 +27,7 @@ import pytest
 
 from fused_cpp_amd.build import CSRC, HIP_FLAGS, ROCM
 
-_KERNEL = re.compile(r"^(_Z\w*grouped_gemm_lds_kernel\w*):", re.M)
+_KERNEL = re.compile(r"^(_Z\w*grouped_gemm_lds_(?:persist_)?kernel\w*):", re.M)
 
 
 @pytest.fixture(scope="module")
@@ -83,3 +88,19 @@ def test_no_flat_memory_instructions(lds_asm):
     for name, body in _kernels(lds_asm).items():
         flat = [line.strip() for line in body if line.strip().startswith("flat_")]
         assert not flat, (name, flat[:3])
+
+
+_VMEM = ("buffer_", "global_", "scratch_", "flat_")
+
+
+def test_k_loop_vector_memory_is_only_its_stage_loads(lds_asm):
+    for name, body in _kernels(lds_asm).items():
+        ops = [line.strip() for line in _k_loop(body) if line.strip().startswith(_VMEM)]
+        assert ops, name
+        other = [op for op in ops if not (op.startswith("buffer_load_dwordx4") and op.split(";")[0].rstrip().endswith("lds"))]
+        assert not other, (name, other[:3])
+
+
+def test_no_kernel_uses_scratch(lds_asm):
+    sizes = [int(v) for v in re.findall(r"\.private_segment_fixed_size:\s+(\d+)", lds_asm)]
+    assert sizes and all(v == 0 for v in sizes), sizes

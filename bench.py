@@ -604,6 +604,77 @@ def int_mm_reference() -> int:
     return 0
 
 
+def probes() -> int:
+    """Chip figures the design relies on, from the library's probe kernels
+    (include/fcmoe.h, fcmoe_probe_*): HBM streaming by launch shape (loads to
+    VGPRs and LDS-DMA), the MFMA + LDS-fragment loop by wave tile and waves per
+    SIMD, MFMA waves beside streaming waves on one CU, and one agent-scope
+    release per workgroup. Best of 5 launches after 1 warmup (torch events on
+    the launch stream)."""
+    import torch
+
+    from fused_cpp_amd import cabi
+
+    L = cabi.lib()
+    dev = torch.device("cuda", 0)
+    stream = cabi.stream_handle()
+    sink = torch.zeros(1 << 16, dtype=torch.int32, device=dev)
+    src = torch.ones(2 << 30, dtype=torch.uint8, device=dev)
+    counters = torch.zeros(1 << 16, dtype=torch.int32, device=dev)
+    rows = torch.empty(64 << 20, dtype=torch.uint8, device=dev)
+
+    def best_ms(launch, reps=5, before=None):
+        times = []
+        for r in range(reps + 1):
+            if before:
+                before()
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            cabi.check(launch(), "probe")
+            b.record()
+            torch.cuda.synchronize()
+            if r:
+                times.append(a.elapsed_time(b))
+        return min(times)
+
+    out = {"stream": [], "mfma": [], "mix": [], "fence": []}
+    for nbytes, wgs, waves, mode, pad in [(2 << 30, 256, 8, 0, 0), (2 << 30, 256, 8, 1, 0), (2 << 30, 144, 8, 0, 98304),
+                                          (2 << 30, 128, 8, 0, 98304), (2 << 30, 128, 8, 1, 98304),
+                                          (2 << 30, 64, 8, 0, 98304), (2 << 30, 64, 8, 1, 98304),
+                                          (2 << 30, 1152, 1, 0, 0), (2 << 30, 4096, 8, 0, 0),
+                                          (264 << 20, 256, 8, 0, 0), (264 << 20, 144, 8, 0, 0)]:
+        ms = best_ms(lambda: L.fcmoe_probe_stream(src.data_ptr(), nbytes, wgs, waves, mode, pad, sink.data_ptr(),
+                                                  stream))
+        moved = nbytes // 1024 // (wgs * waves) * (wgs * waves) * 1024
+        out["stream"].append({"bytes": moved, "workgroups": wgs, "waves": waves,
+                              "path": "lds_dma" if mode else "vgpr_nontemporal", "lds_pad": pad,
+                              "us": round(ms * 1e3, 1), "TBps": round(moved / ms / 1e9, 3),
+                              "GBps_per_busy_cu": round(moved / ms / 1e6 / min(wgs, 256), 1)})
+    for tile, name, waves in [(0, "128x96", 8), (0, "128x96", 4), (1, "128x64", 8), (1, "128x64", 12),
+                              (2, "96x80", 12), (3, "64x96", 12), (4, "64x64", 8), (4, "64x64", 16)]:
+        fm, fn = [int(v) // 16 for v in name.split("x")]
+        iters = 20000 // (fm * fn) * 8
+        ms = best_ms(lambda: L.fcmoe_probe_mfma(tile, waves, 256, iters, sink.data_ptr(), stream))
+        ops = 256 * waves * iters * fm * fn * 32768
+        out["mfma"].append({"wave_tile": name, "waves_per_cu": waves, "reads_per_mfma": round((fm + fn) / (fm * fn), 3),
+                            "us": round(ms * 1e3, 1), "POPS": round(ops / ms / 1e12, 3)})
+    iters = 4000
+    for nc, ns, smfma in [(8, 0, 0), (0, 4, 0), (0, 8, 0), (8, 4, 0), (8, 8, 0), (8, 8, 1), (4, 4, 0), (4, 0, 0)]:
+        ms = best_ms(lambda: L.fcmoe_probe_mix(src.data_ptr(), 2 << 30, nc, ns, iters, smfma, sink.data_ptr(), stream))
+        moved = (2 << 30) // 1024 // (256 * ns) // 8 * 8 * 1024 * 256 * ns if ns else 0
+        ops = 256 * nc * iters * 7 * 32768
+        out["mix"].append({"compute_waves": nc, "stream_waves": ns, "stream_mfma": bool(smfma),
+                           "us": round(ms * 1e3, 1), "POPS": round(ops / ms / 1e12, 3),
+                           "TBps": round(moved / ms / 1e9, 3)})
+    for wgs, waves, rel in [(144, 8, 0), (144, 8, 1), (3552, 8, 0), (3552, 8, 1)]:
+        ms = best_ms(lambda: L.fcmoe_probe_fence(src.data_ptr(), 264 << 20, wgs, waves, rel, counters.data_ptr(),
+                                                 rows.data_ptr(), stream), before=counters.zero_)
+        out["fence"].append({"workgroups": wgs, "waves": waves, "release_per_workgroup": bool(rel),
+                             "bytes": 264 << 20, "us": round(ms * 1e3, 1)})
+    print(json.dumps({"probes": out}))
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -627,7 +698,12 @@ def main() -> int:
                     help="only time the vendor int8 GEMM (torch._int_mm -> hipBLASLt, int32 out, no gather "
                          "or epilogue) at the prefill experts' shapes, as a reference point for the grouped "
                          "kernels' TOPS")
+    ap.add_argument("--probe", action="store_true",
+                    help="only run the library's measurement probes (streaming ceiling, MFMA loop rates, MFMA "
+                         "beside streaming waves, release-fence cost) and print them as one JSON line")
     args = ap.parse_args()
+    if args.probe:
+        return probes()
     if args.int_mm_reference:
         return int_mm_reference()
     if args.copy_calibration:

@@ -423,6 +423,7 @@ int run_w8a8_stage(const TileClasses& tc, const RouteBuffers& rb, int epi, const
     GemmParams pm = gate;
     pm.plan_mixed = 1;
     pm.persist = persistent_wgs();
+    pm.queue = rb.queues + (stage_mixed == FCMOE_STAGE_W13_MIXED_MFMA ? 0 : 8);
     pm.u_n = 3;
     int64_t big_bound = 0;
     for (int u = 0; u < 3; ++u) {

@@ -313,7 +313,7 @@ __device__ __forceinline__ void lds_gemm_body(const GemmParams& p, int n_blocks,
   constexpr int HP = FN / 2;
   static_assert(SA >= 2 && SB >= SA, "A ring of 2+ stages, B ring at least as deep");
   static_assert(WAIT < 64, "vmcnt range");
-  static_assert(SA * A_BYTES + SB * B_BYTES + 8 * BM + 64 * NT <= 160 * 1024, "LDS budget");
+  static_assert(SA * A_BYTES + SB * B_BYTES + 8 * BM + 64 * NT + 16 <= 160 * 1024, "LDS budget");
   static_assert(NT * 16 <= THREADS && BM <= THREADS, "one metadata value per thread");
   static_assert(FM >= 3, "the fragment ring runs two fragments ahead");
   typedef typename Acc<I8>::type AccT;
@@ -323,7 +323,7 @@ __device__ __forceinline__ void lds_gemm_body(const GemmParams& p, int n_blocks,
   // reads apart from the in-flight buffer_load ... lds writes and put a
   // vmcnt(0) in every K iteration, draining the prefetch ring.)
   constexpr int META = SA * A_BYTES + SB * B_BYTES;
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[META + 8 * BM + 64 * NT];
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[META + 8 * BM + 64 * NT + 16];
   float* const meta_rs = (float*)(smem + META);
   int* const meta_orow = (int*)(smem + META + 4 * BM);
   float* const meta_cs = (float*)(smem + META + 8 * BM);
@@ -344,13 +344,42 @@ __device__ __forceinline__ void lds_gemm_body(const GemmParams& p, int n_blocks,
     count = *p.tile_count;
   }
   // Persistent launches (p.persist > 0): gridDim.x workgroups (a multiple of
-  // the XCD count, so an item keeps its XCD) stride over the `grid_items`
-  // item slots; otherwise each workgroup runs slot blockIdx.x.
-  const int slot_step = PERSIST ? (int)gridDim.x : grid_items;
-  for (int it = 0, slot = (int)blockIdx.x; PERSIST ? slot < grid_items : it < 1; ++it, slot += slot_step) {
+  // the XCD count, so an item keeps its XCD) loop over the item slots of
+  // their XCD, x + 8 k: with a queue, k comes from the XCD's counter (the
+  // next item, whatever the other workgroups' items cost); without one,
+  // workgroup b takes k = b / 8, b / 8 + gridDim.x / 8, ... Otherwise each
+  // workgroup runs slot blockIdx.x.
+  // (in the one LDS object: a second __shared__ object costs the K loop a
+  // vmcnt(0) per chunk, see above)
+  int* const next_k = (int*)(smem + META + 8 * BM + 64 * NT);
+  const int xcd = (int)blockIdx.x % kXcds;
+  int xcd_items = 0;  // valid slots of this XCD (lds_work_item's layout)
+  if constexpr (PERSIST) {
+    const int nbf = partial ? n_blocks - 1 : n_blocks;
+    const int F = count * nbf, P = partial ? count : 0;
+    xcd_items = F / kXcds + (xcd < F % kXcds ? 1 : 0) + P / kXcds + (xcd < P % kXcds ? 1 : 0);
+    if (gm <= 0) xcd_items = grid_items;  // plain order: slots are not XCD-local
+  }
+  auto fetch_k = [&](int k_static) -> int {
+    if (!PERSIST || !p.queue) return k_static;
+    __syncthreads();  // everyone has read the previous next_k
+    if (threadIdx.x == 0) *next_k = __hip_atomic_fetch_add(p.queue + xcd, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    return *next_k;
+  };
+  int k = PERSIST ? fetch_k((int)blockIdx.x / kXcds) : 0;
+  for (int it = 0, slot = (int)blockIdx.x; PERSIST ? k < xcd_items : it < 1; ++it) {
+  if constexpr (PERSIST) slot = gm <= 0 ? (int)blockIdx.x + it * (int)gridDim.x : k * kXcds + xcd;
   int tile_idx, nb;
-  if (!lds_work_item(slot, count, n_blocks, partial != 0, gm, tile_idx, nb)) continue;
-  if (PERSIST && slot != (int)blockIdx.x) __syncthreads();  // the previous item's epilogue is done with the stages
+  const bool have = lds_work_item(slot, count, n_blocks, partial != 0, gm, tile_idx, nb);
+  if constexpr (PERSIST) {
+    k = fetch_k(k + (int)gridDim.x / kXcds);
+    if (gm <= 0) k = slot + (int)gridDim.x < grid_items ? 0 : xcd_items;  // plain order: stride over all slots
+    if (!have) continue;
+    if (it > 0) __syncthreads();  // the previous item's epilogue is done with the stages
+  } else {
+    if (!have) return;
+  }
   // last-first within a list, as the register kernel
   const int32_t* tpair = p.tiles + 2 * (count - 1 - tile_idx);
   if constexpr (PERSIST) {

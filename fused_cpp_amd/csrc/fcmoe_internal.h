@@ -53,7 +53,11 @@ struct RouteBuffers {
   int32_t* tiles = nullptr;          // [classes][bound][2] (expert, m_begin)
   int32_t* tile_count = nullptr;     // [classes]
   int32_t* invalid = nullptr;        // [1]
+  int32_t* queues = nullptr;         // [kRouteQueues] work-queue counters, zeroed by the route launch
 };
+// Work-queue counters the route launch zeroes for the GEMM launches after it
+// (the mixed prefill plan's persistent launch: one per XCD and stage).
+constexpr int kRouteQueues = 32;
 // Routes per workgroup of the count / scatter kernels. (1024-route chunks
 // shortened the column scan but left too few workgroups: C3's route stage
 // went from 30 to 39 us.)
@@ -151,6 +155,9 @@ struct GemmParams {
   int u_n;
   const int32_t* u_tiles[3];
   const int32_t* u_count[3];
+  // Persistent LDS launches: per-XCD item counters (8, zero at launch); a
+  // workgroup takes its XCD's next item from them instead of striding.
+  int32_t* queue;
 };
 
 // Whether a launch's plan gate lets it run (device side).

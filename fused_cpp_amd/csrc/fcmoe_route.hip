@@ -43,6 +43,12 @@ struct RouteArgs {
   int scale_routed;
 };
 
+// Block 0 of a route launch zeroes the work-queue counters the GEMM launches
+// after it use.
+__device__ __forceinline__ void zero_queues(int32_t* queues) {
+  if (queues && blockIdx.x == 0 && threadIdx.x < kRouteQueues) queues[threadIdx.x] = 0;
+}
+
 __device__ __forceinline__ int route_expert(const RouteArgs& a, int64_t r, bool* valid) {
   const int64_t t = r / a.kt;
   const int s = (int)(r - t * a.kt);
@@ -257,9 +263,11 @@ __global__ __launch_bounds__(kScanThreads) void route_scan_kernel(int experts, i
 __global__ __launch_bounds__(kRouteChunk) void route_scatter_kernel(RouteArgs a, int64_t routes,
                                                                      const int32_t* chunk_hist,
                                                                      const int32_t* offsets, int32_t* sorted_routes,
-                                                                     int32_t* row_token, int32_t* route_pos) {
+                                                                     int32_t* row_token, int32_t* route_pos,
+                                                                     int32_t* queues) {
   __shared__ __attribute__((aligned(16))) int32_t ex[kRouteChunk];
   const int tid = threadIdx.x;
+  zero_queues(queues);
   const int64_t r = (int64_t)blockIdx.x * kRouteChunk + tid;
   int e = -1;
   if (r < routes) {
@@ -304,6 +312,7 @@ struct RouteOut {
   int32_t* route_pos;
   float* route_weight;
   int32_t* invalid;
+  int32_t* queues;
 };
 
 __device__ __forceinline__ void route_small_body(const RouteArgs& a, int routes, const ClassArgs& cls,
@@ -373,6 +382,7 @@ __device__ __forceinline__ void route_small_body(const RouteArgs& a, int routes,
 
 __global__ __launch_bounds__(kScanThreads) void route_small_kernel(RouteArgs a, int routes, ClassArgs cls,
                                                                    RouteOut o) {
+  zero_queues(o.queues);
   route_small_body(a, routes, cls, o);
 }
 
@@ -397,6 +407,7 @@ template <int CAP>
 __global__ __launch_bounds__(kScanThreads) void route_quant_small_kernel(RouteArgs a, int routes, ClassArgs cls,
                                                                          RouteOut o, QuantRows qr) {
   if (blockIdx.x == 0) {
+    zero_queues(o.queues);
     route_small_body(a, routes, cls, o);
     return;
   }
@@ -492,6 +503,7 @@ void route_take(Arena& ar, RouteBuffers& rb, int64_t routes, int64_t experts, co
   rb.tiles = ar.take<int32_t>(2 * tiles);
   rb.tile_count = ar.take<int32_t>(kMaxClasses);
   rb.invalid = ar.take<int32_t>(1);
+  rb.queues = ar.take<int32_t>(kRouteQueues);
 }
 
 int route_launch(const void* ids, int ids_is_i64, const float* topk_w, int64_t tokens, int64_t top_k,
@@ -521,7 +533,7 @@ int route_launch(const void* ids, int ids_is_i64, const float* topk_w, int64_t t
   const ClassArgs ca = class_args(tc);
   if (routes <= kScanThreads) {
     const RouteOut o{rb.counts,    rb.offsets,   rb.tiles,        rb.tile_count, rb.sorted_routes,
-                     rb.row_token, rb.route_pos, rb.route_weight, invalid};
+                     rb.row_token, rb.route_pos, rb.route_weight, invalid,      rb.queues};
     if (const int cap = quant_done ? quant_cap(quant) : 0) {
       const dim3 grid((unsigned)(1 + ceil_div(quant->rows, kQuantRowsPerGroup))), block(kScanThreads);
       with_cap(cap, [&](auto c) {
@@ -549,7 +561,7 @@ int route_launch(const void* ids, int ids_is_i64, const float* topk_w, int64_t t
                        rb.chunk_hist, rb.counts, rb.offsets, ca, rb.tiles, rb.tile_count, rb.chunk_invalid, invalid);
   }
   hipLaunchKernelGGL(route_scatter_kernel, dim3((unsigned)chunks), dim3(kRouteChunk), 0, stream, a, routes,
-                     rb.chunk_hist, rb.offsets, rb.sorted_routes, rb.row_token, rb.route_pos);
+                     rb.chunk_hist, rb.offsets, rb.sorted_routes, rb.row_token, rb.route_pos, rb.queues);
   return check_launch("route");
 }
 

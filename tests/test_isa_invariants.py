@@ -104,3 +104,31 @@ def test_k_loop_vector_memory_is_only_its_stage_loads(lds_asm):
 def test_no_kernel_uses_scratch(lds_asm):
     sizes = [int(v) for v in re.findall(r"\.private_segment_fixed_size:\s+(\d+)", lds_asm)]
     assert sizes and all(v == 0 for v in sizes), sizes
+
+
+def _vgprs(asm: str) -> dict[str, int]:
+    """VGPR count of every kernel in a device assembly file (from its metadata)."""
+    names = re.findall(r"^\s+\.name:\s+(\S+)", asm, re.M)
+    counts = [int(v) for v in re.findall(r"^\s+\.vgpr_count:\s+(\d+)", asm, re.M)]
+    assert len(names) == len(counts), (len(names), len(counts))
+    return dict(zip(names, counts))
+
+
+def test_mixed_plan_register_budget(lds_asm, tmp_path):
+    """The mixed prefill plan relies on one workgroup of the persistent MFMA
+    kernel (two waves per SIMD) and one of the 16-row streaming kernel (one
+    wave per SIMD) sharing every CU: 2 x 216 + 80 <= 512 VGPRs (allocation
+    granule 8). A kernel that grows past its budget silently loses the
+    co-residency (C3 2.9 -> 5.6 ms when the MFMA kernel reached 225)."""
+    hipcc = ROCM / "bin" / "hipcc"
+    out = tmp_path / "fcmoe_gemm.s"
+    proc = subprocess.run([str(hipcc), *HIP_FLAGS, "--cuda-device-only", "-S", str(CSRC / "fcmoe_gemm.hip"),
+                           "-o", str(out)], capture_output=True, text=True)
+    assert proc.returncode == 0, proc.stdout + proc.stderr
+    mfma = {k: v for k, v in _vgprs(lds_asm).items() if "grouped_gemm_lds_persist_kernelILb1E" in k}
+    stream = {k: v for k, v in _vgprs(out.read_text()).items() if "grouped_gemm_stream_kernelILb1E" in k}
+    assert mfma and stream
+    rnd = lambda v: (v + 7) // 8 * 8  # noqa: E731
+    assert all(rnd(v) <= 216 for v in mfma.values()), mfma
+    assert all(rnd(v) <= 80 for v in stream.values()), stream
+    assert 2 * max(rnd(v) for v in mfma.values()) + max(rnd(v) for v in stream.values()) <= 512

@@ -108,3 +108,44 @@ def test_router_and_i8gemm_graph_replays(gpu):
         return torch.cat([out.float().reshape(-1), w.reshape(-1), ids.float().reshape(-1)])
 
     _replay_matches_eager(fn, make, static)
+
+
+@pytest.mark.parametrize("min_tiles", ["4", "0"])
+def test_w8a8_prefill_mixed_plan_graph_replays(gpu, min_tiles):
+    """Skewed prefill routing where the device picks the mixed launch plan
+    (persistent MFMA launch beside the 16-row streaming launch, forked streams,
+    per-XCD work queues zeroed by the route launch): "4" enqueues both plans
+    (the classic launches exit on the device), "0" forces the mixed plan alone."""
+    import os
+
+    from fused_cpp_amd import moe
+
+    T, Hd, F, E, k = 256, 1024, 512, 96, 6
+    x, ids, w, q13, s13, q2, s2 = H.w8a8_case(31, T, Hd, F, E + 1, k, skew=1.2)
+    ids = np.minimum(ids, E - 1)
+    t = torch.from_numpy
+    prepared = moe.prepare_routed_shared_moe_w8a8_tiled_quantized_weights(
+        t(q13[:-1]), t(s13[:-1]), t(q2[:-1]), t(s2[:-1]), t(q13[-1]), t(s13[-1]), t(q2[-1]), t(s2[-1]))
+    counts = np.bincount(ids.ravel(), minlength=E)
+    assert ((counts > 0) & (counts <= 16)).sum() >= 32, counts  # the mixed plan's default trigger
+    rng = np.random.default_rng(1)
+
+    def make(r):
+        xr = torch.from_numpy(H.bf16_bits(rng.standard_normal((T, Hd)).astype(np.float32)).view(np.int16))
+        _, wr = H.zipf_topk(rng, T, E, k)
+        return xr.to(gpu).view(torch.bfloat16), torch.from_numpy(wr).to(gpu), torch.from_numpy(ids).to(gpu)
+
+    static = list(make(-1))
+
+    def fn(xx, ww, ii):
+        return moe.fused_moe_w8a8_tiled_with_shared(xx, prepared, ww, ii, routed_scaling_factor=2.5)
+
+    old = os.environ.get("FCMOE_PREFILL_MIXED_MIN_TILES")
+    os.environ["FCMOE_PREFILL_MIXED_MIN_TILES"] = min_tiles
+    try:
+        _replay_matches_eager(fn, make, static)
+    finally:
+        if old is None:
+            del os.environ["FCMOE_PREFILL_MIXED_MIN_TILES"]
+        else:
+            os.environ["FCMOE_PREFILL_MIXED_MIN_TILES"] = old

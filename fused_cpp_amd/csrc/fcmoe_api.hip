@@ -396,9 +396,15 @@ namespace {
 // most 16 rows beside MFMA-bound ones (skewed routing, C3: 149 such experts)
 // the HBM stream hides under the MFMA work (C3 3.12 -> 2.81 ms); with few of
 // them the classic plan is faster (uniform routing at T = 1024: 2.15 vs 2.30
-// ms, C4 4.30 vs 5.10 ms). The route scan's count of 16-row tiles picks the
-// plan: every launch of the other plan exits at once (no host round trip).
+// ms, C4 4.30 vs 5.10 ms), and so it is when there is little MFMA work beside
+// them (uniform T = 256: 2.19 vs 5.43 ms -- the 4-wave streaming launch is
+// tuned to sit beside MFMA workgroups, not to stream alone). The route scan's
+// tile counts pick the plan: mixed when the 16-row class has at least
+// kPrefillMixedMinTiles tiles and the 256-row class at least
+// kPrefillMixedMinBigTiles; every launch of the other plan exits at once (no
+// host round trip).
 constexpr int kPrefillMixedMinTiles = 32;
+constexpr int kPrefillMixedMinBigTiles = 16;
 
 // FCMOE_PREFILL_MIXED_MIN_TILES overrides the threshold (0: always the mixed
 // plan; a large value: never); read on every call so that tests can run both
@@ -418,6 +424,10 @@ int run_w8a8_stage(const TileClasses& tc, const RouteBuffers& rb, int epi, const
   if (prefill) {
     gate.plan_tiles = rb.tile_count;  // class 0: the 16-row tiles
     gate.plan_min = mixed_min_tiles();
+    if (gate.plan_min > 0) {  // a forced mixed plan (0) skips the second condition
+      gate.plan_tiles2 = rb.tile_count + 3;  // class 3: the 256-row tiles
+      gate.plan_min2 = kPrefillMixedMinBigTiles;
+    }
     // Mixed plan. The persistent MFMA launch takes classes 256, 192, 128 (in
     // that order) as one item space; the 16-row class streams beside it.
     GemmParams pm = gate;
@@ -444,11 +454,6 @@ int run_w8a8_stage(const TileClasses& tc, const RouteBuffers& rb, int epi, const
       p.plan_mixed = 0;
       p.tiles = rb.tiles + 2 * tile_offset(tc, c);
       p.tile_count = rb.tile_count + c;
-      // The 16-row class loops over its items on one workgroup per CU: a
-      // class with few or no tiles then dispatches 256 workgroups, not the
-      // thousands its host-side bound allows (C4, whose 16-row class is
-      // empty: 4.67 -> 4.30 ms with the classes side by side).
-      if (c == 0) p.persist = persistent_wgs();
       Stage st(stage0 + class_slot(tc.bm[c]), s);
       return gemm_launch(epi, tc.bm[c], p, tc.bound[c], s);
     };

@@ -144,10 +144,13 @@ struct GemmParams {
   // (4 waves per workgroup, few enough VGPRs to share each SIMD with it).
   int stream_role;
   // Launch-plan gate (W8A8 prefill; see the forward): when plan_tiles is set
-  // the launch does its work only if (*plan_tiles >= plan_min) == plan_mixed,
-  // and otherwise every workgroup exits at once.
+  // the launch does its work only if (*plan_tiles >= plan_min and, when
+  // plan_tiles2 is set, *plan_tiles2 >= plan_min2) == plan_mixed, and
+  // otherwise every workgroup exits at once.
   const int32_t* plan_tiles;
   int plan_min;
+  const int32_t* plan_tiles2;  // optional second count that must also reach plan_min2
+  int plan_min2;
   int plan_mixed;
   // Several classes' tile lists as one item space (the persistent LDS launch
   // of the mixed plan): u_n > 0 replaces tiles / tile_count by lists
@@ -162,7 +165,9 @@ struct GemmParams {
 
 // Whether a launch's plan gate lets it run (device side).
 __device__ __forceinline__ bool plan_open(const GemmParams& p) {
-  return !p.plan_tiles || ((*p.plan_tiles >= p.plan_min) == (p.plan_mixed != 0));
+  if (!p.plan_tiles) return true;
+  const bool mixed = *p.plan_tiles >= p.plan_min && (!p.plan_tiles2 || *p.plan_tiles2 >= p.plan_min2);
+  return mixed == (p.plan_mixed != 0);
 }
 
 int gemm_launch(int epi, int bm, const GemmParams& p, int64_t max_tiles, hipStream_t stream);

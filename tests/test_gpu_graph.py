@@ -110,24 +110,27 @@ def test_router_and_i8gemm_graph_replays(gpu):
     _replay_matches_eager(fn, make, static)
 
 
-@pytest.mark.parametrize("min_tiles", ["4", "0"])
+@pytest.mark.parametrize("min_tiles", ["32", "0"])
 def test_w8a8_prefill_mixed_plan_graph_replays(gpu, min_tiles):
     """Skewed prefill routing where the device picks the mixed launch plan
     (persistent MFMA launch beside the 16-row streaming launch, forked streams,
-    per-XCD work queues zeroed by the route launch): "4" enqueues both plans
-    (the classic launches exit on the device), "0" forces the mixed plan alone."""
+    per-XCD work queues zeroed by the route launch): "32" (the default) enqueues
+    both plans (the classic launches exit on the device), "0" forces the mixed
+    plan alone."""
     import os
 
     from fused_cpp_amd import moe
 
-    T, Hd, F, E, k = 256, 1024, 512, 96, 6
+    T, Hd, F, E, k = 2048, 1024, 512, 160, 6
     x, ids, w, q13, s13, q2, s2 = H.w8a8_case(31, T, Hd, F, E + 1, k, skew=1.2)
     ids = np.minimum(ids, E - 1)
     t = torch.from_numpy
     prepared = moe.prepare_routed_shared_moe_w8a8_tiled_quantized_weights(
         t(q13[:-1]), t(s13[:-1]), t(q2[:-1]), t(s2[:-1]), t(q13[-1]), t(s13[-1]), t(q2[-1]), t(s2[-1]))
     counts = np.bincount(ids.ravel(), minlength=E)
-    assert ((counts > 0) & (counts <= 16)).sum() >= 32, counts  # the mixed plan's default trigger
+    # the mixed plan's default trigger: >= 32 tiles of <= 16 rows, >= 16 tiles of 256 rows
+    assert ((counts > 0) & (counts <= 16)).sum() >= 32, counts
+    assert sum((int(c) + 255) // 256 for c in counts if c > 192) + (T + 255) // 256 >= 16, counts
     rng = np.random.default_rng(1)
 
     def make(r):

@@ -194,6 +194,25 @@ def class_of(c: int, decode: bool, kind: str = "w8a8") -> int:
     return CLASS_BM.index(bms[-1])
 
 
+def prefill_plan(counts) -> tuple[str, int]:
+    """Host mirror of the device's W8A8 prefill launch-plan choice
+    (fcmoe_api.hip run_w8a8_stage, fcmoe_internal.h part_wgs): "mixed" when
+    there are >= 32 tiles of 16 rows and >= 16 of 256 rows; otherwise
+    "partitioned" (the 256-row class on its own persistent launch over
+    `wgs` CUs) or "classic". Tile counts: one tile per expert of 1-192 rows,
+    ceil(rows / 256) for larger experts."""
+    counts = np.asarray(counts)
+    t = [int(((counts > 0) & (counts <= 16)).sum()), int(((counts > 16) & (counts <= 128)).sum()),
+         int(((counts > 128) & (counts <= 192)).sum()), int(np.ceil(counts[counts > 192] / 256).sum())]
+    if t[0] >= 32 and t[3] >= 16:
+        return "mixed", 0
+    t3, ts = 20 * t[3], 8 * (t[1] + t[2]) + t[0]
+    if t3 == 0:
+        return "classic", 0
+    w = 256 * t3 // (t3 + ts) // 8 * 8
+    return ("classic", 0) if w > 128 else ("partitioned", max(w, 32))
+
+
 def algorithmic(cfg, counts):
     """Algorithmic HBM bytes and ops of the layer and of each GEMM stage class.
 
@@ -232,6 +251,10 @@ def algorithmic(cfg, counts):
             stages[f"w2_{name}"] = dict(
                 bytes=n_exp * (H * I * eb + H * sb) + r * I * eb + r * H * 4, ops=r * 2 * H * I, experts=n_exp,
                 rows=r)
+        # the partitioned classic plan's persistent launch: the 256-row class
+        for st in ("w13", "w2"):
+            if f"{st}_bm256" in stages:
+                stages[f"{st}_part256"] = stages[f"{st}_bm256"]
     return layer_bytes, layer_ops, stages
 
 
@@ -539,6 +562,11 @@ def measure(cfg, workload: str, args, device, want_cpu: bool):
     counts = expert_counts(cfg, res["ids"])
     layer_bytes, layer_ops, st_alg = algorithmic(cfg, counts)
     ms = res["ms"]
+    plan = None
+    if cfg["kind"] == "w8a8" and counts.sum() > 8 * len(counts):
+        plan, part = prefill_plan(counts)
+        if plan == "partitioned":  # the persistent launch ran the 256-row class, not the mixed plan
+            res["stages"] = {k.replace("_mixed_mfma", "_part256"): v for k, v in res["stages"].items()}
     # dominant kernel: largest per-step GPU time among GEMM stages
     best = None
     for name, (tot, n) in res["stages"].items():
@@ -563,6 +591,8 @@ def measure(cfg, workload: str, args, device, want_cpu: bool):
         layer["bf16_mfma_frac"] = layer.pop("int8_mfma_frac")
     if res.get("tau") is not None:
         layer["zipf_tau"] = res["tau"]
+    if plan is not None:
+        layer["prefill_plan"] = plan if plan != "partitioned" else f"partitioned ({part} CUs for the 256-row class)"
     out = {"ms": ms, "tokens_per_s": cfg["T"] / (ms * 1e-3), "roofline": roof, "layer": layer}
     if cfg["kind"] == "w8a8":
         out["parity"] = parity_check(cfg, res)

@@ -414,6 +414,13 @@ int mixed_min_tiles() {
   return v && v[0] ? atoi(v) : kPrefillMixedMinTiles;
 }
 
+// Partitioned classic plan on (default) or off (FCMOE_PREFILL_PART=0, so
+// that tests can compare both); read on every call.
+bool part_enabled() {
+  const char* v = getenv("FCMOE_PREFILL_PART");
+  return !(v && v[0] == '0');
+}
+
 // One W8A8 GEMM stage (epilogue epi, stage-timing base id stage0) over the
 // prefill class set {16, 128, 192, 256}, or over any other class set with the
 // classic launches only.
@@ -442,6 +449,13 @@ int run_w8a8_stage(const TileClasses& tc, const RouteBuffers& rb, int epi, const
       pm.u_count[u] = rb.tile_count + c;
       big_bound += tc.bound[c];
     }
+    // Partitioned classic plan: the persistent launch also carries the
+    // 256-row class for the case that the classic plan is chosen (its own
+    // queue counters: 16..23 for W13, 24..31 for W2).
+    const int32_t* part = gate.plan_min > 0 && part_enabled() ? rb.tile_count : nullptr;
+    pm.part_counts = part;
+    pm.part_tiles = rb.tiles + 2 * tile_offset(tc, 3);
+    pm.part_queue = rb.queues + (stage_mixed == FCMOE_STAGE_W13_MIXED_MFMA ? 16 : 24);
     GemmParams ps = gate;
     ps.plan_mixed = 1;
     ps.persist = persistent_wgs();
@@ -454,6 +468,10 @@ int run_w8a8_stage(const TileClasses& tc, const RouteBuffers& rb, int epi, const
       p.plan_mixed = 0;
       p.tiles = rb.tiles + 2 * tile_offset(tc, c);
       p.tile_count = rb.tile_count + c;
+      if (c == 3 && part) {  // exits when the persistent launch takes this class
+        p.part_counts = part;
+        p.part_exit = 1;
+      }
       Stage st(stage0 + class_slot(tc.bm[c]), s);
       return gemm_launch(epi, tc.bm[c], p, tc.bound[c], s);
     };

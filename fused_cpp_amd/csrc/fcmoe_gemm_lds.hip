@@ -329,17 +329,26 @@ __device__ __forceinline__ void lds_gemm_body(const GemmParams& p, int n_blocks,
   float* const meta_cs = (float*)(smem + META + 8 * BM);
   uint8_t* const smem_b = smem + SA * A_BYTES;
 
-  if (!plan_open(p)) return;
+  // A persistent launch whose plan is not taken may still run the 256-row
+  // class of the partitioned classic plan on its first part_wgs workgroups.
+  bool part = false;
+  if (!plan_open(p)) {
+    if (!PERSIST || !p.part_counts || (int)blockIdx.x >= part_wgs(p.part_counts)) return;
+    part = true;
+  }
+  const int32_t* const tiles0 = part ? p.part_tiles : p.tiles;
+  int32_t* const queue = part ? p.part_queue : p.queue;
+  const int u_n = part ? 0 : p.u_n;
   // Item space: one class's tile list, or (u_n > 0) several lists back to back.
   int ucount[3] = {0, 0, 0};
   int count;
   if constexpr (PERSIST) {
     count = 0;
-    for (int u = 0; u < p.u_n; ++u) {
+    for (int u = 0; u < u_n; ++u) {
       ucount[u] = *p.u_count[u];
       count += ucount[u];
     }
-    if (p.u_n == 0) count = *p.tile_count;
+    if (u_n == 0) count = part ? p.part_counts[3] : *p.tile_count;
   } else {
     count = *p.tile_count;
   }
@@ -361,9 +370,9 @@ __device__ __forceinline__ void lds_gemm_body(const GemmParams& p, int n_blocks,
     if (gm <= 0) xcd_items = grid_items;  // plain order: slots are not XCD-local
   }
   auto fetch_k = [&](int k_static) -> int {
-    if (!PERSIST || !p.queue) return k_static;
+    if (!PERSIST || !queue) return k_static;
     __syncthreads();  // everyone has read the previous next_k
-    if (threadIdx.x == 0) *next_k = __hip_atomic_fetch_add(p.queue + xcd, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (threadIdx.x == 0) *next_k = __hip_atomic_fetch_add(queue + xcd, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
     return *next_k;
   };
@@ -381,11 +390,11 @@ __device__ __forceinline__ void lds_gemm_body(const GemmParams& p, int n_blocks,
     if (!have) return;
   }
   // last-first within a list, as the register kernel
-  const int32_t* tpair = p.tiles + 2 * (count - 1 - tile_idx);
+  const int32_t* tpair = tiles0 + 2 * (count - 1 - tile_idx);
   if constexpr (PERSIST) {
-    if (p.u_n > 0) {
+    if (u_n > 0) {
       int t = tile_idx, u = 0;
-      while (u + 1 < p.u_n && t >= ucount[u]) t -= ucount[u++];
+      while (u + 1 < u_n && t >= ucount[u]) t -= ucount[u++];
       tpair = p.u_tiles[u] + 2 * (ucount[u] - 1 - t);
     }
   }

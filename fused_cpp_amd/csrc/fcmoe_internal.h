@@ -161,13 +161,39 @@ struct GemmParams {
   // Persistent LDS launches: per-XCD item counters (8, zero at launch); a
   // workgroup takes its XCD's next item from them instead of striding.
   int32_t* queue;
+  // Partitioned classic plan (W8A8 prefill). part_counts: the four class
+  // tile counts of the route scan (NULL: not partitioned). When the classic
+  // plan is chosen and part_wgs(part_counts) > 0, the persistent launch's
+  // first part_wgs workgroups run the 256-row class (part_tiles, items from
+  // part_queue) on their own CUs while the classic launches of the other
+  // classes run on the rest; the classic 256-row launch (part_exit set)
+  // then exits.
+  const int32_t* part_counts;
+  const int32_t* part_tiles;
+  int32_t* part_queue;
+  int part_exit;
 };
 
 // Whether a launch's plan gate lets it run (device side).
+// Workgroups the partitioned classic plan gives the 256-row class (a
+// multiple of the 8 XCDs; 0: not partitioned), from the class tile counts
+// c[0..3] (16 / 128 / 192 / 256 rows). Each 256-row tile holds MFMA-bound
+// work; each 128/192-row tile streams one expert's weights (a 16-row tile an
+// eighth of that). The 256-row class gets CUs in proportion to its weighted
+// share, 2.5 : 1, within [32, 128]; when it would need more than 128 (or has
+// no tiles) the classic launches share every CU instead.
+__host__ __device__ __forceinline__ int part_wgs(const int32_t* c) {
+  const int64_t t3 = 20 * (int64_t)c[3], ts = 8 * ((int64_t)c[1] + c[2]) + c[0];
+  if (t3 == 0) return 0;
+  const int64_t w = 256 * t3 / (t3 + ts) / 8 * 8;
+  return w > 128 ? 0 : (w < 32 ? 32 : (int)w);
+}
+
 __device__ __forceinline__ bool plan_open(const GemmParams& p) {
   if (!p.plan_tiles) return true;
   const bool mixed = *p.plan_tiles >= p.plan_min && (!p.plan_tiles2 || *p.plan_tiles2 >= p.plan_min2);
-  return mixed == (p.plan_mixed != 0);
+  if (mixed != (p.plan_mixed != 0)) return false;
+  return !(p.part_exit && part_wgs(p.part_counts) > 0);
 }
 
 int gemm_launch(int epi, int bm, const GemmParams& p, int64_t max_tiles, hipStream_t stream);

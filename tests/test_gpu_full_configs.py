@@ -105,8 +105,12 @@ def test_w8a8_full_config_bit_exact(gpu, oracle_lib, name):
         assert classes["w13_mixed_mfma"] > 10 * classes["w13_bm256"], classes
         assert classes["w13_mixed_stream"] > 10 * classes["w13_bm16"], classes
     if name == "c4":
-        # the classic plan ran: no 16-row experts, the 192-row class does the work
-        assert classes["w13_bm192"] > 10 * classes["w13_mixed_mfma"], classes
+        # the partitioned classic plan ran: no 16-row experts; the 192-row
+        # class launch does most of the work, the persistent launch took the
+        # 256-row class and the classic 256-row launch only exited
+        assert bench.prefill_plan(counts) == ("partitioned", 64)
+        assert classes["w13_bm192"] > 10 * classes["w13_mixed_stream"], classes
+        assert classes["w13_mixed_mfma"] > 10 * classes["w13_bm256"], classes
 
     tok = _sample_tokens(cfg, ids)
     experts, local = _local(ids[tok], cfg["E"])

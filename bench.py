@@ -638,8 +638,8 @@ def probes() -> int:
     """Chip figures the design relies on, from the library's probe kernels
     (include/fcmoe.h, fcmoe_probe_*): HBM streaming by launch shape (loads to
     VGPRs and LDS-DMA), the MFMA + LDS-fragment loop by wave tile and waves per
-    SIMD, MFMA waves beside streaming waves on one CU, and one agent-scope
-    release per workgroup. Best of 5 launches after 1 warmup (torch events on
+    SIMD, MFMA waves beside streaming waves on one CU, one agent-scope
+    release per workgroup, and the prefill GEMM's weight + A-row load mix. Best of 5 launches after 1 warmup (torch events on
     the launch stream)."""
     import torch
 
@@ -701,6 +701,19 @@ def probes() -> int:
                                                  rows.data_ptr(), stream), before=counters.zero_)
         out["fence"].append({"workgroups": wgs, "waves": waves, "release_per_workgroup": bool(rel),
                              "bytes": 264 << 20, "us": round(ms * 1e3, 1)})
+    arows = torch.ones(16 << 20, dtype=torch.uint8, device=dev)
+    big = torch.ones(3 << 30, dtype=torch.uint8, device=dev)
+    out["ring"] = []
+    for wgs in (256, 96):
+        for la, na, bar in [(2, 0, 1), (2, 2, 1), (4, 2, 1), (6, 2, 1), (2, 2, 0)]:
+            nbytes = 3 << 30 if wgs == 256 else 1 << 30
+            ms = best_ms(lambda: L.fcmoe_probe_ring(big.data_ptr(), nbytes,
+                                                    arows.data_ptr(), wgs, la, na, bar, sink.data_ptr(), stream))
+            chunks = nbytes // (wgs * 8 * 4 * 1024)
+            wb, ab = wgs * chunks * 32768, wgs * chunks * 8 * na * 1024
+            out["ring"].append({"workgroups": wgs, "lookahead": la, "a_kib_per_chunk": 8 * na, "barrier": bool(bar),
+                                "us": round(ms * 1e3, 1), "weights_TBps": round(wb / ms / 1e9, 3),
+                                "GBps_per_cu": round((wb + ab) / ms / 1e6 / wgs, 1)})
     print(json.dumps({"probes": out}))
     return 0
 

@@ -84,6 +84,7 @@ SIGNATURES = {
     "fcmoe_probe_mfma": (_I, [_I, _I, _I, _I, _P, _P]),
     "fcmoe_probe_mix": (_I, [_P, _I64, _I, _I, _I, _I, _P, _P]),
     "fcmoe_probe_fence": (_I, [_P, _I64, _I, _I, _I, _P, _P, _P]),
+    "fcmoe_probe_ring": (_I, [_P, _I64, _P, _I, _I, _I, _I, _P, _P]),
     "fcmoe_stage_timing_enable": (_I, [_I]),
     "fcmoe_stage_timing_read": (_I, [_P, _P]),
 }

@@ -172,6 +172,53 @@ __global__ __launch_bounds__(1024) void probe_fence_kernel(const uint8_t* src, i
   }
 }
 
+// The prefill GEMM's load mix without its arithmetic: per K chunk every one
+// of the 8 waves issues 4 one-KiB weight loads (a contiguous HBM stream per
+// workgroup, nontemporal) and NA one-KiB loads of A rows (8 rows x 128
+// bytes, 7168-byte row stride, from a 2 MiB window per XCD that stays in its
+// L2), all by buffer_load ... lds into a 2-stage LDS ring. It keeps D chunks
+// of loads in flight: wait for chunk c, meet at a barrier (BAR), issue chunk
+// c + D.
+template <int D, int NA, int BAR>
+__global__ __launch_bounds__(512) void probe_ring_kernel(const uint8_t* src, const uint8_t* arows, int64_t chunks,
+                                                         int* sink) {
+#if __HIP_DEVICE_COMPILE__
+  constexpr int NB = 4;
+  constexpr int L = NB + NA;
+  __shared__ __attribute__((aligned(1024))) uint8_t ring[2 * 8 * L * 1024];
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(src + (int64_t)blockIdx.x * chunks * 8 * NB * 1024), (short)0, 0x7ffffff0, 0x00020000);
+  const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(arows + (int64_t)(blockIdx.x % 8) * (2 << 20)), (short)0, 2 << 20, 0x00020000);
+  const uint32_t boff = (uint32_t)(wave * NB * 1024 + lane * 16);
+  const uint32_t aoff = (uint32_t)((wave * NA * 8 + lane / 8) * 7168 + (lane % 8) * 16);
+  auto issue = [&](int64_t c) {
+    const int64_t cc = c < chunks ? c : chunks - 1;
+    probe_lds_ptr dst = (probe_lds_ptr)(ring + ((c & 1) * 8 * L + wave * L) * 1024);
+#pragma unroll
+    for (int u = 0; u < NB; ++u)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (probe_lds_ptr)((uint8_t __attribute__((address_space(3)))*)dst + u * 1024),
+                                               16, boff + u * 1024, (int)(cc * 8 * NB * 1024), 0, 2);
+#pragma unroll
+    for (int u = 0; u < NA; ++u)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (probe_lds_ptr)((uint8_t __attribute__((address_space(3)))*)dst + (NB + u) * 1024),
+                                               16, aoff + u * 8 * 7168, (int)((cc % 56) * 128), 0, 0);
+  };
+#pragma unroll
+  for (int c = 0; c < D; ++c) issue(c);
+  for (int64_t c = 0; c < chunks; ++c) {
+    constexpr int W = (D - 1) * L;
+    __builtin_amdgcn_s_waitcnt((W & 15) | ((W >> 4) << 14) | (7 << 4) | (15 << 8));
+    if (BAR) __builtin_amdgcn_s_barrier();
+    issue(c + D);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (ring[lane] == 0x5a && lane == kWave) sink[0] = 1;  // never true: keeps the loads
+#endif
+}
+
 template <int FM, int FN, int W>
 int launch_mfma(int workgroups, int iters, int* sink, hipStream_t stream) {
   hipLaunchKernelGGL((probe_mfma_kernel<FM, FN, W * kWave>), dim3(workgroups), dim3(W * kWave), 0, stream, iters, sink);
@@ -241,4 +288,24 @@ extern "C" int fcmoe_probe_fence(const void* src, int64_t src_bytes, int workgro
   hipLaunchKernelGGL(probe_fence_kernel, dim3(workgroups), dim3(waves * kWave), 0, stream, (const uint8_t*)src,
                      chunks, release, counters, (v4i*)rows);
   return check_launch("probe_fence");
+}
+
+extern "C" int fcmoe_probe_ring(const void* src, int64_t src_bytes, const void* arows, int workgroups, int lookahead,
+                                int a_loads, int barrier, int* sink, hipStream_t stream) {
+  if (!src || !arows || !sink || workgroups <= 0) return fail(FCMOE_EINVAL, "probe_ring: bad arguments");
+  // arows: at least 16 MiB (a 2 MiB window per XCD)
+  const int64_t chunks = src_bytes / ((int64_t)workgroups * 8 * 4 * 1024);
+  if (chunks < 8 || chunks * 8 * 4 * 1024 > 0x7ffffff0) return fail(FCMOE_EINVAL, "probe_ring: bad source size");
+  const dim3 g((unsigned)workgroups), b(512);
+  const uint8_t* s = (const uint8_t*)src;
+  const uint8_t* a = (const uint8_t*)arows;
+  switch (lookahead * 100 + a_loads * 10 + (barrier ? 1 : 0)) {
+    case 201: hipLaunchKernelGGL((probe_ring_kernel<2, 0, 1>), g, b, 0, stream, s, a, chunks, sink); break;
+    case 221: hipLaunchKernelGGL((probe_ring_kernel<2, 2, 1>), g, b, 0, stream, s, a, chunks, sink); break;
+    case 220: hipLaunchKernelGGL((probe_ring_kernel<2, 2, 0>), g, b, 0, stream, s, a, chunks, sink); break;
+    case 421: hipLaunchKernelGGL((probe_ring_kernel<4, 2, 1>), g, b, 0, stream, s, a, chunks, sink); break;
+    case 621: hipLaunchKernelGGL((probe_ring_kernel<6, 2, 1>), g, b, 0, stream, s, a, chunks, sink); break;
+    default: return fail(FCMOE_EINVAL, "probe_ring: unsupported lookahead / A loads / barrier");
+  }
+  return check_launch("probe_ring");
 }

@@ -249,7 +249,14 @@ int fcmoe_bf16_stage_views(const fcmoe_moe_args* args, int w8a16, const int32_t*
  *   1 KiB to `rows` ([workgroups x waves x 1 KiB]), issues an agent-scope
  *   release fence and the workgroup bumps counters[workgroup / 16] (zeroed
  *   by the caller); the 16th arrival of each group acquires and reads a
- *   neighbour's row. */
+ *   neighbour's row.
+ * _ring: the prefill GEMM's load mix without arithmetic: `workgroups`
+ *   workgroups of 8 waves; per K chunk each wave loads 4 KiB of weights (a
+ *   contiguous stream of src per workgroup) and a_loads KiB of A rows (8 rows
+ *   x 128 bytes, 7168-byte stride, from a 2 MiB window of `arows` per XCD;
+ *   arows >= 16 MiB) by buffer_load ... lds, keeping `lookahead` chunks in
+ *   flight, with (barrier != 0) one workgroup barrier per chunk. Supported
+ *   (lookahead, a_loads, barrier): (2,0,1), (2,2,1), (2,2,0), (4,2,1), (6,2,1). */
 int fcmoe_probe_stream(const void* src, int64_t src_bytes, int workgroups, int waves, int mode, int lds_pad_bytes,
                        int* sink, hipStream_t stream);
 int fcmoe_probe_mfma(int tile, int waves, int workgroups, int iters, int* sink, hipStream_t stream);
@@ -257,6 +264,8 @@ int fcmoe_probe_mix(const void* src, int64_t src_bytes, int compute_waves, int s
                     int stream_mfma, int* sink, hipStream_t stream);
 int fcmoe_probe_fence(const void* src, int64_t src_bytes, int workgroups, int waves, int release, int* counters,
                       void* rows, hipStream_t stream);
+int fcmoe_probe_ring(const void* src, int64_t src_bytes, const void* arows, int workgroups, int lookahead, int a_loads,
+                     int barrier, int* sink, hipStream_t stream);
 
 /* ---- stage timing ------------------------------------------------------ */
 

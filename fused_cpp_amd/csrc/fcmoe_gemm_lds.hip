@@ -70,6 +70,9 @@ __device__ __forceinline__ void wait_vmcnt() {
 // gm = 0 keeps plain tile-major order.
 constexpr int kXcds = 8;
 constexpr int kLdsGroupTiles = 4;
+// gm value of a persistent launch that deals whole row tiles to the XCDs
+// round-robin (see lds_work_item).
+constexpr int kLdsDealTiles = 1 << 20;
 
 // When the channel dimension does not fill the last channel block (W13 at
 // F = 2048 on the 4-wave 256-row tile: 21 blocks of 6 gate/up pairs and one
@@ -92,6 +95,21 @@ __device__ __forceinline__ bool lds_work_item(int b, int count, int n_blocks, bo
       return true;
     }
     lp = b - F;
+  } else if (gm == kLdsDealTiles) {
+    // Persistent launches only: row tile t goes to XCD t % 8 with all its
+    // full channel blocks, then each XCD's last-block items.
+    const int x = b % kXcds, k = b / kXcds;
+    const int tiles_x = count / kXcds + (x < count % kXcds ? 1 : 0);
+    if (k < tiles_x * nbf) {
+      tile_idx = x + kXcds * (k / nbf);
+      nb = k % nbf;
+      return true;
+    }
+    const int kp = k - tiles_x * nbf;
+    if (kp >= (partial ? tiles_x : 0)) return false;
+    tile_idx = x + kXcds * kp;
+    nb = n_blocks - 1;
+    return true;
   } else {
     const int x = b % kXcds, k = b / kXcds;
     const int qf = F / kXcds, rf = F % kXcds, qp = P / kXcds, rp = P % kXcds;
@@ -336,6 +354,7 @@ __device__ __forceinline__ void lds_gemm_body(const GemmParams& p, int n_blocks,
     if (!PERSIST || !p.part_counts || (int)blockIdx.x >= part_wgs(p.part_counts)) return;
     part = true;
   }
+  if (part && gm == kLdsDealTiles) gm = kLdsGroupTiles;  // the partitioned plan keeps XCD windows
   const int32_t* const tiles0 = part ? p.part_tiles : p.tiles;
   int32_t* const queue = part ? p.part_queue : p.queue;
   const int u_n = part ? 0 : p.u_n;
@@ -367,6 +386,10 @@ __device__ __forceinline__ void lds_gemm_body(const GemmParams& p, int n_blocks,
     const int nbf = partial ? n_blocks - 1 : n_blocks;
     const int F = count * nbf, P = partial ? count : 0;
     xcd_items = F / kXcds + (xcd < F % kXcds ? 1 : 0) + P / kXcds + (xcd < P % kXcds ? 1 : 0);
+    if (gm == kLdsDealTiles) {
+      const int tiles_x = count / kXcds + (xcd < count % kXcds ? 1 : 0);
+      xcd_items = tiles_x * (nbf + (partial ? 1 : 0));
+    }
     if (gm <= 0) xcd_items = grid_items;  // plain order: slots are not XCD-local
   }
   auto fetch_k = [&](int k_static) -> int {
@@ -746,10 +769,18 @@ int launch_lds_cfg(const GemmParams& p, int64_t max_tiles, hipStream_t stream) {
     const char* v = getenv("FCMOE_LDS_GROUP");
     return v ? atoi(v) : kLdsGroupTiles;
   }();
+  // The mixed plan's W13 launch deals whole row tiles to the XCDs
+  // round-robin (kLdsDealTiles) instead of contiguous ranges: its item space
+  // runs from full 256-row tiles down to the cheaper partial and 128-row
+  // ones, and contiguous ranges left the XCDs holding the cheap end idle
+  // while others still ran (C3 W13 1.19 -> 1.16 ms alone, layer 2.89 ->
+  // 2.86 ms; T = 8192 5.00 -> 4.78 ms). W2 (28 channel blocks per tile) and
+  // the partitioned plan's launch measured no better that way.
+  const int gm_launch = PERSIST && epi_pair(EPI) && p.u_n > 0 ? kLdsDealTiles : gm;
   if constexpr (PERSIST)
     hipLaunchKernelGGL((grouped_gemm_lds_persist_kernel<I8, EPI, FM, FN, SA, SB, BPOL, AW, WMW, WNW>),
-                       dim3((unsigned)grid), dim3(WMW * WNW * kWave), 0, stream, p, (int)n_blocks, partial, gm,
-                       (int)items);
+                       dim3((unsigned)grid), dim3(WMW * WNW * kWave), 0, stream, p, (int)n_blocks, partial,
+                       gm_launch, (int)items);
   else
     hipLaunchKernelGGL((grouped_gemm_lds_kernel<I8, EPI, FM, FN, SA, SB, BPOL, AW, WMW, WNW>), dim3((unsigned)grid),
                        dim3(WMW * WNW * kWave), 0, stream, p, (int)n_blocks, partial, gm, (int)items);

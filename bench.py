@@ -195,22 +195,16 @@ def class_of(c: int, decode: bool, kind: str = "w8a8") -> int:
 
 
 def prefill_plan(counts) -> tuple[str, int]:
-    """Host mirror of the device's W8A8 prefill launch-plan choice
-    (fcmoe_api.hip run_w8a8_stage, fcmoe_internal.h part_wgs): "mixed" when
-    there are >= 32 tiles of 16 rows and >= 16 of 256 rows; otherwise
-    "partitioned" (the 256-row class on its own persistent launch over
-    `wgs` CUs) or "classic". Tile counts: one tile per expert of 1-192 rows,
-    ceil(rows / 256) for larger experts."""
+    """The W8A8 prefill launch plan the device picks for these expert row
+    counts ("mixed", "classic" or "partitioned" with its CUs for the 256-row
+    class), from the library's own rule (fcmoe_w8a8_prefill_plan). Tile
+    counts: one tile per expert of 1-192 rows, ceil(rows / 256) above."""
+    from fused_cpp_amd import cabi
+
     counts = np.asarray(counts)
     t = [int(((counts > 0) & (counts <= 16)).sum()), int(((counts > 16) & (counts <= 128)).sum()),
          int(((counts > 128) & (counts <= 192)).sum()), int(np.ceil(counts[counts > 192] / 256).sum())]
-    if t[0] >= 32 and t[3] >= 16:
-        return "mixed", 0
-    t3, ts = 20 * t[3], 8 * (t[1] + t[2]) + t[0]
-    if t3 == 0:
-        return "classic", 0
-    w = 256 * t3 // (t3 + ts) // 8 * 8
-    return ("classic", 0) if w > 128 else ("partitioned", max(w, 32))
+    return cabi.w8a8_prefill_plan(t)
 
 
 def algorithmic(cfg, counts):

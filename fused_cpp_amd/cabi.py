@@ -87,6 +87,7 @@ SIGNATURES = {
     "fcmoe_probe_ring": (_I, [_P, _I64, _P, _I, _I, _I, _I, _P, _P]),
     "fcmoe_stage_timing_enable": (_I, [_I]),
     "fcmoe_stage_timing_read": (_I, [_P, _P]),
+    "fcmoe_w8a8_prefill_plan": (_I, [_P, _P]),
 }
 
 FCMOE_STAGE_COUNT = 24
@@ -139,3 +140,14 @@ def stream_handle() -> int:
     import torch
 
     return torch.cuda.current_stream().cuda_stream
+
+
+def w8a8_prefill_plan(class_tiles) -> tuple[str, int]:
+    """The W8A8 prefill launch plan the device picks for these per-class tile
+    counts (16 / 128 / 192 / 256 rows): ("classic" | "mixed" | "partitioned",
+    CUs of the partitioned 256-row class)."""
+    tiles = (ctypes.c_int32 * 4)(*[int(t) for t in class_tiles])
+    wgs = ctypes.c_int(0)
+    rc = lib().fcmoe_w8a8_prefill_plan(ctypes.cast(tiles, ctypes.c_void_p), ctypes.byref(wgs))
+    check(rc if rc < 0 else 0, "w8a8_prefill_plan")
+    return ("classic", "mixed", "partitioned")[rc], wgs.value

@@ -1008,6 +1008,15 @@ extern "C" int fcmoe_stage_timing_enable(int enable) {
   return FCMOE_OK;
 }
 
+extern "C" int fcmoe_w8a8_prefill_plan(const int32_t* class_tiles, int* part_wgs_out) {
+  if (!class_tiles) return fail(FCMOE_EINVAL, "class_tiles is NULL");
+  const int min_tiles = mixed_min_tiles();
+  const bool mixed = class_tiles[0] >= min_tiles && (min_tiles <= 0 || class_tiles[3] >= kPrefillMixedMinBigTiles);
+  const int w = !mixed && min_tiles > 0 && part_enabled() ? part_wgs(class_tiles) : 0;
+  if (part_wgs_out) *part_wgs_out = w;
+  return mixed ? 1 : (w > 0 ? 2 : 0);
+}
+
 extern "C" int fcmoe_stage_timing_read(double* total_ms, int64_t* launches) {
   StageTimer& t = timer();
   std::lock_guard<std::mutex> g(t.mu);

@@ -267,6 +267,16 @@ int fcmoe_probe_fence(const void* src, int64_t src_bytes, int workgroups, int wa
 int fcmoe_probe_ring(const void* src, int64_t src_bytes, const void* arows, int workgroups, int lookahead, int a_loads,
                      int barrier, int* sink, hipStream_t stream);
 
+/* W8A8 prefill launch plan for the route scan's tile counts per class
+ * (class_tiles[0..3]: tiles of 16 / 128 / 192 / 256 rows), as the device
+ * chooses it inside fcmoe_w8a8_forward (same environment overrides): returns
+ * 0 = classic (one launch per class), 1 = mixed (persistent MFMA launch
+ * beside the 16-row streaming launch), 2 = partitioned classic (the 256-row
+ * class on *part_wgs_out CUs); a negative FCMOE_E* code on bad arguments.
+ * No reference counterpart (the reference's CPU planner makes no such
+ * choice); for benchmarks and tests that attribute stage times. */
+int fcmoe_w8a8_prefill_plan(const int32_t* class_tiles, int* part_wgs_out);
+
 /* ---- stage timing ------------------------------------------------------ */
 
 /* Stage ids for fcmoe_stage_timing_read. W13 / W2 class stages are per tile

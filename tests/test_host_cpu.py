@@ -298,3 +298,30 @@ def test_noalloc_rejects_calls_beyond_its_scratch():
     assert "scratch" in L.fcmoe_last_error().decode()
     a.tokens = 64  # C2's decode batch fits the array
     assert L.fcmoe_w8a8_workspace_bytes(ctypes.byref(a)) <= cabi.FCMOE_NOALLOC_SCRATCH_BYTES
+
+
+def test_w8a8_prefill_plan_choice(monkeypatch):
+    """The library's prefill launch-plan rule on the route scan's per-class
+    tile counts (host side; the device evaluates the same inline function):
+    mixed with >= 32 tiles of 16 rows and >= 16 of 256 rows, otherwise the
+    classic plan, partitioned when the 256-row class is a minority of the
+    weighted work (2.5 x a 128/192-row tile, 20 x a 16-row tile), on
+    [32, 128] CUs rounded down to the 8 XCDs."""
+    from fused_cpp_amd import cabi
+
+    monkeypatch.delenv("FCMOE_PREFILL_MIXED_MIN_TILES", raising=False)
+    monkeypatch.delenv("FCMOE_PREFILL_PART", raising=False)
+    assert cabi.w8a8_prefill_plan([149, 20, 15, 140]) == ("mixed", 0)  # C3-like
+    assert cabi.w8a8_prefill_plan([31, 0, 0, 140])[0] != "mixed"
+    assert cabi.w8a8_prefill_plan([149, 20, 15, 15])[0] != "mixed"
+    # C4: 364 experts of 129-192 rows, 52 tiles of 256 rows: 256 * 1040 / 3952 = 67 -> 64
+    assert cabi.w8a8_prefill_plan([0, 0, 364, 52]) == ("partitioned", 64)
+    assert cabi.w8a8_prefill_plan([0, 256, 0, 8]) == ("partitioned", 32)  # clamped up to 32
+    assert cabi.w8a8_prefill_plan([0, 0, 0, 288]) == ("classic", 0)  # the 256-row class dominates
+    assert cabi.w8a8_prefill_plan([5, 10, 0, 0]) == ("classic", 0)  # no 256-row tiles
+    monkeypatch.setenv("FCMOE_PREFILL_PART", "0")
+    assert cabi.w8a8_prefill_plan([0, 0, 364, 52]) == ("classic", 0)
+    monkeypatch.setenv("FCMOE_PREFILL_MIXED_MIN_TILES", "0")
+    assert cabi.w8a8_prefill_plan([0, 0, 364, 52]) == ("mixed", 0)
+    with pytest.raises(RuntimeError):
+        cabi.check(cabi.lib().fcmoe_w8a8_prefill_plan(None, None), "plan")

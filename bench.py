@@ -179,7 +179,7 @@ def expert_counts(cfg, ids):
 
 
 CLASS_BM_PREFILL = (16, 128, 192, 256)  # W8A8 / BF16 prefill tile classes
-CLASS_BM_W8 = (16, 32, 128, 256)  # W8A16 tile classes
+CLASS_BM_W8 = (16, 32, 128, 192, 256)  # W8A16 tile classes
 
 
 def class_of(c: int, decode: bool, kind: str = "w8a8") -> int:

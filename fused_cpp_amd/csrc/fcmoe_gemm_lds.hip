@@ -831,19 +831,22 @@ int launch_lds_bm(int bm, const GemmParams& p, int64_t max_tiles, hipStream_t st
 // W8A16 prefill tiles. The int8 -> bf16 widening is VALU work on the MFMAs'
 // SIMD, done once per chunk and weight tile, so each wave covers 8 row
 // fragments against 4 tiles (two bf16 MFMAs per pair per chunk): the 128-row
-// tile runs 1 x 8 waves, the 256-row tile 2 x 4. As in the int8 classes, the
-// 128-row weights stream nontemporal and the 256-row ones stay cached (their
-// experts' row tiles re-read them).
+// tile runs 1 x 8 waves, the 256-row tile 2 x 4, the 192-row tile 2 x 4 waves
+// of 6 row fragments. As in the int8 classes, the 128/192-row weights stream
+// nontemporal (one row tile per expert) and the 256-row ones stay cached
+// (their experts' row tiles re-read them).
 template <int EPI>
 int launch_lds_w8(int bm, const GemmParams& p, int64_t max_tiles, hipStream_t stream) {
   constexpr int kNT = 2;
   switch (bm) {
     case 128:
       return launch_lds_cfg<false, EPI, 8, 4, 2, 3, kNT, 128, 1, 8>(p, max_tiles, stream);
+    case 192:
+      return launch_lds_cfg<false, EPI, 6, 4, 2, 3, kNT, 128, 2, 4>(p, max_tiles, stream);
     case 256:
       return launch_lds_cfg<false, EPI, 8, 4, 2, 3, 0, 128, 2, 4>(p, max_tiles, stream);
     default:
-      return fail(FCMOE_EINVAL, "W8A16 LDS tiles are 128 or 256 rows");
+      return fail(FCMOE_EINVAL, "W8A16 LDS tiles are 128, 192 or 256 rows");
   }
 }
 

@@ -62,11 +62,13 @@ def test_w8a16_matches_dequantised_fp32_reference(gpu, oracle_lib, activation, l
 
 
 @pytest.mark.parametrize("activation", ["silu", "gelu"])
-@pytest.mark.parametrize("T,Hd,F,E,k", [(200, 256, 128, 4, 2), (700, 200, 96, 4, 2), (900, 320, 160, 14, 2)])
+@pytest.mark.parametrize("T,Hd,F,E,k", [(200, 256, 128, 4, 2), (700, 200, 96, 4, 2), (900, 320, 160, 14, 2),
+                                         (640, 256, 128, 8, 2)])
 def test_w8a16_prefill_classes(gpu, oracle_lib, activation, T, Hd, F, E, k):
     """Prefill-sized experts on the LDS-staged W8A16 tiles: ~100 rows per
-    expert (128-row class), ~350 (two 256-row tiles per expert), and a mix of
-    classes with unaligned H (zero-padded K) and a single-chunk W2."""
+    expert (128-row class), ~350 (two 256-row tiles per expert), a mix of
+    classes with unaligned H (zero-padded K) and a single-chunk W2, and ~160
+    rows per expert (192-row class)."""
     from fused_cpp_amd import moe
 
     x, _, _, q13, s13, q2, s2, ids, w, deq13, deq2 = _case(oracle_lib, T + 3 * Hd, T, Hd, F, E, k)

@@ -660,6 +660,9 @@ __device__ __forceinline__ void lds_gemm_body(const GemmParams& p, int n_blocks,
         af[(i + 1) % 2][0] = *(const v4i*)(sta + (i + 1) * A_FRAG);
         af[(i + 1) % 2][1] = *(const v4i*)(sta + (i + 1) * A_FRAG + a_dhi);
       }
+      // row fragments past the expert's rows skip their MFMAs (an expert
+      // of 33-64 rows fills half of the 128-row tile)
+      if (i >= live_frags) continue;
 #pragma unroll
       for (int j = 0; j < FN; ++j) {
         acc[i][j] = mfma(__builtin_bit_cast(v8bf, af[i % 2][0]), __builtin_bit_cast(v8bf, bl[j]), acc[i][j]);

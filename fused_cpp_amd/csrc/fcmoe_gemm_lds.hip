@@ -83,6 +83,20 @@ constexpr int kLdsDealTiles = 1 << 20;
 // takes its share of the full items, in the order above, then its share of
 // the last-block items; the grid carries kXcds spare workgroups for the two
 // shares' rounding.
+// Row tiles dealt to XCD x (gm == kLdsDealTiles): units of kDealUnit
+// consecutive tiles, unit u to XCD u % 8; the last unit may be short. Two
+// tiles per unit let an XCD's L2 serve one expert's weights to both (C3:
+// 3.88 GB of L2-miss traffic per W13 launch against 5.16 GB with single
+// tiles, 2.77 against 2.82 ms per layer; 3 or 4 tiles per unit: 2.84 / 2.83).
+constexpr int kDealUnit = 2;
+__device__ __forceinline__ int deal_tiles(int count, int x) {
+  constexpr int D = kDealUnit;
+  const int U = (count + D - 1) / D;
+  const int units_x = U / kXcds + (x < U % kXcds ? 1 : 0);
+  const bool has_last = units_x > 0 && x + kXcds * (units_x - 1) == U - 1;
+  return units_x * D - (has_last ? U * D - count : 0);
+}
+
 __device__ __forceinline__ bool lds_work_item(int b, int count, int n_blocks, bool partial, int gm, int& tile_idx,
                                               int& nb) {
   const int nbf = partial ? n_blocks - 1 : n_blocks;  // full channel blocks per row tile
@@ -96,18 +110,25 @@ __device__ __forceinline__ bool lds_work_item(int b, int count, int n_blocks, bo
     }
     lp = b - F;
   } else if (gm == kLdsDealTiles) {
-    // Persistent launches only: row tile t goes to XCD t % 8 with all its
-    // full channel blocks, then each XCD's last-block items.
+    // Persistent launches only: units of kDealUnit consecutive row tiles
+    // (one expert's, mostly) go to the XCDs round-robin, unit u to XCD u % 8,
+    // with all their full channel blocks (row tiles fastest), then each XCD's
+    // last-block items.
     const int x = b % kXcds, k = b / kXcds;
-    const int tiles_x = count / kXcds + (x < count % kXcds ? 1 : 0);
+    const int tiles_x = deal_tiles(count, x);
     if (k < tiles_x * nbf) {
-      tile_idx = x + kXcds * (k / nbf);
-      nb = k % nbf;
+      constexpr int D = kDealUnit;
+      const int U = (count + D - 1) / D;
+      const int m = k / (D * nbf), idx = k % (D * nbf);
+      const int u = x + kXcds * m;
+      const int dm = u == U - 1 ? count - (U - 1) * D : D;
+      tile_idx = u * D + idx % dm;
+      nb = idx / dm;
       return true;
     }
     const int kp = k - tiles_x * nbf;
     if (kp >= (partial ? tiles_x : 0)) return false;
-    tile_idx = x + kXcds * kp;
+    tile_idx = (x + kXcds * (kp / kDealUnit)) * kDealUnit + kp % kDealUnit;
     nb = n_blocks - 1;
     return true;
   } else {
@@ -386,10 +407,7 @@ __device__ __forceinline__ void lds_gemm_body(const GemmParams& p, int n_blocks,
     const int nbf = partial ? n_blocks - 1 : n_blocks;
     const int F = count * nbf, P = partial ? count : 0;
     xcd_items = F / kXcds + (xcd < F % kXcds ? 1 : 0) + P / kXcds + (xcd < P % kXcds ? 1 : 0);
-    if (gm == kLdsDealTiles) {
-      const int tiles_x = count / kXcds + (xcd < count % kXcds ? 1 : 0);
-      xcd_items = tiles_x * (nbf + (partial ? 1 : 0));
-    }
+    if (gm == kLdsDealTiles) xcd_items = deal_tiles(count, xcd) * (nbf + (partial ? 1 : 0));
     if (gm <= 0) xcd_items = grid_items;  // plain order: slots are not XCD-local
   }
   auto fetch_k = [&](int k_static) -> int {
@@ -772,14 +790,13 @@ int launch_lds_cfg(const GemmParams& p, int64_t max_tiles, hipStream_t stream) {
     const char* v = getenv("FCMOE_LDS_GROUP");
     return v ? atoi(v) : kLdsGroupTiles;
   }();
-  // The mixed plan's W13 launch deals whole row tiles to the XCDs
-  // round-robin (kLdsDealTiles) instead of contiguous ranges: its item space
-  // runs from full 256-row tiles down to the cheaper partial and 128-row
-  // ones, and contiguous ranges left the XCDs holding the cheap end idle
-  // while others still ran (C3 W13 1.19 -> 1.16 ms alone, layer 2.89 ->
-  // 2.86 ms; T = 8192 5.00 -> 4.78 ms). W2 (28 channel blocks per tile) and
-  // the partitioned plan's launch measured no better that way.
-  const int gm_launch = PERSIST && epi_pair(EPI) && p.u_n > 0 ? kLdsDealTiles : gm;
+  // The mixed plan's launches deal row tiles to the XCDs round-robin
+  // (kLdsDealTiles) instead of contiguous ranges: their item space runs from
+  // full 256-row tiles down to the cheaper partial and 128-row ones, and
+  // contiguous ranges left the XCDs holding the cheap end idle while others
+  // still ran (C3 2.89 -> 2.77 ms per layer, T = 8192 5.00 -> 4.67 ms). The
+  // partitioned plan's launch keeps the 4-tile windows (no better dealt).
+  const int gm_launch = PERSIST && p.u_n > 0 ? kLdsDealTiles : gm;
   if constexpr (PERSIST)
     hipLaunchKernelGGL((grouped_gemm_lds_persist_kernel<I8, EPI, FM, FN, SA, SB, BPOL, AW, WMW, WNW>),
                        dim3((unsigned)grid), dim3(WMW * WNW * kWave), 0, stream, p, (int)n_blocks, partial,

@@ -110,13 +110,15 @@ def test_router_and_i8gemm_graph_replays(gpu):
     _replay_matches_eager(fn, make, static)
 
 
-@pytest.mark.parametrize("min_tiles", ["32", "0"])
+@pytest.mark.parametrize("min_tiles", ["32", "0", "1000000"])
 def test_w8a8_prefill_mixed_plan_graph_replays(gpu, min_tiles):
     """Skewed prefill routing where the device picks the mixed launch plan
     (persistent MFMA launch beside the 16-row streaming launch, forked streams,
     per-XCD work queues zeroed by the route launch): "32" (the default) enqueues
     both plans (the classic launches exit on the device), "0" forces the mixed
-    plan alone."""
+    plan alone, "1000000" the classic plan, here partitioned (the persistent
+    launch runs the 256-row class on part of the CUs beside the classic
+    launches of the other classes)."""
     import os
 
     from fused_cpp_amd import moe
@@ -131,6 +133,21 @@ def test_w8a8_prefill_mixed_plan_graph_replays(gpu, min_tiles):
     # the mixed plan's default trigger: >= 32 tiles of <= 16 rows, >= 16 tiles of 256 rows
     assert ((counts > 0) & (counts <= 16)).sum() >= 32, counts
     assert sum((int(c) + 255) // 256 for c in counts if c > 192) + (T + 255) // 256 >= 16, counts
+    if min_tiles == "1000000":
+        from fused_cpp_amd import cabi
+
+        allc = np.append(counts, T)  # the shared expert takes every token
+        tiles = [int(((allc > 0) & (allc <= 16)).sum()), int(((allc > 16) & (allc <= 128)).sum()),
+                 int(((allc > 128) & (allc <= 192)).sum()), int(sum((int(c) + 255) // 256 for c in allc if c > 192))]
+        saved = os.environ.get("FCMOE_PREFILL_MIXED_MIN_TILES")
+        os.environ["FCMOE_PREFILL_MIXED_MIN_TILES"] = min_tiles
+        try:
+            assert cabi.w8a8_prefill_plan(tiles)[0] == "partitioned", tiles
+        finally:
+            if saved is None:
+                del os.environ["FCMOE_PREFILL_MIXED_MIN_TILES"]
+            else:
+                os.environ["FCMOE_PREFILL_MIXED_MIN_TILES"] = saved
     rng = np.random.default_rng(1)
 
     def make(r):

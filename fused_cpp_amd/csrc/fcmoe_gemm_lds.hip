@@ -197,6 +197,7 @@ __device__ __forceinline__ void staged_epilogue(const GemmParams& p, const v4i (
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
       const int rbase = row_base + i * 16;
+      if (rbase >= rows) break;  // fragments past the expert's rows (wave-uniform)
       // Batches of QB registers x HP tiles: every table lookup of a batch is
       // issued before the first is used and the batch's 16-lane maxima run
       // side by side (one lookup and max at a time, each waited out alone,
@@ -281,6 +282,7 @@ __device__ __forceinline__ void staged_epilogue(const GemmParams& p, const v4i (
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
       const int rbase = row_base + i * 16;
+      if (rbase >= rows) break;  // fragments past the expert's rows (wave-uniform)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int r = rbase + rq + q;

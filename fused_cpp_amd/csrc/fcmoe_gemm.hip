@@ -341,6 +341,10 @@ int launch_bm(int bm, const GemmParams& p, int64_t max_tiles, hipStream_t stream
       // (144 workgroups) or doubled up at T=2 (272 workgroups, W13
       // 0.108 -> 0.083 ms with one-wave workgroups; T=8 0.243 -> 0.233 ms).
       // At C2 (T=64) the 8-wave form is faster (0.929 vs 0.944 ms).
+      // W2 (K = 2048: 32 chunks per tile) keeps 11 chunks in flight per wave
+      // instead of 7: C2 W2 0.504 -> 0.487 ms, T=8 0.117 -> 0.113 ms, T=1
+      // 25.2 -> 24.4 us. W13 gains nothing from it (T=2 0.080 -> 0.086 ms
+      // with one-wave workgroups) and keeps the 8-deep ring.
       if (p.stream_role) {
         if constexpr (epi_pair(EPI))
           return launch_cfg<I8, EPI, 1, 4, 1, 2, 2, true, true>(p, max_tiles, stream);
@@ -351,12 +355,12 @@ int launch_bm(int bm, const GemmParams& p, int64_t max_tiles, hipStream_t stream
         if constexpr (epi_pair(EPI))
           return launch_cfg<I8, EPI, 1, 1, 1, 2, 8, true>(p, max_tiles, stream);
         else
-          return launch_cfg<I8, EPI, 1, 1, 1, 1, 8, true>(p, max_tiles, stream);
+          return launch_cfg<I8, EPI, 1, 1, 1, 1, 12, true>(p, max_tiles, stream);
       }
       if constexpr (epi_pair(EPI))
         return launch_cfg<I8, EPI, 1, 8, 1, 2, 8, true>(p, max_tiles, stream);
       else
-        return launch_cfg<I8, EPI, 1, 8, 1, 1, 8, true>(p, max_tiles, stream);
+        return launch_cfg<I8, EPI, 1, 8, 1, 1, 12, true>(p, max_tiles, stream);
     case 32:
       return launch_cfg<I8, EPI, 1, 4, 2, 4, 4, true>(p, max_tiles, stream);
     case 64:

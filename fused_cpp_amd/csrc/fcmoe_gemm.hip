@@ -382,14 +382,15 @@ template <int EPI>
 int launch_bm_w8(int bm, const GemmParams& p, int64_t max_tiles, hipStream_t stream) {
   switch (bm) {
     case 16:
-      // W13 runs 8 waves of one gate+up pair with a 4-deep ring (C1 shape:
-      // 0.754 -> 0.747 ms against 4 waves of 2+2 tiles). W2 keeps 4 waves of
-      // 2 tiles: the int8 -> bf16 widening makes the one-tile-per-wave form
-      // slower (0.404 vs 0.445 ms).
+      // W13 runs 8 waves of one gate+up pair with a 6-deep ring (C1 shape:
+      // 0.754 -> 0.747 ms against 4 waves of 2+2 tiles; ring depth 4 / 6 / 8:
+      // 0.707 / 0.699 / 0.714 ms on a later box). W2 keeps 4 waves of 2
+      // tiles: the int8 -> bf16 widening makes the one-tile-per-wave form
+      // slower (0.404 vs 0.445 ms); a 12-deep ring against 8: 0.385 vs 0.396.
       if constexpr (epi_pair(EPI))
-        return launch_cfg<false, EPI, 1, 8, 1, 2, 4, true>(p, max_tiles, stream);
+        return launch_cfg<false, EPI, 1, 8, 1, 2, 6, true>(p, max_tiles, stream);
       else
-        return launch_cfg<false, EPI, 1, 4, 1, 2, 8, true>(p, max_tiles, stream);
+        return launch_cfg<false, EPI, 1, 4, 1, 2, 12, true>(p, max_tiles, stream);
     case 32:
       return launch_cfg<false, EPI, 1, 4, 2, 4, 4, true>(p, max_tiles, stream);
     default:

@@ -345,11 +345,14 @@ int launch_bm(int bm, const GemmParams& p, int64_t max_tiles, hipStream_t stream
       // instead of 7: C2 W2 0.504 -> 0.487 ms, T=8 0.117 -> 0.113 ms, T=1
       // 25.2 -> 24.4 us. W13 gains nothing from it (T=2 0.080 -> 0.086 ms
       // with one-wave workgroups) and keeps the 8-deep ring.
+      // The mixed plan's streaming launches (at most 80 VGPRs): the deepest
+      // rings that fit, 2 for W13 (2 tiles a wave), 5 for W2 (C3 W2 alone
+      // 0.492 -> 0.466 ms against 4, layer 2.78 -> 2.75 ms).
       if (p.stream_role) {
         if constexpr (epi_pair(EPI))
           return launch_cfg<I8, EPI, 1, 4, 1, 2, 2, true, true>(p, max_tiles, stream);
         else
-          return launch_cfg<I8, EPI, 1, 4, 1, 1, 4, true, true>(p, max_tiles, stream);
+          return launch_cfg<I8, EPI, 1, 4, 1, 1, 5, true, true>(p, max_tiles, stream);
       }
       if (max_tiles <= kDecodeFewTiles) {
         if constexpr (epi_pair(EPI))

@@ -59,6 +59,7 @@ __device__ __forceinline__ float tree_merge(const float* route_out, const float*
 // a multiply. Tokens run grid-stride over y.
 constexpr int kSlotBatch = 16;
 typedef float v4f __attribute__((ext_vector_type(4)));
+typedef uint32_t v2u __attribute__((ext_vector_type(2)));
 
 template <int VW>
 __global__ __launch_bounds__(256) void combine_kernel(const float* route_out, const float* route_weight,
@@ -129,7 +130,9 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* route_out, co
   if constexpr (VW == 4) {
     const uint32_t lo = (uint32_t)f32_to_bf16(acc[0]) | ((uint32_t)f32_to_bf16(acc[1]) << 16);
     const uint32_t hi = (uint32_t)f32_to_bf16(acc[2]) | ((uint32_t)f32_to_bf16(acc[3]) << 16);
-    *(uint2*)(out + t * hidden + h0) = make_uint2(lo, hi);
+    // nontemporal: the caller reads the output later, after other work
+    // (C4 combine 0.368 -> 0.348 ms)
+    __builtin_nontemporal_store((v2u){lo, hi}, (v2u*)(out + t * hidden + h0));
   } else {
     out[t * hidden + h0] = f32_to_bf16(acc[0]);
   }

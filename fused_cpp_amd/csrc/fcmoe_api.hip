@@ -493,22 +493,34 @@ int run_w8a8_stage(const TileClasses& tc, const RouteBuffers& rb, int epi, const
     }
     // Every launch of both plans under one fork: the mixed plan's MFMA launch
     // on the caller's stream (first, so its workgroups hold every CU before
-    // the streaming ones arrive), its 16-row launch and the classic classes
-    // (largest first) on side streams; the plan not taken exits at once,
-    // beside the one that runs.
+    // the streaming ones arrive), the rest on three side streams; the plan
+    // not taken exits at once, beside the one that runs. The device has 4
+    // hardware queues, so launches are paired on streams such that at most
+    // one of a pair has much work under either plan: the 16-row streaming
+    // launch, then the classic 16-row class (the mixed plan runs the first,
+    // the classic plan the second); the classic 256-row class (it exits when
+    // the persistent launch takes it), then the 128-row class; the 192-row
+    // class alone. (With a stream per launch, C4's 128-row launch queued
+    // behind the 192-row one on a shared hardware queue.)
     SideStreams* ss = nullptr;
     if ((rc = side_streams(&ss))) return rc;
     if (hipEventRecord(ss->fork, stream) != hipSuccess) return fail(FCMOE_EDEVICE, "hipEventRecord failed");
     if ((rc = gemm_launch(epi, 256, pm, big_bound, stream))) return rc;
-    const int nk = gate.plan_min <= 0 ? 0 : tc.n;  // forced mixed plan: no classic launches
-    for (int k = 0; k <= nk; ++k) {
+    const bool with_classic = gate.plan_min > 0;  // forced mixed plan: no classic launches
+    constexpr int kSides = 3;
+    for (int k = 0; k < kSides; ++k) {
       hipStream_t s = ss->s[k];
       if (hipStreamWaitEvent(s, ss->fork, 0) != hipSuccess) return fail(FCMOE_EDEVICE, "stream wait failed");
-      rc = k == 0 ? gemm_launch(epi, 16, ps, tc.bound[0], s) : classic(tc.n - k, s);
-      if (rc) return rc;
+      if (k == 0) {
+        if ((rc = gemm_launch(epi, 16, ps, tc.bound[0], s))) return rc;
+        if (with_classic && (rc = classic(0, s))) return rc;
+      } else if (with_classic) {
+        if ((rc = classic(k == 1 ? 3 : 2, s))) return rc;
+        if (k == 1 && (rc = classic(1, s))) return rc;
+      }
       if (hipEventRecord(ss->join[k], s) != hipSuccess) return fail(FCMOE_EDEVICE, "hipEventRecord failed");
     }
-    for (int k = 0; k <= nk; ++k)
+    for (int k = 0; k < kSides; ++k)
       if (hipStreamWaitEvent(stream, ss->join[k], 0) != hipSuccess) return fail(FCMOE_EDEVICE, "stream wait failed");
     return FCMOE_OK;
   }

@@ -30,7 +30,7 @@ CSRC = PKG / "csrc"
 ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 ARCH = os.environ.get("FCMOE_OFFLOAD_ARCH", "gfx950")
 
-HIP_SOURCES = ["fcmoe_api.hip", "fcmoe_route.hip", "fcmoe_quant.hip", "fcmoe_gemm.hip", "fcmoe_gemm_lds.hip", "fcmoe_combine.hip", "fcmoe_router.hip", "fcmoe_probe.hip"]
+HIP_SOURCES = ["fcmoe_api.hip", "fcmoe_route.hip", "fcmoe_quant.hip", "fcmoe_gemm.hip", "fcmoe_gemm_lds.hip", "fcmoe_combine.hip", "fcmoe_decode_tail.hip", "fcmoe_router.hip", "fcmoe_probe.hip"]
 HIP_FLAGS = [
     f"--offload-arch={ARCH}",
     "-O3",

@@ -423,6 +423,17 @@ bool part_enabled() {
   return !(v && v[0] == '0');
 }
 
+// Decode batches of at most this many tokens (FCMOE_DECODE_TAIL_MAX_T; 0
+// turns the fused tail off) run requant, W2 and the merge as one launch. At
+// one token it saves two launches (C2 shape: 0.082 -> 0.077 ms); at two the
+// tokens' workgroups each stream the shared expert's weights, and it is
+// slower (0.133 -> 0.136 ms).
+constexpr int kDecodeTailMaxTokens = 1;
+int decode_tail_max_tokens() {
+  const char* v = getenv("FCMOE_DECODE_TAIL_MAX_T");
+  return v && v[0] ? atoi(v) : kDecodeTailMaxTokens;
+}
+
 // One W8A8 GEMM stage (epilogue epi, stage-timing base id stage0) over the
 // prefill class set {16, 128, 192, 256}, or over any other class set with the
 // classic launches only.
@@ -592,6 +603,36 @@ int w8a8_run(const fcmoe_moe_args* a, char* ws_base, size_t ws_bytes, bool seria
   rc = run_w8a8_stage(L.tc, L.rb, kEpiW13SwigluI8, g13, FCMOE_STAGE_W13_CLASS0, FCMOE_STAGE_W13_MIXED_MFMA,
                       serial_classes, stream);
   if (rc) return rc;
+  const int64_t parts = ceil_div(I, 16);
+  if (a->tokens <= decode_tail_max_tokens() && L.kt <= kDecodeTailSlots && parts <= 128) {
+    // requant + W2 + merge in one launch (timed as the W2 16-row stage)
+    DecodeTailArgs d{};
+    d.tokens = a->tokens;
+    d.kt = (int)L.kt;
+    d.top_k = (int)a->top_k;
+    d.shared_id = (int)a->shared_expert_id;
+    d.ids_is_i64 = a->ids_is_i64;
+    d.ids = a->topk_ids;
+    d.route_pos = L.rb.route_pos;
+    d.route_weight = L.rb.route_weight;
+    d.y = L.y;
+    d.ldy = L.ip;
+    d.rowpart = L.rowpart;
+    d.parts = parts;
+    d.inter = I;
+    d.w = a->w2;
+    d.w_expert_bytes = fcmoe_packed_expert_bytes(1, H, I, 1);
+    d.k_chunks = L.ip / 64;
+    d.scale_col = a->w2_scale;
+    d.hidden = H;
+    d.q2 = L.q2;
+    d.ldq = L.ip;
+    d.s2row = L.s2row;
+    d.route_out = L.route_out;
+    d.out = a->out;
+    Stage st(FCMOE_STAGE_W2_CLASS0 + class_slot(16), stream);
+    return decode_tail_launch(d, stream);
+  }
   {
     Stage st(FCMOE_STAGE_REQUANT, stream);
     rc = requant_launch(L.y, L.ip, L.routes, I, L.rowpart, ceil_div(I, 16), L.q2, L.ip, L.s2row, stream);

@@ -207,4 +207,32 @@ constexpr int64_t kLdsMaxABytes = 0x7ffffff0;
 int combine_launch(const float* route_out, const float* route_weight, const int32_t* route_pos, int64_t tokens,
                    int64_t kt, int64_t hidden, int tree, int skip_weighted, uint16_t* out, hipStream_t stream);
 
+// ---- W8A8 decode tail (fcmoe_decode_tail.hip) ----
+// requant + W2 + ordered merge in one launch for batches of a token or two;
+// writes out and the q2 / s2row / route_out views as the unfused path does.
+constexpr int kDecodeTailSlots = 16;  // slots per token (top_k + shared) it supports
+struct DecodeTailArgs {
+  int64_t tokens;
+  int kt, top_k, shared_id, ids_is_i64;
+  const void* ids;             // [tokens, top_k]
+  const int32_t* route_pos;    // [tokens * kt] flat route -> sorted position (-1 dropped)
+  const float* route_weight;   // [tokens * kt]
+  const uint16_t* y;           // [positions, ldy] bf16 intermediate
+  int64_t ldy;
+  const float* rowpart;        // [positions, parts] W13 tile maxima of |y|
+  int64_t parts;               // ceil(inter / 16), at most 128
+  int64_t inter;               // I
+  const void* w;               // packed W2 [E][ceil(H/16) tiles][k_chunks][1 KB]
+  int64_t w_expert_bytes;
+  int64_t k_chunks;            // ldq / 64
+  const float* scale_col;      // [E, hidden]
+  int64_t hidden;
+  int8_t* q2;                  // [positions, ldq] (view)
+  int64_t ldq;
+  float* s2row;                // [positions] (view)
+  float* route_out;            // [tokens * kt, hidden] (view)
+  uint16_t* out;               // [tokens, hidden] bf16
+};
+int decode_tail_launch(const DecodeTailArgs& a, hipStream_t stream);
+
 }  // namespace fcmoe

@@ -564,6 +564,73 @@ int w8a8_run(const fcmoe_moe_args* a, char* ws_base, size_t ws_bytes, bool seria
   W8A8Layout L = w8a8_layout(a, ar);
   if (!ar.ok()) return fail(FCMOE_ESPACE, "W8A8 workspace too small");
   const int64_t H = a->hidden, I = a->inter;
+  const int64_t parts = ceil_div(I, 16);
+  const bool tail = a->tokens <= decode_tail_max_tokens() && L.kt <= kDecodeTailSlots && parts <= 128;
+  auto decode_tail = [&]() {
+    // requant + W2 + merge in one launch (timed as the W2 16-row stage)
+    DecodeTailArgs d{};
+    d.tokens = a->tokens;
+    d.kt = (int)L.kt;
+    d.top_k = (int)a->top_k;
+    d.shared_id = (int)a->shared_expert_id;
+    d.ids_is_i64 = a->ids_is_i64;
+    d.ids = a->topk_ids;
+    d.route_pos = L.rb.route_pos;
+    d.route_weight = L.rb.route_weight;
+    d.y = L.y;
+    d.ldy = L.ip;
+    d.rowpart = L.rowpart;
+    d.parts = parts;
+    d.inter = I;
+    d.w = a->w2;
+    d.w_expert_bytes = fcmoe_packed_expert_bytes(1, H, I, 1);
+    d.k_chunks = L.ip / 64;
+    d.scale_col = a->w2_scale;
+    d.hidden = H;
+    d.q2 = L.q2;
+    d.ldq = L.ip;
+    d.s2row = L.s2row;
+    d.route_out = L.route_out;
+    d.out = a->out;
+    Stage st(FCMOE_STAGE_W2_CLASS0 + class_slot(16), stream);
+    return decode_tail_launch(d, stream);
+  };
+  if (tail && a->tokens == 1 && L.hp <= kDecodeHeadMaxK && ceil_div(H / 8, 64) <= 16) {
+    // one token: route + row quantisation + W13 in one launch (timed as the
+    // W13 16-row stage), then the tail
+    DecodeHeadArgs h{};
+    h.kt = (int)L.kt;
+    h.top_k = (int)a->top_k;
+    h.shared_id = (int)a->shared_expert_id;
+    h.ids_is_i64 = a->ids_is_i64;
+    h.valid_experts = (int)a->valid_experts;
+    h.scale_routed = a->shared_expert_id >= 0 ? 1 : 0;
+    h.scale = a->routed_scaling;
+    h.ids = a->topk_ids;
+    h.topk_w = a->topk_weights;
+    h.x = (const uint16_t*)a->x;
+    h.hidden = H;
+    h.w = a->w13;
+    h.w_expert_bytes = fcmoe_packed_expert_bytes(1, 2 * I, H, 2);
+    h.k_chunks = L.hp / 64;
+    h.n_tiles = parts;
+    h.inter = I;
+    h.scale_col = a->w13_scale;
+    h.y = L.y;
+    h.ldy = L.ip;
+    h.rowpart = L.rowpart;
+    h.xs = L.xs;
+    h.route_pos = L.rb.route_pos;
+    h.route_weight = L.rb.route_weight;
+    h.sorted_routes = L.rb.sorted_routes;
+    h.row_token = L.rb.row_token;
+    h.invalid = a->invalid_count ? a->invalid_count : L.rb.invalid;
+    {
+      Stage st(FCMOE_STAGE_W13_CLASS0 + class_slot(16), stream);
+      if ((rc = decode_head_launch(h, stream))) return rc;
+    }
+    return decode_tail();
+  }
 
   bool quant_done = false;
   {
@@ -603,36 +670,7 @@ int w8a8_run(const fcmoe_moe_args* a, char* ws_base, size_t ws_bytes, bool seria
   rc = run_w8a8_stage(L.tc, L.rb, kEpiW13SwigluI8, g13, FCMOE_STAGE_W13_CLASS0, FCMOE_STAGE_W13_MIXED_MFMA,
                       serial_classes, stream);
   if (rc) return rc;
-  const int64_t parts = ceil_div(I, 16);
-  if (a->tokens <= decode_tail_max_tokens() && L.kt <= kDecodeTailSlots && parts <= 128) {
-    // requant + W2 + merge in one launch (timed as the W2 16-row stage)
-    DecodeTailArgs d{};
-    d.tokens = a->tokens;
-    d.kt = (int)L.kt;
-    d.top_k = (int)a->top_k;
-    d.shared_id = (int)a->shared_expert_id;
-    d.ids_is_i64 = a->ids_is_i64;
-    d.ids = a->topk_ids;
-    d.route_pos = L.rb.route_pos;
-    d.route_weight = L.rb.route_weight;
-    d.y = L.y;
-    d.ldy = L.ip;
-    d.rowpart = L.rowpart;
-    d.parts = parts;
-    d.inter = I;
-    d.w = a->w2;
-    d.w_expert_bytes = fcmoe_packed_expert_bytes(1, H, I, 1);
-    d.k_chunks = L.ip / 64;
-    d.scale_col = a->w2_scale;
-    d.hidden = H;
-    d.q2 = L.q2;
-    d.ldq = L.ip;
-    d.s2row = L.s2row;
-    d.route_out = L.route_out;
-    d.out = a->out;
-    Stage st(FCMOE_STAGE_W2_CLASS0 + class_slot(16), stream);
-    return decode_tail_launch(d, stream);
-  }
+  if (tail) return decode_tail();
   {
     Stage st(FCMOE_STAGE_REQUANT, stream);
     rc = requant_launch(L.y, L.ip, L.routes, I, L.rowpart, ceil_div(I, 16), L.q2, L.ip, L.s2row, stream);

@@ -35,6 +35,7 @@ namespace {
 constexpr int kRing = 12;   // weight / y chunks per wave ring (issue runs kRing - 1 ahead)
 constexpr int kQAhead = 2;  // chunks quantised ahead of the MFMA
 constexpr int kQRing = 4;   // per-wave LDS ring of quantised 64-byte chunks
+constexpr int kHeadEarly = 3;  // head: weight chunks issued before the token row is quantised
 
 __global__ __launch_bounds__(kDecodeTailSlots * kWave) void decode_tail_kernel(DecodeTailArgs a) {
   __shared__ float s_val[kDecodeTailSlots][16];
@@ -50,11 +51,13 @@ __global__ __launch_bounds__(kDecodeTailSlots * kWave) void decode_tail_kernel(D
   const int64_t ch = (int64_t)tile * 16 + col;
   const bool cvalid = ch < a.hidden;
   const int64_t r = (int64_t)t * a.kt + slot;
+  // the route's position and expert id, loaded together (the id is valid
+  // whenever the position is)
   const int pos = a.route_pos[r];  // -1: the id was invalid and the route is dropped
+  const int64_t idx = (int64_t)t * a.top_k + (slot < a.top_k ? slot : 0);
+  const int eid = a.ids_is_i64 ? (int)((const int64_t*)a.ids)[idx] : ((const int32_t*)a.ids)[idx];
   if (pos >= 0) {
-    const int64_t idx = (int64_t)t * a.top_k + slot;
-    const int e = slot < a.top_k ? (a.ids_is_i64 ? (int)((const int64_t*)a.ids)[idx] : ((const int32_t*)a.ids)[idx])
-                                 : a.shared_id;
+    const int e = slot < a.top_k ? eid : a.shared_id;
     const int kc = (int)a.k_chunks;
     const uint8_t* wb = (const uint8_t*)a.w + (int64_t)e * a.w_expert_bytes + (int64_t)tile * kc * 1024;
     const uint32_t* yw = (const uint32_t*)(a.y + (int64_t)pos * a.ldy);  // 32-bit words: two bf16 each
@@ -150,6 +153,173 @@ __global__ __launch_bounds__(kDecodeTailSlots * kWave) void decode_tail_kernel(D
   }
 }
 
+
+// ---- one-token head: route + token-row quantisation + W13 in one launch.
+//
+// Workgroup (j, s) is one wave: gate/up channel tile pair j of slot s of the
+// single token. It reads the token's ids, derives its route's sorted position
+// (routes ordered by expert, then by slot: the ascending flat route order of
+// kernels.cpp:583-592) with a ballot, quantises the token row into LDS
+// (quantize_bf16_row, kernels.cpp:211-228) and streams its expert's gate and
+// up tiles through a ring, the row in row 0 of the MFMA as in the tail. The
+// epilogue is the W13 one (w13_epilogue, kernels.cpp:230-246: clamped SwiGLU
+// with the FEXPA exp, bf16 y and the per-(row, gate tile) max of |y|).
+// Workgroups j = 0 write the route metadata the tail and the stage views read
+// (route_pos, route_weight, sorted_routes, row_token); (0, 0) writes the
+// invalid-id count.
+template <int CAP>
+__global__ __launch_bounds__(kWave) void decode_head_kernel(DecodeHeadArgs a) {
+  __shared__ __attribute__((aligned(16))) int8_t s_x[kDecodeHeadMaxK];
+  const int lane = threadIdx.x;
+  const int j = blockIdx.x;
+  const int s = blockIdx.y;
+
+  // the token row: CAP 16-byte units per lane, in flight with the ids
+  const int64_t units = a.hidden / 8;
+  const uint4* xp = (const uint4*)a.x;
+  uint4 xv[CAP];
+#pragma unroll
+  for (int u = 0; u < CAP; ++u) {
+    // unconditional loads (a conditional one would be waited for alone):
+    // units past the row re-read its last unit, which leaves the max
+    // unchanged; the quantised row holds zeros there
+    const int64_t i = lane + (int64_t)u * kWave;
+    xv[u] = xp[i < units ? i : units - 1];
+  }
+  // the token's slots: expert, validity (route_expert) and combined weight (route_weight_of)
+  int e_l = 0;
+  bool ok_l = false;
+  float w_l = 0.0f;
+  {
+    const int li = lane < a.top_k ? lane : 0;  // unconditional loads, results selected
+    const int64_t e = a.ids_is_i64 ? ((const int64_t*)a.ids)[li] : (int64_t)((const int32_t*)a.ids)[li];
+    float w = a.topk_w ? a.topk_w[li] : 1.0f;
+    if (a.scale_routed) w = w * a.scale;
+    if (lane < a.top_k) {
+      ok_l = e >= 0 && e < a.valid_experts;
+      e_l = ok_l ? (int)e : 0;
+      w_l = w;
+    } else if (lane < a.kt) {
+      e_l = a.shared_id;
+      ok_l = true;
+      w_l = 1.0f;
+    }
+  }
+  const int e_s = __builtin_amdgcn_readlane(e_l, s);
+  const bool ok_s = __builtin_amdgcn_readlane((int)ok_l, s) != 0;
+  const int pos = __popcll(__ballot(ok_l && (e_l < e_s || (e_l == e_s && lane < s))));
+  const int n_invalid = __popcll(__ballot(lane < a.top_k && !ok_l));  // all lanes vote
+  if (j == 0 && lane == 0) {
+    a.route_pos[s] = ok_s ? pos : -1;
+    a.route_weight[s] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w_l), s));
+    if (ok_s) {
+      a.sorted_routes[pos] = s;
+      a.row_token[pos] = 0;
+    }
+    if (s == 0) *a.invalid = n_invalid;
+  }
+  if (!ok_s) return;
+
+  // gate tile j and up tile n_tiles + j of expert e_s (packed [group][tile][chunk][1 KB]);
+  // the ring's first chunks go out before the row is quantised
+  const int kc = (int)a.k_chunks;
+  const uint8_t* wg = (const uint8_t*)a.w + (int64_t)e_s * a.w_expert_bytes + (int64_t)j * kc * 1024;
+  const uint8_t* wu = wg + (int64_t)a.n_tiles * kc * 1024;
+  v4i bg[kRing], bu[kRing];
+  auto issue = [&](int c, auto slot_c) {
+    constexpr int b = decltype(slot_c)::value;
+    const int cc = c < kc ? c : kc - 1;  // past the end: re-read, never consumed
+    bg[b] = __builtin_nontemporal_load((const v4i*)(wg + (int64_t)cc * 1024) + lane);
+    bu[b] = __builtin_nontemporal_load((const v4i*)(wu + (int64_t)cc * 1024) + lane);
+  };
+  // the first kHeadEarly chunks before the row is quantised, the rest after
+  // (all at once, the row's registers and the ring would not fit two waves
+  // per SIMD)
+  [&]<int... S>(std::integer_sequence<int, S...>) {
+    (issue(S, std::integral_constant<int, S>{}), ...);
+  }(std::make_integer_sequence<int, kHeadEarly>{});
+  // quantize_bf16_row: scale = max|x| / 127, q = round(x / scale) half away
+  float m = 0.0f;
+#pragma unroll
+  for (int u = 0; u < CAP; ++u) {
+    const uint32_t w[4] = {xv[u].x, xv[u].y, xv[u].z, xv[u].w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      m = fmaxf(m, fabsf(__uint_as_float(w[k] << 16)));
+      m = fmaxf(m, fabsf(__uint_as_float(w[k] & 0xffff0000u)));
+    }
+  }
+  m = wave_max(m);
+  const float xs = m > 0.0f ? m / 127.0f : 1.0f;
+  const float xinv = 1.0f / xs;
+  if (j == 0 && s == 0 && lane == 0) *a.xs = xs;
+#pragma unroll
+  for (int u = 0; u < CAP; ++u) {
+    const int64_t i = lane + (int64_t)u * kWave;
+    if (i * 8 < a.k_chunks * 64) {
+      const uint32_t w[4] = {xv[u].x, xv[u].y, xv[u].z, xv[u].w};
+      uint32_t lo = 0, hi = 0;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const uint32_t qa = (uint8_t)quant_value(__uint_as_float(w[k] << 16), xs, xinv, 0);
+        const uint32_t qb = (uint8_t)quant_value(__uint_as_float(w[k] & 0xffff0000u), xs, xinv, 0);
+        const uint32_t pair = qa | (qb << 8);
+        if (k < 2)
+          lo |= pair << (16 * k);
+        else
+          hi |= pair << (16 * (k - 2));
+      }
+      *(uint2*)(&s_x[i * 8]) = i < units ? make_uint2(lo, hi) : make_uint2(0, 0);  // K padding: zeros
+    }
+  }
+  __syncthreads();
+  [&]<int... S>(std::integer_sequence<int, S...>) {
+    (issue(kHeadEarly + S, std::integral_constant<int, kHeadEarly + S>{}), ...);
+  }(std::make_integer_sequence<int, kRing - 1 - kHeadEarly>{});
+
+  v4i acc_g = v4i{0, 0, 0, 0}, acc_u = v4i{0, 0, 0, 0};
+  const int a_off = 16 * (lane / 16);
+  auto body = [&](int c, auto b_c) {
+    constexpr int b = decltype(b_c)::value;
+    issue(c + kRing - 1, std::integral_constant<int, (b + kRing - 1) % kRing>{});
+    const v4i av = *(const v4i*)(&s_x[c * 64 + a_off]);
+    acc_g = mfma(av, bg[b % kRing], acc_g);
+    acc_u = mfma(av, bu[b % kRing], acc_u);
+  };
+  int c0 = 0;
+  for (; c0 + kRing <= kc; c0 += kRing) {
+    [&]<int... S>(std::integer_sequence<int, S...>) {
+      (body(c0 + S, std::integral_constant<int, S>{}), ...);
+    }(std::make_integer_sequence<int, kRing>{});
+  }
+  [&]<int... S>(std::integer_sequence<int, S...>) {
+    ((c0 + S < kc ? body(c0 + S, std::integral_constant<int, S>{}) : void()), ...);
+  }(std::make_integer_sequence<int, kRing - 1>{});
+
+  // w13_epilogue on output row 0 (lanes 0..15, register 0); evaluated on every
+  // lane so the FEXPA table read sees all lanes active
+  const int col = lane % 16;
+  const int64_t f = (int64_t)j * 16 + col;
+  const bool fv = f < a.inter;
+  const int64_t fc = fv ? f : 0;
+  const float cg = a.scale_col[(int64_t)e_s * 2 * a.inter + fc];
+  const float cu = a.scale_col[(int64_t)e_s * 2 * a.inter + a.inter + fc];
+  float gate = (float)acc_g[0] * (xs * cg);
+  float up = (float)acc_u[0] * (xs * cu);
+  gate = fminf(gate, 10.0f);
+  up = fmaxf(fminf(up, 10.0f), -10.0f);
+  const float ex = fexpa_exp_neg_v(gate, fexpa_table_lane());
+  const float y = (gate * up) / (ex + 1.0f);
+  const uint16_t yb = f32_to_bf16(y);
+  float ya = 0.0f;
+  if (lane < 16 && fv) {
+    a.y[(int64_t)pos * a.ldy + f] = yb;
+    ya = fabsf(bf16_to_f32(yb));
+  }
+  const float amax = max16(ya);
+  if (lane == 0) a.rowpart[(int64_t)pos * a.n_tiles + j] = amax;
+}
+
 }  // namespace
 
 int decode_tail_launch(const DecodeTailArgs& a, hipStream_t stream) {
@@ -160,6 +330,21 @@ int decode_tail_launch(const DecodeTailArgs& a, hipStream_t stream) {
   hipLaunchKernelGGL(decode_tail_kernel, dim3((unsigned)ceil_div(a.hidden, 16), (unsigned)a.tokens),
                      dim3(a.kt * kWave), 0, stream, a);
   return check_launch("decode_tail");
+}
+
+int decode_head_launch(const DecodeHeadArgs& a, hipStream_t stream) {
+  const int64_t units = ceil_div(a.hidden / 8, kWave);  // x units per lane
+  if (a.kt <= 0 || a.kt > kDecodeTailSlots || a.hidden % 8 || a.k_chunks * 64 > kDecodeHeadMaxK ||
+      a.k_chunks * 64 < a.hidden || units > 16 || a.n_tiles <= 0)
+    return fail(FCMOE_EINVAL, "decode head: shapes outside its domain");
+  const dim3 grid((unsigned)a.n_tiles, (unsigned)a.kt), block(kWave);
+  if (units <= 4)
+    hipLaunchKernelGGL(decode_head_kernel<4>, grid, block, 0, stream, a);
+  else if (units <= 8)
+    hipLaunchKernelGGL(decode_head_kernel<8>, grid, block, 0, stream, a);
+  else
+    hipLaunchKernelGGL(decode_head_kernel<16>, grid, block, 0, stream, a);
+  return check_launch("decode_head");
 }
 
 }  // namespace fcmoe

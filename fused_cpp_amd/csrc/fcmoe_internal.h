@@ -234,5 +234,33 @@ struct DecodeTailArgs {
   uint16_t* out;               // [tokens, hidden] bf16
 };
 int decode_tail_launch(const DecodeTailArgs& a, hipStream_t stream);
+// One-token head: route + token-row quantisation + W13 in one launch; writes
+// y, rowpart and the route metadata (route_pos, route_weight, sorted_routes,
+// row_token, the invalid count) as the route and W13 launches do.
+constexpr int64_t kDecodeHeadMaxK = 8192;  // padded hidden size it takes (the row lives in LDS)
+struct DecodeHeadArgs {
+  int kt, top_k, shared_id, ids_is_i64, valid_experts, scale_routed;
+  float scale;
+  const void* ids;           // [top_k] the token's ids
+  const float* topk_w;       // [top_k] or null (weights 1)
+  const uint16_t* x;         // [hidden] bf16 token row
+  int64_t hidden;
+  const void* w;             // packed W13 [E][2 groups][n_tiles][k_chunks][1 KB]
+  int64_t w_expert_bytes;
+  int64_t k_chunks;          // hp / 64
+  int64_t n_tiles;           // ceil(inter / 16)
+  int64_t inter;
+  const float* scale_col;    // [E, 2 inter]
+  uint16_t* y;               // [positions, ldy]
+  int64_t ldy;
+  float* rowpart;            // [positions, n_tiles]
+  float* xs;                 // [1] the token row's scale
+  int32_t* route_pos;        // [kt]
+  float* route_weight;       // [kt]
+  int32_t* sorted_routes;    // [kt]
+  int32_t* row_token;        // [kt]
+  int32_t* invalid;          // [1]
+};
+int decode_head_launch(const DecodeHeadArgs& a, hipStream_t stream);
 
 }  // namespace fcmoe

@@ -1,12 +1,16 @@
-"""The W8A8 decode tail: requant + W2 + ordered merge in one launch
-(fcmoe_decode_tail.hip; one-token batches by default, forced here for up to
-two with FCMOE_DECODE_TAIL_MAX_T=2), against the three launches it replaces
-(FCMOE_DECODE_TAIL_MAX_T=0) and the CPU oracle.
+"""The W8A8 decode tail (requant + W2 + ordered merge in one launch) and, at one
+token, the decode head (route + token-row quantisation + W13 in one launch)
+of fcmoe_decode_tail.hip, against the launches they replace
+(FCMOE_DECODE_TAIL_MAX_T=0) and the CPU oracle. The tail runs for one-token
+batches by default and is forced here for up to two
+(FCMOE_DECODE_TAIL_MAX_T=2); the head always takes one-token batches with it.
 
-Reference semantics: quantize_bf16_row of the intermediate and store_w2
-(csrc/moe/arm/i8mm_w8a8/kernels.cpp:211-228, 248-257, 650-657) and the ordered
-top-k merge (kernels.cpp:674-688). Everything is compared bit for bit: the
-output, and the q2 / s2row / route_out views that the unfused path leaves.
+Reference semantics: the route order (kernels.cpp:583-592), quantize_bf16_row
+of the token row and of the intermediate, w13_epilogue and store_w2
+(csrc/moe/arm/i8mm_w8a8/kernels.cpp:211-257, 650-657) and the ordered top-k
+merge (kernels.cpp:674-688). Everything is compared bit for bit: the output,
+the invalid-id count, and the sorted_routes / y / q2 / s2row / route_out views
+that the unfused path leaves.
 """
 
 from __future__ import annotations
@@ -47,6 +51,8 @@ def _compare(a, b, ids, valid_experts, shared):
     np.testing.assert_array_equal(out_a, out_b)
     routes = _valid_routes(ids, valid_experts, shared)
     n = len(routes)
+    np.testing.assert_array_equal(st_a["sorted_routes"][:n], st_b["sorted_routes"][:n])
+    np.testing.assert_array_equal(st_a["y"][:n], st_b["y"][:n])
     np.testing.assert_array_equal(st_a["q2"][:n], st_b["q2"][:n])
     np.testing.assert_array_equal(st_a["s2row"][:n].view(np.uint32), st_b["s2row"][:n].view(np.uint32))
     np.testing.assert_array_equal(st_a["route_out"][routes].view(np.uint32), st_b["route_out"][routes].view(np.uint32))
@@ -99,6 +105,25 @@ def test_decode_tail_with_dropped_routes(gpu):
     _compare(fused, plain, ids, 10, False)
     assert fused[1]["invalid"] == plain[1]["invalid"] == 6
     assert not fused[0][1].any()  # the merge of nothing is 0
+
+
+@pytest.mark.parametrize("shared", [True, False])
+def test_decode_head_one_token_dropped_routes(gpu, shared):
+    """One token (the head path) with out-of-range ids, and with every routed id
+    out of range (only the shared slot left, or no slot at all)."""
+    E = 10
+    case = H.w8a8_case(31, 1, 512, 128, E, 4)
+    x, ids, w, q13, s13, q2, s2 = case
+    sid = E - 1 if shared else -1
+    for bad in ([1, 3], [0, 1, 2, 3]):
+        ids_b = np.minimum(ids, E - 2).copy()
+        ids_b[0, bad] = [E + 5, -2, 77, -1][: len(bad)]
+        c = (x, ids_b, w, q13, s13, q2, s2)
+        print(f"[decode-head] shared={shared} dropped slots {bad}", flush=True)
+        fused = _run(c, gpu, tail=True, shared_id=sid, valid_experts=E - 1 if shared else E)
+        plain = _run(c, gpu, tail=False, shared_id=sid, valid_experts=E - 1 if shared else E)
+        _compare(fused, plain, ids_b, E - 1 if shared else E, shared)
+        assert fused[1]["invalid"] == plain[1]["invalid"] == len(bad)
 
 
 def test_decode_tail_int32_ids_and_third_token_falls_back(gpu, oracle_lib):

@@ -424,10 +424,11 @@ bool part_enabled() {
 }
 
 // Decode batches of at most this many tokens (FCMOE_DECODE_TAIL_MAX_T; 0
-// turns the fused tail off) run requant, W2 and the merge as one launch. At
-// one token it saves two launches (C2 shape: 0.082 -> 0.077 ms); at two the
-// tokens' workgroups each stream the shared expert's weights, and it is
-// slower (0.133 -> 0.136 ms).
+// turns both off) run requant, W2 and the merge as one launch (the tail), and
+// a one-token batch runs route, row quantisation and W13 as one (the head).
+// At one token the tail saves two launches (C2 shape: 0.082 -> 0.077 ms) and
+// the head one more (0.074 ms); at two the tokens' workgroups each stream the
+// shared expert's weights, and the tail is slower (0.133 -> 0.136 ms).
 constexpr int kDecodeTailMaxTokens = 1;
 int decode_tail_max_tokens() {
   const char* v = getenv("FCMOE_DECODE_TAIL_MAX_T");

@@ -1,5 +1,7 @@
-// fcmoe_decode_tail.hip -- the last three steps of the W8A8 layer in one
-// launch for decode batches of a token or two:
+// fcmoe_decode_tail.hip -- small-batch W8A8 decode in few launches. The
+// decode head (below) does route, token-row quantisation and W13 for a
+// one-token batch. The decode tail does the last three steps of the layer in
+// one launch for a token or two:
 //   requant: quantize_bf16_row of each route's intermediate row
 //            (csrc/moe/arm/i8mm_w8a8/kernels.cpp:650-657, 211-228),
 //   W2:      the int8 GEMM row with store_w2's scaling (kernels.cpp:248-257),

@@ -56,8 +56,11 @@ __global__ __launch_bounds__(kDecodeTailSlots * kWave) void decode_tail_kernel(D
   // the route's position and expert id, loaded together (the id is valid
   // whenever the position is)
   const int pos = a.route_pos[r];  // -1: the id was invalid and the route is dropped
+  // (with top_k = 0 there are no ids: the only slot is the shared expert)
   const int64_t idx = (int64_t)t * a.top_k + (slot < a.top_k ? slot : 0);
-  const int eid = a.ids_is_i64 ? (int)((const int64_t*)a.ids)[idx] : ((const int32_t*)a.ids)[idx];
+  const int eid = a.top_k == 0 ? 0
+                  : a.ids_is_i64 ? (int)((const int64_t*)a.ids)[idx]
+                                 : ((const int32_t*)a.ids)[idx];
   if (pos >= 0) {
     const int e = slot < a.top_k ? eid : a.shared_id;
     const int kc = (int)a.k_chunks;
@@ -193,9 +196,12 @@ __global__ __launch_bounds__(kWave) void decode_head_kernel(DecodeHeadArgs a) {
   bool ok_l = false;
   float w_l = 0.0f;
   {
-    const int li = lane < a.top_k ? lane : 0;  // unconditional loads, results selected
-    const int64_t e = a.ids_is_i64 ? ((const int64_t*)a.ids)[li] : (int64_t)((const int32_t*)a.ids)[li];
-    float w = a.topk_w ? a.topk_w[li] : 1.0f;
+    // unconditional loads, results selected (top_k = 0: no ids, only the shared slot)
+    const int li = lane < a.top_k ? lane : 0;
+    const int64_t e = a.top_k == 0 ? 0
+                      : a.ids_is_i64 ? ((const int64_t*)a.ids)[li]
+                                     : (int64_t)((const int32_t*)a.ids)[li];
+    float w = a.topk_w && a.top_k > 0 ? a.topk_w[li] : 1.0f;
     if (a.scale_routed) w = w * a.scale;
     if (lane < a.top_k) {
       ok_l = e >= 0 && e < a.valid_experts;

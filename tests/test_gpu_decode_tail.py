@@ -126,6 +126,20 @@ def test_decode_head_one_token_dropped_routes(gpu, shared):
         assert fused[1]["invalid"] == plain[1]["invalid"] == len(bad)
 
 
+@pytest.mark.parametrize("T", [1, 2])
+def test_decode_shared_expert_only(gpu, T):
+    """top_k = 0 with a shared expert: no ids at all (the pointers are NULL)."""
+    x, ids, w, q13, s13, q2, s2 = H.w8a8_case(40 + T, T, 256, 128, 3, 1)
+    ids0 = np.zeros((T, 0), np.int64)
+    w0 = np.zeros((T, 0), np.float32)
+    c = (x, ids0, w0, q13, s13, q2, s2)
+    print(f"[decode] shared expert only, T={T}", flush=True)
+    fused = _run(c, gpu, tail=True, shared_id=2)
+    plain = _run(c, gpu, tail=False, shared_id=2)
+    _compare(fused, plain, ids0, 3, True)
+    assert fused[1]["invalid"] == plain[1]["invalid"] == 0
+
+
 def test_decode_tail_int32_ids_and_third_token_falls_back(gpu, oracle_lib):
     """int32 ids through the tail; T=3 runs the unfused path (same result)."""
     for T in (2, 3):

@@ -75,10 +75,10 @@ struct QuantRows {
   float* scales;
 };
 // quant / quant_done: optional. When the rows qualify (cols % 8 == 0,
-// ldq % 8 == 0, cols <= 16384), they are quantised by the extra workgroups of
-// a single-workgroup route launch (the whole small-batch routing, or the
-// column scan of a larger one) and *quant_done is set; otherwise *quant_done
-// is false and the caller runs quant_rows_launch.
+// ldq % 8 == 0, cols <= 16384), they are quantised by extra workgroups of a
+// route launch (the single-workgroup small-batch routing, or the count launch
+// of a larger one) and *quant_done is set; otherwise *quant_done is false and
+// the caller runs quant_rows_launch.
 int route_launch(const void* ids, int ids_is_i64, const float* topk_w, int64_t tokens, int64_t top_k,
                  int64_t experts, int64_t valid_experts, int64_t shared_id, float routed_scale, bool scale_routed,
                  const RouteBuffers& rb, const TileClasses& tc, int32_t* invalid_out, hipStream_t stream,

@@ -9,7 +9,9 @@
 // by routed_scaling_factor (src/fused_cpp/moe/bf16_tiled.py:1007-1013).
 //
 // Three launches, all O(routes):
-//   1. count:   per 256-route chunk, an LDS histogram over experts.
+//   1. count:   per 256-route chunk, an LDS histogram over experts (the
+//               W8A8 token rows are quantised by extra workgroups of this
+//               launch).
 //   2. scan:    one block: per-expert exclusive scan over chunks, exclusive
 //               scan over experts (offsets), and the per-tile-class work lists
 //               for the grouped GEMMs (the tokens-per-expert tile selector).
@@ -78,8 +80,8 @@ __device__ __forceinline__ float route_weight_of(const RouteArgs& a, int64_t r) 
 // Invalid ids are counted per chunk (chunk_invalid, plain stores) and summed
 // by the scan kernel, which writes the total: the caller's counter needs no
 // zeroing launch beforehand.
-__global__ __launch_bounds__(kRouteChunk) void route_count_kernel(RouteArgs a, int64_t routes, int32_t* chunk_hist,
-                                                                   float* route_weight, int32_t* chunk_invalid) {
+__device__ __forceinline__ void route_count_body(const RouteArgs& a, int64_t routes, int32_t* chunk_hist,
+                                                 float* route_weight, int32_t* chunk_invalid) {
   extern __shared__ int32_t hist[];
   __shared__ int32_t n_invalid;
   const int tid = threadIdx.x;
@@ -100,6 +102,11 @@ __global__ __launch_bounds__(kRouteChunk) void route_count_kernel(RouteArgs a, i
   if (tid == 0) chunk_invalid[blockIdx.x] = n_invalid;
   int32_t* dst = chunk_hist + (int64_t)blockIdx.x * a.experts;
   for (int e = tid; e < a.experts; e += kRouteChunk) dst[e] = hist[e];
+}
+
+__global__ __launch_bounds__(kRouteChunk) void route_count_kernel(RouteArgs a, int64_t routes, int32_t* chunk_hist,
+                                                                   float* route_weight, int32_t* chunk_invalid) {
+  route_count_body(a, routes, chunk_hist, route_weight, chunk_invalid);
 }
 
 struct ClassArgs {
@@ -414,21 +421,22 @@ __global__ __launch_bounds__(kScanThreads) void route_quant_small_kernel(RouteAr
   quant_row_group<CAP>(qr);
 }
 
-// Larger routings: the column scan is one workgroup that leaves the rest of
-// the GPU idle for its whole duration (22-33 us at C3/C4), so the token rows
-// are quantised by the same launch's other workgroups.
+// Larger routings: the token rows are quantised by extra workgroups of the
+// count launch (one row per kRowThreads-thread workgroup), so the column scan,
+// a single latency-bound workgroup, runs with the memory system to itself
+// (beside the quantisation it took C4's route from ~40 to ~72 us).
+static_assert(kRouteChunk == kRowThreads, "count workgroups and row workgroups share the launch's block size");
 template <int CAP>
-__global__ __launch_bounds__(kScanThreads) void route_scan_quant_kernel(int experts, int64_t chunks,
-                                                                        int32_t* chunk_hist, int32_t* counts,
-                                                                        int32_t* offsets, ClassArgs cls,
-                                                                        int32_t* tiles, int32_t* tile_count,
-                                                                        const int32_t* chunk_invalid,
-                                                                        int32_t* invalid, QuantRows qr) {
-  if (blockIdx.x == 0) {
-    route_scan_body(experts, chunks, chunk_hist, counts, offsets, cls, tiles, tile_count, chunk_invalid, invalid);
+__global__ __launch_bounds__(kRouteChunk) void route_count_quant_kernel(RouteArgs a, int64_t routes, int64_t chunks,
+                                                                         int32_t* chunk_hist, float* route_weight,
+                                                                         int32_t* chunk_invalid, QuantRows qr) {
+  if ((int64_t)blockIdx.x < chunks) {
+    route_count_body(a, routes, chunk_hist, route_weight, chunk_invalid);
     return;
   }
-  quant_row_group<CAP>(qr);
+  __shared__ float wmax[kRowThreads / kWave];
+  const int64_t row = (int64_t)blockIdx.x - chunks;
+  quant_row_wg<CAP>(qr.x, qr.cols, qr.rounding, qr.q, qr.ldq, qr.scales, row, true, (int)threadIdx.x, wmax);
 }
 
 // 16-byte units per thread when kRowThreads threads quantise one row of
@@ -546,20 +554,19 @@ int route_launch(const void* ids, int ids_is_i64, const float* topk_w, int64_t t
     hipLaunchKernelGGL(route_small_kernel, dim3(1), dim3(kScanThreads), 0, stream, a, (int)routes, ca, o);
     return check_launch("route");
   }
-  hipLaunchKernelGGL(route_count_kernel, dim3((unsigned)chunks), dim3(kRouteChunk), experts * sizeof(int32_t),
-                     stream, a, routes, rb.chunk_hist, rb.route_weight, rb.chunk_invalid);
   if (const int cap = quant_done ? quant_cap(quant) : 0) {
-    const dim3 grid((unsigned)(1 + ceil_div(quant->rows, kQuantRowsPerGroup))), block(kScanThreads);
     with_cap(cap, [&](auto c) {
-      hipLaunchKernelGGL(route_scan_quant_kernel<decltype(c)::value>, grid, block, 0, stream, (int)experts, chunks,
-                         rb.chunk_hist, rb.counts, rb.offsets, ca, rb.tiles, rb.tile_count, rb.chunk_invalid,
-                         invalid, *quant);
+      hipLaunchKernelGGL(route_count_quant_kernel<decltype(c)::value>, dim3((unsigned)(chunks + quant->rows)),
+                         dim3(kRouteChunk), experts * sizeof(int32_t), stream, a, routes, chunks, rb.chunk_hist,
+                         rb.route_weight, rb.chunk_invalid, *quant);
     });
     *quant_done = true;
   } else {
-    hipLaunchKernelGGL(route_scan_kernel, dim3(1), dim3(kScanThreads), 0, stream, (int)experts, chunks,
-                       rb.chunk_hist, rb.counts, rb.offsets, ca, rb.tiles, rb.tile_count, rb.chunk_invalid, invalid);
+    hipLaunchKernelGGL(route_count_kernel, dim3((unsigned)chunks), dim3(kRouteChunk), experts * sizeof(int32_t),
+                       stream, a, routes, rb.chunk_hist, rb.route_weight, rb.chunk_invalid);
   }
+  hipLaunchKernelGGL(route_scan_kernel, dim3(1), dim3(kScanThreads), 0, stream, (int)experts, chunks, rb.chunk_hist,
+                     rb.counts, rb.offsets, ca, rb.tiles, rb.tile_count, rb.chunk_invalid, invalid);
   hipLaunchKernelGGL(route_scatter_kernel, dim3((unsigned)chunks), dim3(kRouteChunk), 0, stream, a, routes,
                      rb.chunk_hist, rb.offsets, rb.sorted_routes, rb.row_token, rb.route_pos, rb.queues);
   return check_launch("route");

@@ -68,6 +68,32 @@ def test_w8a8_forward_graph_replays(gpu):
     _replay_matches_eager(fn, make, static)
 
 
+def test_w8a8_one_token_decode_graph_replays(gpu):
+    """One token: the decode head and tail launches (route + quantisation + W13,
+    then requant + W2 + merge) under capture."""
+    from fused_cpp_amd import moe
+
+    case = H.w8a8_case(23, 1, 1024, 512, 17, 4)
+    x, ids, w, q13, s13, q2, s2 = case
+    t = torch.from_numpy
+    prepared = moe.prepare_routed_shared_moe_w8a8_tiled_quantized_weights(
+        t(q13[:-1]), t(s13[:-1]), t(q2[:-1]), t(s2[:-1]), t(q13[-1]), t(s13[-1]), t(q2[-1]), t(s2[-1]))
+    rng = np.random.default_rng(5)
+
+    def make(r):
+        xr = torch.from_numpy(H.bf16_bits(rng.standard_normal((1, 1024)).astype(np.float32)).view(np.int16))
+        idr = torch.from_numpy(rng.choice(16, size=(1, 4), replace=False).astype(np.int64))
+        wr = torch.from_numpy(rng.random((1, 4)).astype(np.float32))
+        return xr.to(gpu).view(torch.bfloat16), wr.to(gpu), idr.to(gpu)
+
+    static = list(make(-1))
+
+    def fn(xx, ww, ii):
+        return moe.fused_moe_w8a8_tiled_with_shared(xx, prepared, ww, ii, routed_scaling_factor=2.5)
+
+    _replay_matches_eager(fn, make, static)
+
+
 def test_bf16_and_w8a16_forward_graph_replays(gpu):
     from fused_cpp_amd import moe
 

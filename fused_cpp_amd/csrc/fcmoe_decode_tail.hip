@@ -37,7 +37,7 @@ namespace {
 constexpr int kRing = 12;   // weight / y chunks per wave ring (issue runs kRing - 1 ahead)
 constexpr int kQAhead = 2;  // chunks quantised ahead of the MFMA
 constexpr int kQRing = 4;   // per-wave LDS ring of quantised 64-byte chunks
-constexpr int kHeadEarly = 3;  // head: weight chunks issued before the token row is quantised
+constexpr int kHeadEarly = 8;  // head: weight chunks issued before the token row is quantised (246 VGPRs: two waves per SIMD)
 
 __global__ __launch_bounds__(kDecodeTailSlots * kWave) void decode_tail_kernel(DecodeTailArgs a) {
   __shared__ float s_val[kDecodeTailSlots][16];

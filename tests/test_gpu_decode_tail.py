@@ -140,6 +140,23 @@ def test_decode_shared_expert_only(gpu, T):
     assert fused[1]["invalid"] == plain[1]["invalid"] == 0
 
 
+def test_decode_tail_repeated_expert(gpu, oracle_lib):
+    """Two tokens whose ids repeat one expert: 22 routes of expert 0 (two 16-row
+    blocks, the second mixing both tokens) plus the shared pair, through the tail
+    and the unfused path."""
+    E = 6
+    x, _, _, q13, s13, q2, s2 = H.w8a8_case(50, 2, 256, 64, E, 4)
+    ids = np.array([[0] * 12, [0, 0, 0, 0, 1, 2] + [0] * 6], np.int64)
+    w = np.random.default_rng(51).uniform(0.05, 0.3, size=ids.shape).astype(np.float32)
+    c = (x, ids, w, q13, s13, q2, s2)
+    print("[decode-tail] repeated expert, T=2", flush=True)
+    fused = _run(c, gpu, tail=True, shared_id=E - 1)
+    plain = _run(c, gpu, tail=False, shared_id=E - 1)
+    _compare(fused, plain, ids, E, True)
+    ref = oracle_lib.w8a8_forward(x, ids, w, q13, s13, q2, s2, shared_id=E - 1)
+    np.testing.assert_array_equal(fused[0], ref)
+
+
 def test_decode_tail_int32_ids_and_third_token_falls_back(gpu, oracle_lib):
     """int32 ids through the tail; T=3 runs the unfused path (same result)."""
     for T in (2, 3):

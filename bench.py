@@ -10,9 +10,10 @@ inputs resident in HBM. Prints ONE JSON line.
 
 ``--config c3`` / ``c4`` run the prefill configs, ``c1`` / ``c0`` the BF16
 ones and ``c1w8`` the W8A16 one; ``--tokens`` overrides a config's token
-count. The default C2 line also carries, as ``secondary`` entries, C3 and
-C4 prefill, decode at T=1 and T=2 on the C2 layer, and C1 (BF16), each with
-its own kernel roofline, layer roofline and sampled bit-exact parity check.
+count. The default C2 line also carries, as ``secondary`` entries, decode at
+T=1 and T=2 on the C2 layer (timed over at least 1000 steps), C3 and C4
+prefill, and C1 (BF16), each with its own kernel roofline, layer roofline and
+sampled bit-exact parity check.
 
 roofline: the dominant kernel (largest GPU time per step among the grouped
 GEMM tile-class launches) is timed live with hipEvents recorded by libfcmoe
@@ -551,8 +552,17 @@ def kernel_roofline(workload: str, best, st_alg, peak_ops):
     return roof
 
 
-def measure(cfg, workload: str, args, device, want_cpu: bool):
-    res = run_gpu(cfg, args.steps, args.warmup, device, graph=args.graph)
+# Decode secondaries (a few tokens, ~0.07-0.13 ms per step) time at least this
+# many steps: every timed region carries a fixed ~75 us ramp out of idle, 5% of
+# a 20-step one-token region (C2 at T=1: 0.0732 ms at 20 steps, 0.0727 at 50,
+# 0.0703 at 200, 0.0694 at 1000; T=2 0.1318 -> 0.1291). The main line times
+# exactly --steps.
+DECODE_MIN_STEPS = 1000
+
+
+def measure(cfg, workload: str, args, device, want_cpu: bool, min_steps: int = 0):
+    steps = max(args.steps, min_steps)
+    res = run_gpu(cfg, steps, args.warmup, device, graph=args.graph)
     counts = expert_counts(cfg, res["ids"])
     layer_bytes, layer_ops, st_alg = algorithmic(cfg, counts)
     ms = res["ms"]
@@ -579,7 +589,7 @@ def measure(cfg, workload: str, args, device, want_cpu: bool):
         "int8_mfma_frac": round(layer_ops / (ms * 1e-3) / 1e12 / peak_ops, 4),
         "roofline_ms": round(layer_roof_s * 1e3, 4),
         "roofline_frac": round(layer_roof_s * 1e3 / ms, 4),
-        "stage_ms_per_step": {k: round(v[0] / args.steps, 4) for k, v in res["stages"].items()},
+        "stage_ms_per_step": {k: round(v[0] / steps, 4) for k, v in res["stages"].items()},
     }
     if cfg["kind"] != "w8a8":
         layer["bf16_mfma_frac"] = layer.pop("int8_mfma_frac")
@@ -587,7 +597,7 @@ def measure(cfg, workload: str, args, device, want_cpu: bool):
         layer["zipf_tau"] = res["tau"]
     if plan is not None:
         layer["prefill_plan"] = plan if plan != "partitioned" else f"partitioned ({part} CUs for the 256-row class)"
-    out = {"ms": ms, "tokens_per_s": cfg["T"] / (ms * 1e-3), "roofline": roof, "layer": layer}
+    out = {"ms": ms, "steps": steps, "tokens_per_s": cfg["T"] / (ms * 1e-3), "roofline": roof, "layer": layer}
     if cfg["kind"] == "w8a8":
         out["parity"] = parity_check(cfg, res)
     if want_cpu and cfg["kind"] == "w8a8":
@@ -599,7 +609,7 @@ def measure(cfg, workload: str, args, device, want_cpu: bool):
 
 # Extra workloads measured by default after the headline one, each on its own
 # layer: the prefill configs and decode at its smallest batches.
-SECONDARY = [("c3", "c3", 0), ("c4", "c4", 0), ("c2_t1", "c2", 1), ("c2_t2", "c2", 2), ("c1", "c1", 0)]
+SECONDARY = [("c2_t1", "c2", 1), ("c2_t2", "c2", 2), ("c3", "c3", 0), ("c4", "c4", 0), ("c1", "c1", 0)]
 
 
 def int_mm_reference() -> int:
@@ -797,9 +807,10 @@ def main() -> int:
             c = CONFIGS[name] if tokens <= 0 else dict(CONFIGS[name], T=tokens,
                                                        desc=f"{CONFIGS[name]['desc']}, run at T={tokens}")
             log(f"[bench] secondary {wl}: {c['desc']}")
-            sec = measure(c, wl, args, device, want_cpu=False)
+            sec = measure(c, wl, args, device, want_cpu=False,
+                          min_steps=DECODE_MIN_STEPS if c["T"] <= 8 else 0)
             entry = {"workload": c["desc"], "dtype": "int8" if c["kind"] == "w8a8" else "bf16",
-                     "tokens_per_s": round(sec["tokens_per_s"], 1), "ms_per_step": round(sec["ms"], 4),
+                     "tokens_per_s": round(sec["tokens_per_s"], 1), "ms_per_step": round(sec["ms"], 4), "steps": sec["steps"],
                      "roofline": sec["roofline"], "layer": sec["layer"]}
             if "parity" in sec:
                 entry["parity"] = sec["parity"]

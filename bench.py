@@ -259,9 +259,9 @@ _LAYERS: dict = {}
 def get_layer(cfg, device):
     """Prepared weights for cfg's shape, built once per (kind, shape) and shared
     by every workload of that shape (C2, C3 and the small-batch decode lines
-    use the same seeded E=256 layer). W8A8 / W8A16 entries also hold the
-    unpacked int8 device tensors, from which parity checks and the CPU
-    baselines copy the experts they touch."""
+    use the same seeded E=256 layer). Entries also hold the unpacked device
+    tensors (int8 + scales, or the bf16 weights), from which parity checks and
+    the CPU baselines copy the experts they touch."""
     kind = "w8" if cfg["kind"] in ("w8a8", "w8a16") else "bf16"
     key = (kind, cfg["E"], cfg["H"], cfg["I"], cfg["shared"])
     if key not in _LAYERS:
@@ -277,7 +277,7 @@ def get_layer(cfg, device):
         if kind == "w8":
             weights, _, dev = build_layer(cfg, device, False, keep_device_int8=True)
         else:
-            weights, dev = build_bf16_layer(cfg, device), None
+            weights, dev = build_bf16_layer(cfg, device, keep_device=True)
         log(f"[bench] {cfg['desc']}: weights ready in {time.time() - t0:.1f}s")
         _LAYERS[key] = (weights, dev)
     return _LAYERS[key]
@@ -427,6 +427,36 @@ def torch_eager_expert_layer(x_bf16, ids, w, cfg, experts, host, routes):
     return out
 
 
+def cpu_threads() -> tuple[int, int]:
+    """(host CPUs as os.cpu_count() reports them, CPUs this process may run
+    on). The CPU baselines run torch on the second: on a shared GPU box the
+    affinity mask is the host share this job holds."""
+    n_host = os.cpu_count() or 1
+    try:
+        n_use = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        n_use = n_host
+    return n_host, max(1, min(n_use, n_host))
+
+
+def _set_torch_threads() -> tuple[int, int]:
+    import torch
+
+    n_host, n_use = cpu_threads()
+    torch.set_num_threads(n_use)
+    return n_host, torch.get_num_threads()
+
+
+def _median_time(fn, reps: int = 3) -> float:
+    fn()  # warmup
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return float(np.median(times))
+
+
 def cpu_baseline_torch(cfg, res, budget_experts: int):
     """The north-star CPU baseline: the repo tests' PyTorch eager reference
     (grouped per expert, float64 accumulation) on this host's cores, timed on
@@ -438,26 +468,140 @@ def cpu_baseline_torch(cfg, res, budget_experts: int):
     host = _host_experts(res["dev_int8"], experts)
     routes, _ = _expert_routes(cfg, res["ids"], experts)
     x = res["x"].cpu()
-    torch.set_num_threads(torch.get_num_threads())
-    torch_eager_expert_layer(x, res["ids"], res["w"], cfg, experts[:2], tuple(a[:2] for a in host), routes[:2])
-    times = []
-    for _ in range(3):
-        t0 = time.perf_counter()
-        torch_eager_expert_layer(x, res["ids"], res["w"], cfg, experts, host, routes)
-        times.append(time.perf_counter() - t0)
-    t = float(np.median(times))
+    n_host, threads = _set_torch_threads()
+    t = _median_time(lambda: torch_eager_expert_layer(x, res["ids"], res["w"], cfg, experts, host, routes))
     layer_s = t * n_active / len(experts)
     rows = sum(len(r) for r in routes)
     return {
         "value": round(cfg["T"] / layer_s, 2),
         "unit": "tokens/s",
-        "cores": torch.get_num_threads(),
+        "cores": threads,
+        "host_cpus": n_host,
         "kind": "torch_eager",
         "sample": f"PyTorch eager grouped restatement of tests/test_moe_w8a8.py:40-69 (float64 GEMMs, "
-                  f"{torch.get_num_threads()} threads) on a seeded uniform sample of {len(experts)} of the "
-                  f"{n_active} active experts ({rows} routes), median of 3 = {t:.2f}s after 1 warmup, "
-                  f"scaled by {n_active}/{len(experts)} to the full layer ({layer_s:.2f}s/layer)",
+                  f"torch.set_num_threads({threads}), host os.cpu_count() = {n_host}) on a seeded uniform sample "
+                  f"of {len(experts)} of the {n_active} active experts ({rows} routes), median of 3 = {t:.2f}s "
+                  f"after 1 warmup, scaled by {n_active}/{len(experts)} to the full layer ({layer_s:.2f}s/layer)",
     }
+
+
+def _bf16_host_experts(cfg, dev, experts: np.ndarray, exact: bool = False):
+    """Host copies of the given experts' [2I, H] and [H, I] weights: the bf16
+    layer's own weights, or for W8A16 the int8 weights dequantised, q * s: in
+    fp32 with exact=True (the W8A16 tests' reference: the kernel applies the
+    fp32 scale to the fp32 accumulator), else rounded to bf16 for the CPU
+    baseline's bf16 F.linear."""
+    import torch
+
+    sel = torch.from_numpy(np.ascontiguousarray(experts, np.int64))
+    if cfg["kind"] == "w8a16":
+        q13, s13, q2, s2 = (t.index_select(0, sel.to(t.device)).cpu() for t in dev)
+        d13, d2 = q13.float() * s13[..., None], q2.float() * s2[..., None]
+        return (d13, d2) if exact else (d13.to(torch.bfloat16), d2.to(torch.bfloat16))
+    w13, w2 = dev
+    return tuple(t.index_select(0, sel.to(t.device)).cpu() for t in (w13, w2))
+
+
+def torch_naive_bf16_layer(x_bf16, ids, w, cfg, w13, w2, routes):
+    """Grouped per-expert restatement, in PyTorch eager on the CPU, of the
+    reference's fused_moe_naive (src/fused_cpp/moe/naive.py:161-272): F.linear
+    of each expert's token rows in bf16, SiLU(gate) * up, F.linear, then the
+    [T, slots, H] route rows times the routing weights in fp32, summed over
+    slots and cast to bf16. Routed+shared calls add the shared expert as one
+    more slot of weight 1 with the routed weights scaled (bf16_tiled.py:807-828)."""
+    import torch
+    import torch.nn.functional as F
+
+    T, Hd = x_bf16.shape
+    kt = cfg["k"] + (1 if cfg["shared"] else 0)
+    new_x = torch.zeros((T * kt, Hd), dtype=torch.bfloat16)
+    for j in range(len(routes)):
+        r = torch.from_numpy(routes[j])
+        if r.numel() == 0:
+            continue
+        gate_up = F.linear(x_bf16.index_select(0, r // kt), w13[j])
+        d = gate_up.shape[1] // 2
+        new_x[r] = F.linear(F.silu(gate_up[:, :d]) * gate_up[:, d:], w2[j])
+    wt = torch.from_numpy(w).float() * (cfg["scale"] if cfg["shared"] else 1.0)
+    if cfg["shared"]:
+        wt = torch.cat([wt, torch.ones((T, 1))], 1)
+    return (new_x.view(T, kt, Hd).float() * wt[:, :, None]).sum(1).to(torch.bfloat16)
+
+
+def cpu_baseline_bf16(cfg, res, budget_experts: int):
+    """CPU baseline of the BF16 / W8A16 lines: the reference's PyTorch naive
+    MoE (naive.py:161-272, grouped F.linear in bf16) on this host's cores, on a
+    seeded uniform sample of the active experts scaled to the layer; median
+    of 3 after 1 warmup."""
+    experts, n_active, _ = _expert_sample(cfg, res["ids"], budget_experts)
+    w13, w2 = _bf16_host_experts(cfg, res["dev_int8"], experts)
+    routes, _ = _expert_routes(cfg, res["ids"], experts)
+    x = res["x"].cpu()
+    n_host, threads = _set_torch_threads()
+    t = _median_time(lambda: torch_naive_bf16_layer(x, res["ids"], res["w"], cfg, w13, w2, routes))
+    layer_s = t * n_active / len(experts)
+    deq = " on the int8 weights dequantised to bf16 (outside the timed region)" if cfg["kind"] == "w8a16" else ""
+    return {
+        "value": round(cfg["T"] / layer_s, 2),
+        "unit": "tokens/s",
+        "cores": threads,
+        "host_cpus": n_host,
+        "kind": "torch_eager",
+        "sample": f"PyTorch eager grouped restatement of fused_moe_naive (src/fused_cpp/moe/naive.py:161-272; "
+                  f"bf16 F.linear per expert{deq}; torch.set_num_threads({threads}), host os.cpu_count() = "
+                  f"{n_host}) on a seeded uniform sample of {len(experts)} of the {n_active} active experts, "
+                  f"median of 3 = {t:.3f}s after 1 warmup, scaled by {n_active}/{len(experts)} to the layer "
+                  f"({layer_s:.3f}s/layer)",
+    }
+
+
+def bf16_parity(cfg, res, n: int = 4, tol: float = 2e-2, cos_min: float = 0.9999) -> dict:
+    """BF16 / W8A16 outputs of n tokens (the first n-1 and the last) against
+    the fp32 oracle (oracle.bf16_moe_reference, the naive semantics; for
+    W8A16 on the dequantised weights with the activation output rounded to
+    bf16, as its tests do) on the experts they touch; north-star bar max-abs
+    <= 2e-2, cosine >= 0.9999."""
+    import torch
+
+    import oracle
+
+    T = cfg["T"]
+    tok = np.unique(np.array(list(range(min(n - 1, T))) + [T - 1]))
+    ids = res["ids"][tok]
+    wts = res["w"][tok].astype(np.float32)
+    if cfg["shared"]:
+        ids = np.concatenate([ids, np.full((len(tok), 1), cfg["E"])], 1)
+        wts = np.concatenate([wts * np.float32(cfg["scale"]), np.ones((len(tok), 1), np.float32)], 1)
+    touched = np.unique(ids)
+    w13, w2 = (t.float().numpy() for t in _bf16_host_experts(cfg, res["dev_int8"], touched, exact=True))
+    tk = torch.from_numpy(tok).to(res["x"].device)
+    x = res["x"][tk].float().cpu().numpy()
+    ref = oracle.bf16_moe_reference(x, w13, w2, wts, np.searchsorted(touched, ids),
+                                    round_intermediate=cfg["kind"] == "w8a16")
+    got = res["out"][tk].float().cpu().numpy().astype(np.float64)
+    return _tolerance_report(got, ref, len(tok), tol, cos_min)
+
+
+def _bf16_half_ulp(x):
+    """Half a bf16 ulp at each |x|: the rounding a correctly rounded bf16
+    output carries against an fp32 reference (0.031 at |x| >= 8)."""
+    _, e = np.frexp(np.abs(np.asarray(x, np.float64)))
+    return np.ldexp(1.0, e - 9)
+
+
+def _tolerance_report(got, ref, n: int, tol: float = 2e-2, cos_min: float = 0.9999) -> dict:
+    """max-abs error against the fp32 reference, raw and beyond the bf16
+    output's own rounding (half an ulp of the reference value; the bound
+    applies to this part), and the cosine."""
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    diff = np.abs(got - ref)
+    excess = float((diff - _bf16_half_ulp(ref)).max())
+    cos = float((got * ref).sum() / np.sqrt((got * got).sum() * (ref * ref).sum() + 1e-300))
+    return {"tokens_checked": int(n), "max_abs": round(float(diff.max()), 6),
+            "max_abs_beyond_bf16_rounding": round(excess, 6), "cosine": round(cos, 7),
+            "tolerance": f"max-abs beyond the bf16 output rounding <= {tol}, cosine >= {cos_min}",
+            "within_tolerance": bool(excess <= tol and cos >= cos_min)}
 
 
 def cpu_baseline_oracle(cfg, res, budget_experts: int):
@@ -560,7 +704,7 @@ def kernel_roofline(workload: str, best, st_alg, peak_ops):
 DECODE_MIN_STEPS = 1000
 
 
-def measure(cfg, workload: str, args, device, want_cpu: bool, min_steps: int = 0):
+def measure(cfg, workload: str, args, device, want_cpu: bool, min_steps: int = 0, with_oracle: bool = False):
     steps = max(args.steps, min_steps)
     res = run_gpu(cfg, steps, args.warmup, device, graph=args.graph)
     counts = expert_counts(cfg, res["ids"])
@@ -598,18 +742,198 @@ def measure(cfg, workload: str, args, device, want_cpu: bool, min_steps: int = 0
     if plan is not None:
         layer["prefill_plan"] = plan if plan != "partitioned" else f"partitioned ({part} CUs for the 256-row class)"
     out = {"ms": ms, "steps": steps, "tokens_per_s": cfg["T"] / (ms * 1e-3), "roofline": roof, "layer": layer}
-    if cfg["kind"] == "w8a8":
-        out["parity"] = parity_check(cfg, res)
-    if want_cpu and cfg["kind"] == "w8a8":
-        out["cpu_baseline"] = cpu_baseline_torch(cfg, res, args.cpu_experts)
-        out["cpu_baseline_oracle"] = cpu_baseline_oracle(cfg, res, args.cpu_experts)
+    out["parity"] = parity_check(cfg, res) if cfg["kind"] == "w8a8" else bf16_parity(cfg, res)
+    if want_cpu:
+        if cfg["kind"] == "w8a8":
+            out["cpu_baseline"] = cpu_baseline_torch(cfg, res, args.cpu_experts)
+            if with_oracle:
+                out["cpu_baseline_oracle"] = cpu_baseline_oracle(cfg, res, args.cpu_experts)
+        else:
+            out["cpu_baseline"] = cpu_baseline_bf16(cfg, res, args.cpu_experts)
     del res
     return out
 
 
 # Extra workloads measured by default after the headline one, each on its own
-# layer: the prefill configs and decode at its smallest batches.
-SECONDARY = [("c2_t1", "c2", 1), ("c2_t2", "c2", 2), ("c3", "c3", 0), ("c4", "c4", 0), ("c1", "c1", 0)]
+# layer: decode at small batches, the same C2 layer and T=1 with the default
+# id validation on (one device->host read of the invalid-id count per call),
+# the prefill configs, the BF16 configs, W8A16 at the C1 shape and at
+# T=4096. (workload, config, tokens, validate_ids)
+SECONDARY = [("c2_t1", "c2", 1, False), ("c2_t2", "c2", 2, False), ("c2_t8", "c2", 8, False),
+             ("c2_t32", "c2", 32, False), ("c2_validate_ids", "c2", 0, True), ("c2_t1_validate_ids", "c2", 1, True),
+             ("c3", "c3", 0, False), ("c4", "c4", 0, False), ("c1", "c1", 0, False), ("c0", "c0", 0, False),
+             ("c1w8", "c1w8", 0, False), ("c1w8_t4096", "c1w8", 4096, False)]
+
+# The other operators of the drop-in surface, at DeepSeek-V3.2-shaped sizes
+# (public model config: hidden 7168, q_lora_rank 1536, main Q projection
+# 128 heads x 192 = 24576, indexer Q projection 64 heads x 128 = 8192, output
+# projection 128 x 128 = 16384 -> 7168): the i8gemm pair (one quantisation,
+# two GEMMs; deepseek_v4_w8a8.py:114-132), the single i8gemm (wo_b,
+# :135-143), both at decode (64 rows) and prefill (4096 rows), and the BF16
+# shared MLP (bf16_tiled.py:1805-1873) at T=64. (workload, op, M, K, N list)
+OP_SECONDARY = [("i8gemm_pair_q_m64", "pair", 64, 1536, (24576, 8192)),
+                ("i8gemm_pair_q_m4096", "pair", 4096, 1536, (24576, 8192)),
+                ("i8gemm_wo_b_m64", "single", 64, 16384, (7168,)),
+                ("i8gemm_wo_b_m4096", "single", 4096, 16384, (7168,)),
+                ("shared_mlp_t64", "shared_mlp", 64, 7168, (2048,))]
+
+
+def _time_op(fn, steps: int, warmup: int):
+    """ms per call of fn on the current stream (torch events), then one pass
+    with the library's stage timing on: {stage: (total ms, launches)}."""
+    import torch
+
+    from fused_cpp_amd import cabi
+
+    for _ in range(max(warmup, 1)):
+        fn()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(steps):
+        fn()
+    b.record()
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / steps
+    cabi.stage_timing_read()
+    cabi.stage_timing_enable(True)
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    stages = cabi.stage_timing_read()
+    cabi.stage_timing_enable(False)
+    return ms, stages
+
+
+def _op_roofline(stages, steps: int, names, alg_bytes: int, alg_ops: int, peak_ops: float, kernel: str):
+    """Roofline of an operator's GEMM launches (stage names `names`): their
+    algorithmic bytes / ops per step over their GPU time per step."""
+    tot = sum(stages[n][0] for n in names if n in stages)
+    launches = sum(stages[n][1] for n in names if n in stages)
+    if not launches:
+        return None
+    t_s = tot / steps * 1e-3
+    if alg_bytes / (HBM_PEAK_GBPS * 1e9) >= alg_ops / (peak_ops * 1e12):
+        ach = alg_bytes / t_s / 1e9
+        roof = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                "frac": round(ach / HBM_PEAK_GBPS, 4)}
+    else:
+        ach = alg_ops / t_s / 1e12
+        roof = {"bound": "mfma", "achieved": round(ach, 1), "peak": peak_ops, "unit": "TFLOP/s",
+                "frac": round(ach / peak_ops, 4)}
+    roof.update({"kernel": kernel, "avg_launch_ms": round(tot / launches, 4), "launches_per_step": launches // steps,
+                 "traffic": None, "algorithmic_bytes": alg_bytes, "algorithmic_ops": alg_ops})
+    return roof
+
+
+def measure_op(wl: str, op: str, M: int, K: int, Ns, args, device, want_cpu: bool) -> dict:
+    """One operator secondary: time, kernel roofline, parity (i8gemm bit-exact
+    vs the oracle on 4 rows; shared MLP within the north-star tolerance of the
+    fp32 reference) and a CPU baseline (PyTorch eager on the host)."""
+    import torch
+    import torch.nn.functional as F
+
+    import oracle
+    from fused_cpp_amd import i8gemm as ig
+    from fused_cpp_amd.moe import prepare_shared_mlp_bf16_tiled_weights, shared_mlp_bf16_tiled
+
+    g = torch.Generator(device=device).manual_seed(99)
+    x = torch.randn((M, K), generator=g, device=device).to(torch.bfloat16)
+    steps = max(args.steps, 100 if M <= 64 else 0)
+    entry = {"workload": wl}
+    if op == "shared_mlp":
+        I = Ns[0]
+        w13 = (torch.randn((1, 2 * I, K), generator=g, device=device) * 0.02).to(torch.bfloat16)
+        w2 = (torch.randn((1, K, I), generator=g, device=device) * 0.02).to(torch.bfloat16)
+        prepared = prepare_shared_mlp_bf16_tiled_weights(w13[0], w2[0])
+        out = torch.empty_like(x)
+
+        def fn():
+            return shared_mlp_bf16_tiled(x, prepared, out=out)
+
+        ms, stages = _time_op(fn, steps, args.warmup)
+        gemm = [n for n in stages if n.startswith(("w13_", "w2_"))]
+        alg_b = 3 * K * I * 2 + 2 * M * K * 2
+        alg_o = 6 * M * K * I
+        entry.update({"workload": f"BF16 shared MLP (one dense SwiGLU expert), T={M}, H={K}, I={I}",
+                      "dtype": "bf16", "tokens_per_s": round(M / (ms * 1e-3), 1)})
+        roof = _op_roofline(stages, steps, gemm, alg_b, alg_o, BF16_PEAK_TFLOPS, "grouped_gemm (W13 + W2 launches)")
+        tok = np.array([0, 1, M // 2, M - 1])
+        xs = x[torch.from_numpy(tok).to(device)].float().cpu().numpy()
+        ref = oracle.bf16_moe_reference(xs, w13.float().cpu().numpy(), w2.float().cpu().numpy(),
+                                        np.ones((len(tok), 1), np.float32), np.zeros((len(tok), 1), np.int64))
+        got = out[torch.from_numpy(tok).to(device)].float().cpu().numpy()
+        entry["parity"] = _tolerance_report(got, ref, len(tok))
+        if want_cpu:
+            hx, h13, h2 = x.cpu(), w13[0].cpu(), w2[0].cpu()
+            n_host, threads = _set_torch_threads()
+
+            def cpu():
+                gu = F.linear(hx, h13)
+                return F.linear(F.silu(gu[:, :I]) * gu[:, I:], h2)
+
+            t = _median_time(cpu)
+            entry["cpu_baseline"] = {
+                "value": round(M / t, 2), "unit": "tokens/s", "cores": threads, "host_cpus": n_host,
+                "kind": "torch_eager",
+                "sample": f"the whole op: PyTorch eager bf16 F.linear -> SiLU * up -> F.linear (naive.py:161-272 "
+                          f"with one expert, weight 1), torch.set_num_threads({threads}), median of 3 = {t * 1e3:.2f} "
+                          f"ms after 1 warmup"}
+    else:
+        ws, preps = [], []
+        for n in Ns:
+            w = torch.randint(-127, 128, (n, K), generator=g, device=device, dtype=torch.int8)
+            sc = torch.rand((n,), generator=g, device=device) * 0.004 + 0.0005
+            ws.append((w, sc))
+            preps.append(ig.prepare(w, sc))
+        if op == "pair":
+            fn = lambda: ig.dynamic_scaled_mm_pair(x, preps[0], preps[1])  # noqa: E731
+        else:
+            fn = lambda: ig.dynamic_scaled_mm(x, preps[0])  # noqa: E731
+        ms, stages = _time_op(fn, steps, args.warmup)
+        outs = fn()
+        outs = outs if isinstance(outs, tuple) else (outs,)
+        torch.cuda.synchronize()
+        gemm = [n for n in stages if n.startswith("w13_")]
+        alg_b = sum(n * K + 4 * n + M * K + M * n * 2 for n in Ns)
+        alg_o = sum(2 * M * K * n for n in Ns)
+        shape = " + ".join(f"[{n}, {K}]" for n in Ns)
+        entry.update({"workload": f"i8gemm {'dynamic_scaled_mm_pair' if op == 'pair' else 'dynamic_scaled_mm'}: "
+                                  f"x [{M}, {K}] bf16 against {shape} int8, bf16 out",
+                      "dtype": "int8", "rows_per_s": round(M / (ms * 1e-3), 1)})
+        roof = _op_roofline(stages, steps, gemm, alg_b, alg_o, INT8_PEAK_TOPS, "grouped_gemm (i8gemm GEMM launches)")
+        rows = np.array([0, 1, M // 2, M - 1])
+        xr = x[torch.from_numpy(rows).to(device)].cpu().view(torch.int16).numpy().view(np.uint16)
+        ok = True
+        for (w, sc), o in zip(ws, outs):
+            ref = oracle.i8gemm(xr, w.cpu().numpy(), sc.cpu().numpy(), None, True)
+            got = o[torch.from_numpy(rows).to(device)].cpu().view(torch.int16).numpy().view(np.uint16)
+            ok = ok and bool(np.array_equal(ref, got))
+        entry["parity"] = {"rows_checked": len(rows), "bit_exact": ok}
+        if want_cpu:
+            hx = x.cpu()
+            hw = [(w.cpu().double(), sc.cpu()) for w, sc in ws]
+            n_host, threads = _set_torch_threads()
+
+            def cpu():
+                # tests/test_deepseek_v4_w8a8.py:19-50: per-row scale max|x|/127, round
+                # half to even, clamp +-127, exact integer GEMM (float64), fp32 scales, bf16
+                f = hx.float()
+                m = f.abs().amax(1, keepdim=True)
+                s_x = torch.where(m > 0, m / 127.0, torch.ones_like(m))
+                q = (f / s_x).round().clamp(-127, 127).double()
+                return [((q @ w.T).float() * s_x * sc).to(torch.bfloat16) for w, sc in hw]
+
+            t = _median_time(cpu)
+            entry["cpu_baseline"] = {
+                "value": round(M / t, 2), "unit": "rows/s", "cores": threads, "host_cpus": n_host,
+                "kind": "torch_eager",
+                "sample": f"the whole op: PyTorch eager restatement of tests/test_deepseek_v4_w8a8.py:19-50 "
+                          f"(quantise once, float64 integer GEMMs), torch.set_num_threads({threads}), median of 3 "
+                          f"= {t * 1e3:.1f} ms after 1 warmup"}
+    entry.update({"ms_per_step": round(ms, 4), "steps": steps, "roofline": roof,
+                  "stage_ms_per_step": {k: round(v[0] / steps, 4) for k, v in stages.items()}})
+    return entry
 
 
 def int_mm_reference() -> int:
@@ -638,9 +962,28 @@ def int_mm_reference() -> int:
     return 0
 
 
+def probe_lib():
+    """libfcmoe_probe.so (fused_cpp_amd/csrc/fcmoe_probe.h): the measurement
+    probes, built beside libfcmoe.so but not part of the operator library."""
+    import ctypes
+
+    from fused_cpp_amd import build as fbuild
+
+    if not fbuild.PROBE_LIB.exists():
+        raise RuntimeError(f"{fbuild.PROBE_LIB} is not built (python -m fused_cpp_amd.build)")
+    lib = ctypes.CDLL(str(fbuild.PROBE_LIB))
+    P, I, I64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64
+    for name, args in {"fcmoe_probe_stream": [P, I64, I, I, I, I, P, P], "fcmoe_probe_mfma": [I, I, I, I, P, P],
+                       "fcmoe_probe_mix": [P, I64, I, I, I, I, P, P], "fcmoe_probe_fence": [P, I64, I, I, I, P, P, P],
+                       "fcmoe_probe_ring": [P, I64, P, I64, I, I, I, I, P, P]}.items():
+        fn = getattr(lib, name)
+        fn.restype, fn.argtypes = I, args
+    return lib
+
+
 def probes() -> int:
-    """Chip figures the design relies on, from the library's probe kernels
-    (include/fcmoe.h, fcmoe_probe_*): HBM streaming by launch shape (loads to
+    """Chip figures the design relies on, from the probe kernels
+    (libfcmoe_probe.so, fused_cpp_amd/csrc/fcmoe_probe.h): HBM streaming by launch shape (loads to
     VGPRs and LDS-DMA), the MFMA + LDS-fragment loop by wave tile and waves per
     SIMD, MFMA waves beside streaming waves on one CU, one agent-scope
     release per workgroup, and the prefill GEMM's weight + A-row load mix. Best of 5 launches after 1 warmup (torch events on
@@ -649,7 +992,8 @@ def probes() -> int:
 
     from fused_cpp_amd import cabi
 
-    L = cabi.lib()
+    L = probe_lib()
+    cabi.lib()
     dev = torch.device("cuda", 0)
     stream = cabi.stream_handle()
     sink = torch.zeros(1 << 16, dtype=torch.int32, device=dev)
@@ -712,7 +1056,7 @@ def probes() -> int:
         for la, na, bar in [(2, 0, 1), (2, 2, 1), (4, 2, 1), (6, 2, 1), (2, 2, 0)]:
             nbytes = 3 << 30 if wgs == 256 else 1 << 30
             ms = best_ms(lambda: L.fcmoe_probe_ring(big.data_ptr(), nbytes,
-                                                    arows.data_ptr(), wgs, la, na, bar, sink.data_ptr(), stream))
+                                                    arows.data_ptr(), arows.numel(), wgs, la, na, bar, sink.data_ptr(), stream))
             chunks = nbytes // (wgs * 8 * 4 * 1024)
             wb, ab = wgs * chunks * 32768, wgs * chunks * 8 * na * 1024
             out["ring"].append({"workgroups": wgs, "lookahead": la, "a_kib_per_chunk": 8 * na, "barrier": bool(bar),
@@ -775,7 +1119,7 @@ def main() -> int:
     if args.tokens > 0:
         cfg = dict(cfg, T=args.tokens, desc=f"{cfg['desc']} (T overridden to {args.tokens})")
     workload = args.config if args.tokens <= 0 else f"{args.config}_t{args.tokens}"
-    res = measure(cfg, workload, args, device, want_cpu=not args.no_cpu_baseline)
+    res = measure(cfg, workload, args, device, want_cpu=not args.no_cpu_baseline, with_oracle=True)
     line = {
         "metric": {"w8a8": "W8A8", "w8a16": "W8A16", "bf16": "BF16"}[cfg["kind"]] + " MoE-layer tokens/s",
         "value": round(res["tokens_per_s"], 1),
@@ -792,6 +1136,7 @@ def main() -> int:
         "config": {"workload": cfg["desc"], "tokens": cfg["T"], "hidden": cfg["H"], "intermediate": cfg["I"],
                    "routed_experts": cfg["E"], "top_k": cfg["k"], "shared_experts": int(cfg["shared"]),
                    "routed_scaling": cfg["scale"], "parallelism": "single GPU",
+                   "validate_ids": os.environ.get("FUSED_CPP_AMD_VALIDATE_IDS", "1") != "0",
                    "launch": "hip_graph_replay" if args.graph else "eager"},
         "roofline": res["roofline"],
         "layer": res["layer"],
@@ -803,18 +1148,30 @@ def main() -> int:
         line["cpu_baseline_oracle"] = res["cpu_baseline_oracle"]
     if args.config == "c2" and args.tokens <= 0 and not args.no_secondary:
         line["secondary"] = []
-        for wl, name, tokens in SECONDARY:
+        for wl, name, tokens, validate in SECONDARY:
             c = CONFIGS[name] if tokens <= 0 else dict(CONFIGS[name], T=tokens,
                                                        desc=f"{CONFIGS[name]['desc']}, run at T={tokens}")
+            if validate:
+                c = dict(c, desc=f"{c['desc']}, default id validation on (one device->host read per call)")
             log(f"[bench] secondary {wl}: {c['desc']}")
-            sec = measure(c, wl, args, device, want_cpu=False,
-                          min_steps=DECODE_MIN_STEPS if c["T"] <= 8 else 0)
-            entry = {"workload": c["desc"], "dtype": "int8" if c["kind"] == "w8a8" else "bf16",
+            os.environ["FUSED_CPP_AMD_VALIDATE_IDS"] = "1" if validate else "0"
+            try:
+                sec = measure(c, wl, args, device, want_cpu=not args.no_cpu_baseline,
+                              min_steps=DECODE_MIN_STEPS if c["T"] <= 8 else 0)
+            finally:
+                os.environ["FUSED_CPP_AMD_VALIDATE_IDS"] = "0"
+            entry = {"workload": c["desc"], "name": wl, "validate_ids": validate,
+                     "dtype": "int8" if c["kind"] == "w8a8" else "bf16",
                      "tokens_per_s": round(sec["tokens_per_s"], 1), "ms_per_step": round(sec["ms"], 4), "steps": sec["steps"],
                      "roofline": sec["roofline"], "layer": sec["layer"]}
-            if "parity" in sec:
-                entry["parity"] = sec["parity"]
+            for key in ("parity", "cpu_baseline"):
+                if key in sec:
+                    entry[key] = sec[key]
             line["secondary"].append(entry)
+        for wl, op, M, K, Ns in OP_SECONDARY:
+            log(f"[bench] secondary {wl}")
+            line["secondary"].append(dict(measure_op(wl, op, M, K, Ns, args, device,
+                                                     want_cpu=not args.no_cpu_baseline), name=wl))
     print(json.dumps(line), flush=True)
     return 0
 

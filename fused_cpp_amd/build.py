@@ -4,6 +4,8 @@ Produces, next to this file:
 
 * ``libfcmoe.so`` -- the HIP kernels and the C ABI of ``include/fcmoe.h``
   (``hipcc --offload-arch=gfx950``; no torch dependency);
+* ``libfcmoe_probe.so`` -- the measurement probes ``bench.py --probe`` runs
+  (``csrc/fcmoe_probe.h``); not part of the operator ABI;
 * ``_moe_C<EXT_SUFFIX>`` -- the C++ torch extension that marshals tensors into
   that C ABI (g++ against the torch / ROCm headers, rpath ``$ORIGIN``).
 
@@ -30,7 +32,9 @@ CSRC = PKG / "csrc"
 ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 ARCH = os.environ.get("FCMOE_OFFLOAD_ARCH", "gfx950")
 
-HIP_SOURCES = ["fcmoe_api.hip", "fcmoe_route.hip", "fcmoe_quant.hip", "fcmoe_gemm.hip", "fcmoe_gemm_lds.hip", "fcmoe_combine.hip", "fcmoe_decode_tail.hip", "fcmoe_router.hip", "fcmoe_probe.hip"]
+HIP_SOURCES = ["fcmoe_api.hip", "fcmoe_route.hip", "fcmoe_quant.hip", "fcmoe_gemm.hip", "fcmoe_gemm_lds.hip", "fcmoe_gemm_pipe.hip", "fcmoe_combine.hip", "fcmoe_decode_tail.hip", "fcmoe_router.hip"]
+# bench-only measurement probes: a library of their own (fcmoe_probe.h), linked against libfcmoe.so
+PROBE_SOURCES = ["fcmoe_probe.hip"]
 HIP_FLAGS = [
     f"--offload-arch={ARCH}",
     "-O3",
@@ -47,7 +51,12 @@ HIP_FLAGS = [
     "-packed-fp32-ops",
 ]
 
+# Sources whose MFMA accumulators live in AGPRs (one wave per SIMD, 192-256
+# accumulators per lane): built without the VGPR-form flag.
+AGPR_SOURCES = {"fcmoe_gemm_pipe.hip"}
+
 LIB = PKG / "libfcmoe.so"
+PROBE_LIB = PKG / "libfcmoe_probe.so"
 EXT = PKG / ("_moe_C" + sysconfig.get_config_var("EXT_SUFFIX"))
 BUILD_DIR = PKG / "_build"
 
@@ -79,16 +88,23 @@ def build_lib() -> Path:
 
     def compile_one(src: str) -> str:
         obj = BUILD_DIR / (src + ".o")
-        remarks = _run([hipcc, *HIP_FLAGS, "-Rpass-analysis=kernel-resource-usage", "-c", str(CSRC / src), "-o",
-                        str(obj)])
+        flags = HIP_FLAGS
+        if src in AGPR_SOURCES:
+            flags = [f for f in HIP_FLAGS if f not in ("-mllvm", "-amdgpu-mfma-vgpr-form=1")]
+        remarks = _run([hipcc, *flags, "-Rpass-analysis=kernel-resource-usage", "-c", str(CSRC / src), "-o", str(obj)])
         _check_no_scratch(src, remarks)
         return str(obj)
 
-    with ThreadPoolExecutor(max_workers=min(len(HIP_SOURCES), os.cpu_count() or 1)) as ex:
-        objs = list(ex.map(compile_one, HIP_SOURCES))
+    srcs = HIP_SOURCES + PROBE_SOURCES
+    with ThreadPoolExecutor(max_workers=min(len(srcs), os.cpu_count() or 1)) as ex:
+        objs = dict(zip(srcs, ex.map(compile_one, srcs)))
     tmp = LIB.with_suffix(".so.tmp")
-    _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *objs])
+    _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *[objs[s] for s in HIP_SOURCES]])
     os.replace(tmp, LIB)
+    tmp = PROBE_LIB.with_suffix(".so.tmp")
+    _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *[objs[s] for s in PROBE_SOURCES],
+          f"-L{PKG}", "-lfcmoe", "-Wl,-rpath,$ORIGIN"])
+    os.replace(tmp, PROBE_LIB)
     return LIB
 
 

@@ -80,11 +80,6 @@ SIGNATURES = {
     "fcmoe_grouped_gemm_workspace_bytes": (_SZ, [_I64, _I64]),
     "fcmoe_w8a8_stage_views": (_I, [ctypes.POINTER(MoeArgs), _P, _P, _P, _P, _P, _P, _P]),
     "fcmoe_bf16_stage_views": (_I, [ctypes.POINTER(MoeArgs), _I, _P, _P, _P]),
-    "fcmoe_probe_stream": (_I, [_P, _I64, _I, _I, _I, _I, _P, _P]),
-    "fcmoe_probe_mfma": (_I, [_I, _I, _I, _I, _P, _P]),
-    "fcmoe_probe_mix": (_I, [_P, _I64, _I, _I, _I, _I, _P, _P]),
-    "fcmoe_probe_fence": (_I, [_P, _I64, _I, _I, _I, _P, _P, _P]),
-    "fcmoe_probe_ring": (_I, [_P, _I64, _P, _I, _I, _I, _I, _P, _P]),
     "fcmoe_stage_timing_enable": (_I, [_I]),
     "fcmoe_stage_timing_read": (_I, [_P, _P]),
     "fcmoe_w8a8_prefill_plan": (_I, [_P, _P]),

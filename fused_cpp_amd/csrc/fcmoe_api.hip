@@ -248,6 +248,38 @@ int side_streams(SideStreams** out) {
 bool timing_on();
 int persistent_wgs();
 
+// Waits between two side streams under HIP graph capture are refused. The
+// launch plans here fork from the caller's stream and join back into it
+// only: every side stream waits on an event recorded on the caller's stream,
+// and the caller's stream waits on each side stream's join event. A dropped
+// form that also made one side stream wait on another's event ended a
+// capture with a host segmentation fault in hipStreamEndCapture (its other
+// changes were launches of kinds the kept plans capture without trouble);
+// fork_wait refuses that edge while the caller's stream is capturing, and
+// w8a8_run refuses a call that would add one before it enqueues anything.
+// FCMOE_SIDE_CHAIN_WAIT=1 adds such an edge to the W8A8 prefill fork (side
+// stream 1 waits for side stream 0's join event; harmless outside capture)
+// so that tests can reach the refusal.
+bool side_chain_wait() {
+  const char* v = getenv("FCMOE_SIDE_CHAIN_WAIT");
+  return v && v[0] == '1';
+}
+
+bool stream_capturing(hipStream_t stream) {
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  return hipStreamIsCapturing(stream, &st) == hipSuccess && st == hipStreamCaptureStatusActive;
+}
+
+// `waiter` waits for `ev`, last recorded on `recorded_on`; `caller` is the
+// forward's own stream.
+int fork_wait(hipStream_t waiter, hipEvent_t ev, hipStream_t recorded_on, hipStream_t caller) {
+  if (waiter != caller && recorded_on != caller && stream_capturing(caller))
+    return fail(FCMOE_EINVAL, "a wait between two side streams is refused under HIP graph capture");
+  if (hipStreamWaitEvent(waiter, ev, 0) != hipSuccess) return fail(FCMOE_EDEVICE, "stream wait failed");
+  return FCMOE_OK;
+}
+
+
 template <typename F>
 int run_classes(const TileClasses& tc, hipStream_t stream, F&& gemm, bool serial = false) {
   // Stage timing brackets each launch with events on its stream, so it runs
@@ -266,12 +298,12 @@ int run_classes(const TileClasses& tc, hipStream_t stream, F&& gemm, bool serial
   if (hipEventRecord(ss->fork, stream) != hipSuccess) return fail(FCMOE_EDEVICE, "hipEventRecord failed");
   if ((rc = gemm(tc.n - 1, stream))) return rc;
   for (int c = tc.n - 2; c >= 0; --c) {
-    if (hipStreamWaitEvent(ss->s[c], ss->fork, 0) != hipSuccess) return fail(FCMOE_EDEVICE, "stream wait failed");
+    if ((rc = fork_wait(ss->s[c], ss->fork, stream, stream))) return rc;
     if ((rc = gemm(c, ss->s[c]))) return rc;
     if (hipEventRecord(ss->join[c], ss->s[c]) != hipSuccess) return fail(FCMOE_EDEVICE, "hipEventRecord failed");
   }
   for (int c = tc.n - 2; c >= 0; --c)
-    if (hipStreamWaitEvent(stream, ss->join[c], 0) != hipSuccess) return fail(FCMOE_EDEVICE, "stream wait failed");
+    if ((rc = fork_wait(stream, ss->join[c], ss->s[c], stream))) return rc;
   return FCMOE_OK;
 }
 
@@ -522,7 +554,8 @@ int run_w8a8_stage(const TileClasses& tc, const RouteBuffers& rb, int epi, const
     constexpr int kSides = 3;
     for (int k = 0; k < kSides; ++k) {
       hipStream_t s = ss->s[k];
-      if (hipStreamWaitEvent(s, ss->fork, 0) != hipSuccess) return fail(FCMOE_EDEVICE, "stream wait failed");
+      if ((rc = fork_wait(s, ss->fork, stream, stream))) return rc;
+      if (k == 1 && side_chain_wait() && (rc = fork_wait(s, ss->join[0], ss->s[0], stream))) return rc;
       if (k == 0) {
         if ((rc = gemm_launch(epi, 16, ps, tc.bound[0], s))) return rc;
         if (with_classic && (rc = classic(0, s))) return rc;
@@ -533,7 +566,7 @@ int run_w8a8_stage(const TileClasses& tc, const RouteBuffers& rb, int epi, const
       if (hipEventRecord(ss->join[k], s) != hipSuccess) return fail(FCMOE_EDEVICE, "hipEventRecord failed");
     }
     for (int k = 0; k < kSides; ++k)
-      if (hipStreamWaitEvent(stream, ss->join[k], 0) != hipSuccess) return fail(FCMOE_EDEVICE, "stream wait failed");
+      if ((rc = fork_wait(stream, ss->join[k], ss->s[k], stream))) return rc;
     return FCMOE_OK;
   }
   // Outside the prefill class set: the classic launches only.
@@ -558,6 +591,8 @@ int w8a8_run(const fcmoe_moe_args* a, char* ws_base, size_t ws_bytes, bool seria
   if ((rc = check_common(a))) return rc;
   if (!a->w13_scale || !a->w2_scale) return fail(FCMOE_EINVAL, "W8A8 scales are NULL");
   if (a->tokens == 0) return FCMOE_OK;
+  if (!serial_classes && !timing_on() && side_chain_wait() && stream_capturing(stream))
+    return fail(FCMOE_EINVAL, "a wait between two side streams is refused under HIP graph capture");
   Arena ar;
   ar.base = ws_base;
   ar.cap = ws_bytes;
@@ -566,7 +601,11 @@ int w8a8_run(const fcmoe_moe_args* a, char* ws_base, size_t ws_bytes, bool seria
   if (!ar.ok()) return fail(FCMOE_ESPACE, "W8A8 workspace too small");
   const int64_t H = a->hidden, I = a->inter;
   const int64_t parts = ceil_div(I, 16);
-  const bool tail = a->tokens <= decode_tail_max_tokens() && L.kt <= kDecodeTailSlots && parts <= 128;
+  // the fused tail's whole launch domain (decode_tail_launch refuses anything
+  // else), so that a larger FCMOE_DECODE_TAIL_MAX_T falls back to the unfused
+  // launches instead of failing
+  const bool tail = a->tokens <= decode_tail_max_tokens() && a->tokens <= 65535 && L.kt <= kDecodeTailSlots &&
+                    parts <= 2 * kWave && H > 0;
   auto decode_tail = [&]() {
     // requant + W2 + merge in one launch (timed as the W2 16-row stage)
     DecodeTailArgs d{};
@@ -989,6 +1028,7 @@ int i8gemm_run(const I8Layout& L, int64_t k, const void* w_packed, const float* 
     GemmParams p = g;
     p.tiles = L.tiles + 2 * tile_offset(L.tc, c);
     p.tile_count = L.tile_count + c;
+    Stage st(FCMOE_STAGE_W13_CLASS0 + class_slot(L.tc.bm[c]), stream);
     const int rc = gemm_launch(kEpiI8Gemm, L.tc.bm[c], p, L.tc.bound[c], stream);
     if (rc) return rc;
   }
@@ -1003,8 +1043,11 @@ int i8gemm_prologue(const void* x, int x_is_f32, int64_t m, int64_t k, void* wor
   ar.cap = workspace_bytes;
   *L = i8_layout(m, k, ar);
   if (!ar.base || !ar.ok()) return fail(FCMOE_ESPACE, "i8gemm: workspace too small");
-  int rc = quant_rows_launch(x, x_is_f32, m, k, 1, L->xq, L->kp, L->xs, stream);
-  if (rc) return rc;
+  int rc;
+  {
+    Stage st(FCMOE_STAGE_QUANT, stream);
+    if ((rc = quant_rows_launch(x, x_is_f32, m, k, 1, L->xq, L->kp, L->xs, stream))) return rc;
+  }
   hipLaunchKernelGGL(single_expert_counts_kernel, dim3(1), dim3(1), 0, stream, L->counts, L->offsets, (int32_t)m);
   if ((rc = check_launch("i8gemm counts"))) return rc;
   return tiles_from_counts_launch(L->counts, 1, L->tc, L->tiles, L->tile_count, stream);

@@ -7,7 +7,7 @@
 // products route*w, then adjacent-pair additions splitting each range at its
 // largest power of two below its length, ((0+1)+(2+3))+(4+5) for 6
 // (csrc/moe/arm/sve_bf16/route_merge.cpp:47-86). skip_weighted copies the
-// single route (naive.py:392-393). One thread per output element: consecutive
+// single route (naive.py:259-261). One thread per output element: consecutive
 // threads read consecutive h of each route row (HBM-bound, coalesced).
 #include "fcmoe_device.h"
 #include "fcmoe_internal.h"

@@ -3,11 +3,14 @@
 // MFMA + LDS-fragment loop rate by wave tile and waves per SIMD, a CU running
 // MFMA waves and streaming waves side by side, and the cost of one agent-scope
 // release per workgroup. Each entry enqueues one launch on `stream`; the
-// caller times it (bench.py --probe). None of them is on the operators' path.
+// caller times it (bench.py --probe). None of them is on the operators' path:
+// this file builds into libfcmoe_probe.so (declared in fcmoe_probe.h), which
+// only the benchmark loads, not into libfcmoe.so.
 #include <stdint.h>
 
 #include "fcmoe_device.h"
 #include "fcmoe_internal.h"
+#include "fcmoe_probe.h"
 
 namespace fcmoe {
 namespace {
@@ -290,10 +293,12 @@ extern "C" int fcmoe_probe_fence(const void* src, int64_t src_bytes, int workgro
   return check_launch("probe_fence");
 }
 
-extern "C" int fcmoe_probe_ring(const void* src, int64_t src_bytes, const void* arows, int workgroups, int lookahead,
-                                int a_loads, int barrier, int* sink, hipStream_t stream) {
+extern "C" int fcmoe_probe_ring(const void* src, int64_t src_bytes, const void* arows, int64_t arows_bytes,
+                                int workgroups, int lookahead, int a_loads, int barrier, int* sink,
+                                hipStream_t stream) {
   if (!src || !arows || !sink || workgroups <= 0) return fail(FCMOE_EINVAL, "probe_ring: bad arguments");
-  // arows: at least 16 MiB (a 2 MiB window per XCD)
+  // the kernel reads a 2 MiB window of arows per XCD: 16 MiB in all
+  if (arows_bytes < ((int64_t)16 << 20)) return fail(FCMOE_EINVAL, "probe_ring: arows must hold at least 16 MiB");
   const int64_t chunks = src_bytes / ((int64_t)workgroups * 8 * 4 * 1024);
   if (chunks < 8 || chunks * 8 * 4 * 1024 > 0x7ffffff0) return fail(FCMOE_EINVAL, "probe_ring: bad source size");
   const dim3 g((unsigned)workgroups), b(512);

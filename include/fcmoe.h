@@ -226,47 +226,6 @@ int fcmoe_w8a8_stage_views(const fcmoe_moe_args* args, const int32_t** sorted_ro
 int fcmoe_bf16_stage_views(const fcmoe_moe_args* args, int w8a16, const int32_t** route_pos,
                            const float** route_weight, const float** route_out);
 
-/* ---- measurement probes ------------------------------------------------ */
-
-/* Microbenchmarks behind the chip figures the design relies on (no
- * counterpart in the reference; bench.py --probe times them with events on
- * `stream`). Each enqueues one launch and returns at once. `sink` is a device
- * int32 buffer the kernels only write on an impossible condition.
- * _stream: `workgroups` x `waves` waves each stream src_bytes / (workgroups x
- *   waves) bytes (whole KiB, at least 8) of `src`: mode 0 nontemporal 16-byte
- *   loads to VGPRs (8-deep ring), mode 1 buffer_load ... lds into an 8 KiB
- *   per-wave LDS ring; lds_pad_bytes of dynamic LDS per workgroup (at least
- *   waves x 8 KiB in mode 1) limits the workgroups per CU.
- * _mfma: `workgroups` workgroups of `waves` waves, each looping `iters` times
- *   over (tile rows + channels) / 16 LDS fragment reads and the
- *   v_mfma_i32_16x16x64_i8 of one wave tile: tile 0 = 128x96 (waves 4 or 8),
- *   1 = 128x64 (8, 12), 2 = 96x80 (12), 3 = 64x96 (12), 4 = 64x64 (8, 16).
- * _mix: 256 workgroups (one per CU) of compute_waves MFMA + LDS-read waves
- *   (iters iterations of 2 reads and 7 MFMAs) and stream_waves waves that
- *   stream src_bytes / (256 x stream_waves) bytes each (accumulating with
- *   MFMAs when stream_mfma); compute_waves + stream_waves <= 16.
- * _fence: the mode-0 stream of _stream, then (release != 0) each wave stores
- *   1 KiB to `rows` ([workgroups x waves x 1 KiB]), issues an agent-scope
- *   release fence and the workgroup bumps counters[workgroup / 16] (zeroed
- *   by the caller); the 16th arrival of each group acquires and reads a
- *   neighbour's row.
- * _ring: the prefill GEMM's load mix without arithmetic: `workgroups`
- *   workgroups of 8 waves; per K chunk each wave loads 4 KiB of weights (a
- *   contiguous stream of src per workgroup) and a_loads KiB of A rows (8 rows
- *   x 128 bytes, 7168-byte stride, from a 2 MiB window of `arows` per XCD;
- *   arows >= 16 MiB) by buffer_load ... lds, keeping `lookahead` chunks in
- *   flight, with (barrier != 0) one workgroup barrier per chunk. Supported
- *   (lookahead, a_loads, barrier): (2,0,1), (2,2,1), (2,2,0), (4,2,1), (6,2,1). */
-int fcmoe_probe_stream(const void* src, int64_t src_bytes, int workgroups, int waves, int mode, int lds_pad_bytes,
-                       int* sink, hipStream_t stream);
-int fcmoe_probe_mfma(int tile, int waves, int workgroups, int iters, int* sink, hipStream_t stream);
-int fcmoe_probe_mix(const void* src, int64_t src_bytes, int compute_waves, int stream_waves, int iters,
-                    int stream_mfma, int* sink, hipStream_t stream);
-int fcmoe_probe_fence(const void* src, int64_t src_bytes, int workgroups, int waves, int release, int* counters,
-                      void* rows, hipStream_t stream);
-int fcmoe_probe_ring(const void* src, int64_t src_bytes, const void* arows, int workgroups, int lookahead, int a_loads,
-                     int barrier, int* sink, hipStream_t stream);
-
 /* W8A8 prefill launch plan for the route scan's tile counts per class
  * (class_tiles[0..3]: tiles of 16 / 128 / 192 / 256 rows), as the device
  * chooses it inside fcmoe_w8a8_forward (same environment overrides): returns
@@ -299,7 +258,10 @@ int fcmoe_w8a8_prefill_plan(const int32_t* class_tiles, int* part_wgs_out);
 #define FCMOE_STAGE_COUNT 24
 
 /* Per-stage GPU timing with hipEvents recorded on the launch stream around
- * each stage of fcmoe_w8a8_forward / fcmoe_bf16_forward: the device-side
+ * each stage of fcmoe_w8a8_forward / fcmoe_bf16_forward / fcmoe_w8a16_forward
+ * (fcmoe_i8gemm and _pair record their row quantisation as
+ * FCMOE_STAGE_QUANT and each GEMM launch under the W13 class of its tile
+ * rows): the device-side
  * counterpart of the reference's FUSED_CPP_MOE_STAGE_TIMING stderr timers
  * (csrc/moe/arm/common/fused_moe_bf16_tiled.cpp:6446, 7122-7131).
  * enable != 0 starts recording (the environment variable

@@ -13,7 +13,7 @@ Two parts:
 * ``router_topk``: numpy restatement of the caller-side router (softmax ->
   top-k -> renormalise -> scale) that produces the MoE op's ids and weights.
 * ``bf16_moe_reference``: an fp32 numpy restatement of the BF16 fused MoE
-  semantics of ``src/fused_cpp/moe/naive.py:309-422`` (grouped per-expert
+  semantics of ``src/fused_cpp/moe/naive.py:161-272`` (grouped per-expert
   linear, activation, weighted top-k sum) used as the tolerance reference.
 """
 
@@ -281,7 +281,7 @@ def _act_f32(gate_up: np.ndarray, mode: str) -> np.ndarray:
 def bf16_moe_reference(x: np.ndarray, w13: np.ndarray, w2: np.ndarray, topk_w: np.ndarray, ids: np.ndarray, *,
                        w13_bias=None, w2_bias=None, activation: str = "silu", skip_weighted: bool = False,
                        round_intermediate: bool = False) -> np.ndarray:
-    """fp32 restatement of fused_moe_naive (src/fused_cpp/moe/naive.py:309-422).
+    """fp32 restatement of fused_moe_naive (src/fused_cpp/moe/naive.py:161-272).
 
     x [T,H], w13 [E,2F,H], w2 [E,H,F] as float32 arrays (already bf16-valued);
     returns float32 [T,H] before the final bf16 cast. ``round_intermediate``

@@ -20,6 +20,14 @@ def bits_to_f32(b: np.ndarray) -> np.ndarray:
     return (np.asarray(b, np.uint16).astype(np.uint32) << 16).view(np.float32)
 
 
+def bf16_half_ulp(x: np.ndarray) -> np.ndarray:
+    """Half a bf16 ulp at each |x| (8 significant bits): the rounding error a
+    correctly rounded bf16 output already carries against an fp32 reference.
+    At |x| >= 8 it is 2^-5 = 0.031, above a 2e-2 absolute bound."""
+    _, e = np.frexp(np.abs(np.asarray(x, np.float64)))
+    return np.ldexp(1.0, e - 9)
+
+
 def softmax_topk(logits: np.ndarray, k: int, scale: float = 1.0, renorm: bool = True):
     """softmax -> top-k -> renormalise (-> scale): the router of BASELINE configs."""
     z = logits - logits.max(axis=1, keepdims=True)

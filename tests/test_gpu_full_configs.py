@@ -20,6 +20,7 @@ import pytest
 import torch
 
 import bench
+from tests import helpers as H
 
 pytestmark = pytest.mark.gpu
 
@@ -146,7 +147,14 @@ def test_bf16_full_config_c1_within_tolerance(gpu, oracle_lib):
     classes = _stage_classes(run)
     assert set(classes) == {"w13_bm16", "w2_bm16"}, classes
 
-    tok = np.array([0, 17, cfg["T"] - 1])
+    # 16+ tokens: a spread over the batch plus every token routed to the most-
+    # and to the least-loaded active routed expert
+    counts = np.bincount(ids.reshape(-1), minlength=cfg["E"])
+    active = np.nonzero(counts)[0]
+    hot, cold = active[np.argmax(counts[active])], active[np.argmin(counts[active])]
+    tok = np.unique(np.concatenate([np.linspace(0, cfg["T"] - 1, 14).astype(np.int64),
+                                    np.nonzero((ids == hot).any(1))[0], np.nonzero((ids == cold).any(1))[0]]))
+    assert len(tok) >= 16
     experts, local = _local(ids[tok], cfg["E"])
     sel = torch.from_numpy(experts).to(gpu)
     h13 = w13.index_select(0, sel).float().cpu().numpy()
@@ -157,11 +165,20 @@ def test_bf16_full_config_c1_within_tolerance(gpu, oracle_lib):
     w_c = np.concatenate([w[tok] * np.float32(cfg["scale"]), np.ones((T, 1), np.float32)], 1)
     ref = oracle_lib.bf16_moe_reference(xs, h13, h2, w_c, ids_c)
     got = out[torch.from_numpy(tok).to(gpu)].float().cpu().numpy()
-    err = np.abs(got - ref).max() / max(1.0, np.abs(ref).max())
+    diff = np.abs(got.astype(np.float64) - ref)
+    abs_err = float(diff.max())
+    # error beyond the bf16 output's own rounding (half an ulp of the value):
+    # outputs here reach |y| ~ 11, where that rounding alone is 0.031
+    excess = float((diff - H.bf16_half_ulp(ref)).max())
+    err = abs_err / max(1.0, np.abs(ref).max())
     cos = float((got * ref).sum() / np.sqrt((got * got).sum() * (ref * ref).sum()))
-    print(f"[full-config] c1: tokens {tok.tolist()} max-abs/scale {err:.3e} cosine {cos:.7f}", flush=True)
-    # north-star tolerance against the fp32 reference
-    assert err <= 2e-2 and cos >= 0.9999, (err, cos)
+    print(f"[full-config] c1: {len(tok)} tokens (hot expert {hot}: {counts[hot]} routes, cold {cold}: "
+          f"{counts[cold]}) max-abs {abs_err:.3e} (beyond bf16 output rounding {excess:.3e}) "
+          f"max-abs/scale {err:.3e} cosine {cos:.7f}", flush=True)
+    # north-star tolerance against the fp32 reference: max-abs <= 2e-2 on top of
+    # the bf16 output rounding, cosine >= 0.9999 (and the scaled form the other
+    # BF16 tests use)
+    assert excess <= 2e-2 and err <= 2e-2 and cos >= 0.9999, (abs_err, excess, err, cos)
     del weights, w13, w2, out
     _free()
 

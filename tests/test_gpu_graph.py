@@ -195,3 +195,63 @@ def test_w8a8_prefill_mixed_plan_graph_replays(gpu, min_tiles):
             del os.environ["FCMOE_PREFILL_MIXED_MIN_TILES"]
         else:
             os.environ["FCMOE_PREFILL_MIXED_MIN_TILES"] = old
+
+
+def test_side_to_side_stream_wait_refused_under_capture(gpu):
+    """The prefill fork joins side streams only through the caller's stream;
+    a wait of one side stream on another's event (FCMOE_SIDE_CHAIN_WAIT=1 adds
+    one) runs eagerly, bit-exact with the default fork, and is refused under
+    graph capture before the forward enqueues anything (the capture then ends
+    empty and replays nothing)."""
+    import os
+
+    from fused_cpp_amd import moe
+
+    T, Hd, F, E, k = 2048, 1024, 512, 160, 6
+    x, ids, w, q13, s13, q2, s2 = H.w8a8_case(31, T, Hd, F, E + 1, k, skew=1.2)
+    ids = np.minimum(ids, E - 1)
+    t = torch.from_numpy
+    prepared = moe.prepare_routed_shared_moe_w8a8_tiled_quantized_weights(
+        t(q13[:-1]), t(s13[:-1]), t(q2[:-1]), t(s2[:-1]), t(q13[-1]), t(s13[-1]), t(q2[-1]), t(s2[-1]))
+    xd = torch.from_numpy(x.view(np.int16)).to(gpu).view(torch.bfloat16)
+    wd, idd = torch.from_numpy(w).to(gpu), torch.from_numpy(ids).to(gpu)
+
+    def fn(out=None):
+        return moe.fused_moe_w8a8_tiled_with_shared(xd, prepared, wd, idd, routed_scaling_factor=2.5, out=out)
+
+    ref = fn()
+    torch.cuda.synchronize()
+    old = os.environ.get("FCMOE_SIDE_CHAIN_WAIT")
+    os.environ["FCMOE_SIDE_CHAIN_WAIT"] = "1"
+    try:
+        chained = fn()
+        torch.cuda.synchronize()
+        assert torch.equal(chained, ref)
+        static = torch.zeros_like(ref)
+        g = torch.cuda.CUDAGraph()
+        with pytest.raises(RuntimeError, match="refused under HIP graph capture"):
+            with torch.cuda.graph(g):
+                fn(out=static)
+        torch.cuda.synchronize()
+    finally:
+        if old is None:
+            del os.environ["FCMOE_SIDE_CHAIN_WAIT"]
+        else:
+            os.environ["FCMOE_SIDE_CHAIN_WAIT"] = old
+    # nothing was captured: the output buffer is untouched, and the default
+    # fork still captures and replays
+    assert not static.any()
+    g2 = torch.cuda.CUDAGraph()
+    static2 = torch.zeros_like(ref)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn(out=static2)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g2):
+        fn(out=static2)
+    static2.zero_()
+    g2.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(static2, ref)

@@ -325,3 +325,22 @@ def test_w8a8_prefill_plan_choice(monkeypatch):
     assert cabi.w8a8_prefill_plan([0, 0, 364, 52]) == ("mixed", 0)
     with pytest.raises(RuntimeError):
         cabi.check(cabi.lib().fcmoe_w8a8_prefill_plan(None, None), "plan")
+
+
+def test_bf16_half_ulp_bounds_bf16_rounding():
+    """The allowance the BF16 tolerance checks add for the output's own
+    rounding: it bounds |bf16(x) - x| (round to nearest even, the oracle's
+    converter) and is reached, i.e. it is exactly half a bf16 ulp."""
+    import numpy as np
+
+    import oracle
+    from tests import helpers as H
+
+    rng = np.random.default_rng(3)
+    x = (rng.standard_normal(200000) * np.exp(rng.uniform(-6, 6, 200000))).astype(np.float32)
+    r = H.bits_to_f32(oracle.f32_to_bf16_bits(x)).astype(np.float64)
+    err = np.abs(r - x.astype(np.float64))
+    half = H.bf16_half_ulp(x)
+    assert (err <= half).all()
+    assert (err / half).max() > 0.999
+    assert H.bf16_half_ulp(np.array([1.0, 10.0, 0.75]))[1] == 2.0 ** -5

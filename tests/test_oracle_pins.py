@@ -324,7 +324,7 @@ def test_bf16_activation_within_one_ulp_of_float64(oracle_lib, mode):
 
 
 def test_bf16_reference_matches_per_token_brute_force(oracle_lib):
-    """Grouped numpy reference == per-token float64 loops (naive.py:309-422 semantics)."""
+    """Grouped numpy reference == per-token float64 loops (naive.py:161-272 semantics)."""
     rng = np.random.default_rng(4)
     T, Hd, F, E, k = 37, 13, 11, 4, 2
     x = rng.standard_normal((T, Hd)).astype(np.float32)

@@ -32,7 +32,7 @@ CSRC = PKG / "csrc"
 ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 ARCH = os.environ.get("FCMOE_OFFLOAD_ARCH", "gfx950")
 
-HIP_SOURCES = ["fcmoe_api.hip", "fcmoe_route.hip", "fcmoe_quant.hip", "fcmoe_gemm.hip", "fcmoe_gemm_lds.hip", "fcmoe_gemm_pipe.hip", "fcmoe_combine.hip", "fcmoe_decode_tail.hip", "fcmoe_router.hip"]
+HIP_SOURCES = ["fcmoe_api.hip", "fcmoe_route.hip", "fcmoe_quant.hip", "fcmoe_gemm.hip", "fcmoe_gemm_lds.hip", "fcmoe_combine.hip", "fcmoe_decode_tail.hip", "fcmoe_router.hip"]
 # bench-only measurement probes: a library of their own (fcmoe_probe.h), linked against libfcmoe.so
 PROBE_SOURCES = ["fcmoe_probe.hip"]
 HIP_FLAGS = [
@@ -50,10 +50,6 @@ HIP_FLAGS = [
     "-Xclang",
     "-packed-fp32-ops",
 ]
-
-# Sources whose MFMA accumulators live in AGPRs (one wave per SIMD, 192-256
-# accumulators per lane): built without the VGPR-form flag.
-AGPR_SOURCES = {"fcmoe_gemm_pipe.hip"}
 
 LIB = PKG / "libfcmoe.so"
 PROBE_LIB = PKG / "libfcmoe_probe.so"
@@ -88,10 +84,8 @@ def build_lib() -> Path:
 
     def compile_one(src: str) -> str:
         obj = BUILD_DIR / (src + ".o")
-        flags = HIP_FLAGS
-        if src in AGPR_SOURCES:
-            flags = [f for f in HIP_FLAGS if f not in ("-mllvm", "-amdgpu-mfma-vgpr-form=1")]
-        remarks = _run([hipcc, *flags, "-Rpass-analysis=kernel-resource-usage", "-c", str(CSRC / src), "-o", str(obj)])
+        remarks = _run([hipcc, *HIP_FLAGS, "-Rpass-analysis=kernel-resource-usage", "-c", str(CSRC / src), "-o",
+                        str(obj)])
         _check_no_scratch(src, remarks)
         return str(obj)
 

@@ -197,9 +197,6 @@ __device__ __forceinline__ bool plan_open(const GemmParams& p) {
 }
 
 int gemm_launch(int epi, int bm, const GemmParams& p, int64_t max_tiles, hipStream_t stream);
-// The persistent 256 x 256 W8A8 GEMM at one wave per SIMD
-// (fcmoe_gemm_pipe.hip): epi kEpiW13SwigluI8 or kEpiW2RouteI8, p.persist > 0.
-int gemm_pipe_launch(int epi, const GemmParams& p, int64_t max_tiles, hipStream_t stream);
 // LDS-staged kernel for bm in {128, 192, 256} (fcmoe_gemm_lds.hip); gemm_launch
 // dispatches to it unless FCMOE_GEMM_LDS=0.
 int gemm_lds_launch(int epi, int bm, const GemmParams& p, int64_t max_tiles, hipStream_t stream);

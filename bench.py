@@ -858,7 +858,7 @@ def measure_op(wl: str, op: str, M: int, K: int, Ns, args, device, want_cpu: boo
         entry.update({"workload": f"BF16 shared MLP (one dense SwiGLU expert), T={M}, H={K}, I={I}",
                       "dtype": "bf16", "tokens_per_s": round(M / (ms * 1e-3), 1)})
         roof = _op_roofline(stages, steps, gemm, alg_b, alg_o, BF16_PEAK_TFLOPS, "grouped_gemm (W13 + W2 launches)")
-        tok = np.array([0, 1, M // 2, M - 1])
+        tok = np.unique(np.array([0, 1, M // 2, M - 1]).clip(0, M - 1))
         xs = x[torch.from_numpy(tok).to(device)].float().cpu().numpy()
         ref = oracle.bf16_moe_reference(xs, w13.float().cpu().numpy(), w2.float().cpu().numpy(),
                                         np.ones((len(tok), 1), np.float32), np.zeros((len(tok), 1), np.int64))
@@ -902,7 +902,7 @@ def measure_op(wl: str, op: str, M: int, K: int, Ns, args, device, want_cpu: boo
                                   f"x [{M}, {K}] bf16 against {shape} int8, bf16 out",
                       "dtype": "int8", "rows_per_s": round(M / (ms * 1e-3), 1)})
         roof = _op_roofline(stages, steps, gemm, alg_b, alg_o, INT8_PEAK_TOPS, "grouped_gemm (i8gemm GEMM launches)")
-        rows = np.array([0, 1, M // 2, M - 1])
+        rows = np.unique(np.array([0, 1, M // 2, M - 1]).clip(0, M - 1))
         xr = x[torch.from_numpy(rows).to(device)].cpu().view(torch.int16).numpy().view(np.uint16)
         ok = True
         for (w, sc), o in zip(ws, outs):

@@ -32,7 +32,7 @@ CSRC = PKG / "csrc"
 ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 ARCH = os.environ.get("FCMOE_OFFLOAD_ARCH", "gfx950")
 
-HIP_SOURCES = ["fcmoe_api.hip", "fcmoe_route.hip", "fcmoe_quant.hip", "fcmoe_gemm.hip", "fcmoe_gemm_lds.hip", "fcmoe_combine.hip", "fcmoe_decode_tail.hip", "fcmoe_router.hip"]
+HIP_SOURCES = ["fcmoe_api.hip", "fcmoe_route.hip", "fcmoe_quant.hip", "fcmoe_gemm.hip", "fcmoe_gemm_lds.hip", "fcmoe_gemm_smallm.hip", "fcmoe_combine.hip", "fcmoe_decode_tail.hip", "fcmoe_router.hip"]
 # bench-only measurement probes: a library of their own (fcmoe_probe.h), linked against libfcmoe.so
 PROBE_SOURCES = ["fcmoe_probe.hip"]
 HIP_FLAGS = [

@@ -73,7 +73,8 @@ SIGNATURES = {
     "fcmoe_bf16_forward": (_I, [ctypes.POINTER(MoeArgs), _P]),
     "fcmoe_w8a16_workspace_bytes": (_SZ, [ctypes.POINTER(MoeArgs)]),
     "fcmoe_w8a16_forward": (_I, [ctypes.POINTER(MoeArgs), _P]),
-    "fcmoe_i8gemm_workspace_bytes": (_SZ, [_I64, _I64]),
+    "fcmoe_i8gemm_workspace_bytes": (_SZ, [_I64, _I64, _I64]),
+    "fcmoe_i8gemm_pair_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64]),
     "fcmoe_i8gemm": (_I, [_P, _I, _I64, _I64, _P, _P, _I64, _P, _P, _I, _P, _SZ, _P]),
     "fcmoe_i8gemm_pair": (_I, [_P, _I64, _I64, _P, _P, _I64, _P, _P, _I64, _P, _P, _P, _SZ, _P]),
     "fcmoe_grouped_gemm_i8_acc": (_I, [_P, _I64, _P, _P, _P, _I64, _I64, _P, _I64, _I64, _P, _P, _SZ, _P]),

@@ -49,8 +49,24 @@ int class_slot(int bm) {
 constexpr int kPrefillClassBM[] = {16, 128, 192, 256};
 constexpr int kNumPrefillClasses = 4;
 
+// Few rows in all (a dense MLP or i8gemm at decode batch sizes, a small MoE
+// batch): the 16-row class, whose one- or eight-wave workgroups spread the
+// weight stream over every CU. A larger class would give one workgroup per
+// channel block and row tile, e.g. 8 for the DSv3 shared MLP at 64 rows on
+// the 128-row tile; the 16-row tiles of one expert re-read its weights, which
+// the tiles running side by side find in L2 / Infinity Cache.
+// FCMOE_SMALL_ROWS overrides the bound (read on every call).
+int64_t small_rows() {
+  const char* v = getenv("FCMOE_SMALL_ROWS");
+  return v && v[0] ? atoll(v) : 64;
+}
+
+bool decode_rows(int64_t routes, int64_t experts) {
+  return routes <= kDecodeRowsPerExpert * experts || routes <= small_rows();
+}
+
 TileClasses select_classes(int64_t routes, int64_t experts) {
-  if (routes <= kDecodeRowsPerExpert * experts) return make_tile_classes(kClassBM, 1, routes, experts);
+  if (decode_rows(routes, experts)) return make_tile_classes(kClassBM, 1, routes, experts);
   return make_tile_classes(kPrefillClassBM, kNumPrefillClasses, routes, experts);
 }
 
@@ -144,7 +160,7 @@ Bf16Layout bf16_layout(const fcmoe_moe_args* a, Arena& ar, bool w8 = false) {
                       fcmoe_packed_expert_bytes(1, a->hidden, a->inter, 1) < kLdsMaxABytes;
   if (w8)
     L.tc = make_tile_classes(kClassBMW8,
-                             L.routes <= kDecodeRowsPerExpert * a->experts ? 1 : (w8_lds ? kNumClassesW8 : 2),
+                             decode_rows(L.routes, a->experts) ? 1 : (w8_lds ? kNumClassesW8 : 2),
                              L.routes, a->experts);
   else
     L.tc = select_classes(L.routes, a->experts);
@@ -976,12 +992,16 @@ struct I8Layout {
   int32_t* offsets;
   int32_t* tiles;
   int32_t* tile_count;
+  int32_t* partial;  // small-M K splits' partial sums (empty with one split)
+  size_t partial_bytes;
 };
-I8Layout i8_layout(int64_t m, int64_t k, Arena& ar) {
+// partial_bytes: room for the small-M GEMMs' partial sums (the largest of the
+// GEMMs that run on this layout)
+I8Layout i8_layout(int64_t m, int64_t k, size_t partial_bytes, Arena& ar) {
   I8Layout L;
   L.m = m;
   L.kp = round_up(k, 64);
-  L.tc = make_tile_classes(kClassBM, kNumClasses, m, 1);
+  L.tc = make_tile_classes(kClassBM, decode_rows(m, 1) ? 1 : kNumClasses, m, 1);
   L.xq = ar.take<int8_t>(m * L.kp);
   L.xs = ar.take<float>(m);
   L.counts = ar.take<int32_t>(1);
@@ -990,13 +1010,22 @@ I8Layout i8_layout(int64_t m, int64_t k, Arena& ar) {
   for (int c = 0; c < L.tc.n; ++c) t += L.tc.bound[c];
   L.tiles = ar.take<int32_t>(2 * t);
   L.tile_count = ar.take<int32_t>(kMaxClasses);
+  L.partial = ar.take<int32_t>(partial_bytes / sizeof(int32_t));
+  L.partial_bytes = partial_bytes;
   return L;
 }
 }  // namespace
 
-extern "C" size_t fcmoe_i8gemm_workspace_bytes(int64_t m, int64_t k) {
+extern "C" size_t fcmoe_i8gemm_workspace_bytes(int64_t m, int64_t k, int64_t n) {
   Arena ar;
-  i8_layout(m, k, ar);
+  i8_layout(m, k, smallm_workspace_bytes(m, k, n), ar);
+  return ar.used + 256;
+}
+
+extern "C" size_t fcmoe_i8gemm_pair_workspace_bytes(int64_t m, int64_t k, int64_t n1, int64_t n2) {
+  const size_t p1 = smallm_workspace_bytes(m, k, n1), p2 = smallm_workspace_bytes(m, k, n2);
+  Arena ar;
+  i8_layout(m, k, p1 > p2 ? p1 : p2, ar);
   return ar.used + 256;
 }
 
@@ -1005,6 +1034,11 @@ namespace {
 // One int8 GEMM of the quantised rows in L against a packed [n, k] weight.
 int i8gemm_run(const I8Layout& L, int64_t k, const void* w_packed, const float* w_scale, int64_t n, const float* bias,
                void* out, int out_is_bf16, hipStream_t stream) {
+  if (smallm_splits(L.m, k, n) > 0) {
+    Stage st(FCMOE_STAGE_W13_CLASS0 + class_slot(16), stream);
+    return smallm_i8gemm_launch(L.xq, L.kp, L.m, k, w_packed, L.xs, w_scale, n, bias, out, out_is_bf16, L.partial,
+                                L.partial_bytes, stream);
+  }
   GemmParams g{};
   g.a = L.xq;
   g.lda = L.kp;
@@ -1036,18 +1070,19 @@ int i8gemm_run(const I8Layout& L, int64_t k, const void* w_packed, const float* 
 }
 
 // Row quantisation (ties to even) and the single-expert tile list.
-int i8gemm_prologue(const void* x, int x_is_f32, int64_t m, int64_t k, void* workspace, size_t workspace_bytes,
-                    I8Layout* L, hipStream_t stream) {
+int i8gemm_prologue(const void* x, int x_is_f32, int64_t m, int64_t k, size_t partial_bytes, void* workspace,
+                    size_t workspace_bytes, I8Layout* L, hipStream_t stream) {
   Arena ar;
   ar.base = (char*)workspace;
   ar.cap = workspace_bytes;
-  *L = i8_layout(m, k, ar);
+  *L = i8_layout(m, k, partial_bytes, ar);
   if (!ar.base || !ar.ok()) return fail(FCMOE_ESPACE, "i8gemm: workspace too small");
   int rc;
   {
     Stage st(FCMOE_STAGE_QUANT, stream);
     if ((rc = quant_rows_launch(x, x_is_f32, m, k, 1, L->xq, L->kp, L->xs, stream))) return rc;
   }
+  if (smallm_splits(m, k, 1) > 0) return FCMOE_OK;  // the small-M GEMM needs no tile list
   hipLaunchKernelGGL(single_expert_counts_kernel, dim3(1), dim3(1), 0, stream, L->counts, L->offsets, (int32_t)m);
   if ((rc = check_launch("i8gemm counts"))) return rc;
   return tiles_from_counts_launch(L->counts, 1, L->tc, L->tiles, L->tile_count, stream);
@@ -1062,7 +1097,7 @@ extern "C" int fcmoe_i8gemm(const void* x, int x_is_f32, int64_t m, int64_t k, c
   if (m == 0) return FCMOE_OK;
   if (m > INT32_MAX / 2) return fail(FCMOE_EINVAL, "i8gemm: too many rows");
   I8Layout L;
-  int rc = i8gemm_prologue(x, x_is_f32, m, k, workspace, workspace_bytes, &L, stream);
+  int rc = i8gemm_prologue(x, x_is_f32, m, k, smallm_workspace_bytes(m, k, n), workspace, workspace_bytes, &L, stream);
   if (rc) return rc;
   return i8gemm_run(L, k, w_packed, w_scale, n, bias, out, out_is_bf16, stream);
 }
@@ -1076,7 +1111,8 @@ extern "C" int fcmoe_i8gemm_pair(const uint16_t* x, int64_t m, int64_t k, const 
   if (m > INT32_MAX / 2) return fail(FCMOE_EINVAL, "i8gemm_pair: too many rows");
   if (!x || !out1 || !out2) return fail(FCMOE_EINVAL, "i8gemm_pair: NULL tensor");
   I8Layout L;
-  int rc = i8gemm_prologue(x, 0, m, k, workspace, workspace_bytes, &L, stream);
+  const size_t p1 = smallm_workspace_bytes(m, k, n1), p2 = smallm_workspace_bytes(m, k, n2);
+  int rc = i8gemm_prologue(x, 0, m, k, p1 > p2 ? p1 : p2, workspace, workspace_bytes, &L, stream);
   if (rc) return rc;
   if ((rc = i8gemm_run(L, k, w1_packed, w1_scale, n1, nullptr, out1, 1, stream))) return rc;
   return i8gemm_run(L, k, w2_packed, w2_scale, n2, nullptr, out2, 1, stream);

@@ -1,0 +1,249 @@
+// fcmoe_gemm_smallm.hip -- i8gemm at few rows (M <= 64), weight streaming.
+//
+// At decode batch sizes an i8gemm is a weight stream: DeepSeek's attention
+// output projection at 64 rows reads 117 MB of int8 weights for 15 GOP. The
+// row-tiled grouped GEMM gives such a product one workgroup per channel block
+// (28 workgroups for a [7168, 16384] weight on the 64-row tile), or re-reads
+// the weights for every 16-row tile. Here:
+//   * a workgroup is 8 waves, one 16-channel weight tile each, over a range
+//     of K chunks; every wave holds all M rows (FM = ceil(M / 16) row
+//     fragments of v_mfma_i32_16x16x64_i8), so each weight byte is read once;
+//   * the rows' 64-byte K chunk (FM KB) is staged in LDS by buffer_load ...
+//     lds and read by all 8 waves: A costs FM KB of L2 reads per 8 KB of
+//     weights;
+//   * each wave streams its tile's 1 KB chunks with nontemporal buffer loads
+//     into a register ring; A stages and weight chunks are issued in pairs, kSmDepth
+//     - 1 pairs ahead;
+//   * K is split over the grid's y dimension so that the launch has about one
+//     workgroup per CU; the splits' exact int32 partial sums go to a workspace
+//     and a second launch adds them (in split order; int32 sums are exact in
+//     any order) and applies the i8gemm epilogue. With one split the GEMM
+//     launch applies the epilogue itself.
+// The epilogue is write_scaled_output's (csrc/i8gemm.cpp:148-164):
+// (float)acc * s_x * s_w left to right, + bias, then bf16 (RNE) or fp32.
+#include <cstdlib>
+#include <utility>
+
+#include "fcmoe_gemm_common.h"
+
+namespace fcmoe {
+
+namespace {
+
+constexpr int kSmWaves = 8;  // waves per workgroup, one 16-channel tile each
+constexpr int kSmDepth = 8;  // ring depth: A stages (LDS) and weight chunks (registers)
+constexpr int kSmBufWord3 = 0x00020000;
+typedef __attribute__((address_space(3))) void* sm_lds_ptr;
+
+template <int N>
+__device__ __forceinline__ void sm_wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+struct SmallMArgs {
+  const int8_t* a;  // quantised rows [m, lda]
+  int64_t lda;      // bytes per row (a multiple of 64)
+  int m;
+  int64_t kc;       // 64-byte K chunks
+  int64_t cps;      // chunks per split (grid.y splits)
+  const void* w;    // packed [n_tiles][kc][64 lanes][16 B]
+  int64_t n, n_tiles;
+  const float* scale_row;  // [m]
+  const float* scale_col;  // [n]
+  const float* bias;       // [n] or null
+  void* out;
+  int out_bf16;
+  int64_t ldo;
+  int32_t* partial;  // [splits][m][n] when grid.y > 1, else null
+};
+
+__device__ __forceinline__ void sm_store(const SmallMArgs& p, int row, int64_t ch, int32_t acc) {
+  // write_scaled_output, csrc/i8gemm.cpp:148-164 (left to right)
+  float v = (float)acc * p.scale_row[row] * p.scale_col[ch];
+  if (p.bias) v = v + p.bias[ch];
+  if (p.out_bf16)
+    ((uint16_t*)p.out)[(int64_t)row * p.ldo + ch] = f32_to_bf16(v);
+  else
+    ((float*)p.out)[(int64_t)row * p.ldo + ch] = v;
+}
+
+template <int FM>
+__global__ __launch_bounds__(kSmWaves * kWave) void smallm_i8_kernel(SmallMArgs p) {
+#if __HIP_DEVICE_COMPILE__
+  constexpr int D = kSmDepth;
+  constexpr int ABYTES = FM * 1024;  // 16 FM rows x 64 bytes
+  __shared__ __attribute__((aligned(1024))) uint8_t sa[D * ABYTES];
+  const int lane = threadIdx.x % kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int64_t tile = (int64_t)blockIdx.x * kSmWaves + wave;
+  const bool tv = tile < p.n_tiles;
+  const int64_t c0 = (int64_t)blockIdx.y * p.cps;
+  const int64_t c1 = c0 + p.cps < p.kc ? c0 + p.cps : p.kc;
+  // 32-bit chunk counters keep the loop's compares scalar (a 64-bit compare
+  // took a VGPR with a load in flight and drained the ring every 8 chunks)
+  const int nch = (int)(c1 - c0);  // >= 1 (the host sizes the splits)
+
+  // A stage load of this wave: rows 16 g + lane / 4 with g = wave % FM (waves
+  // beyond FM repeat a load: same bytes to the same place, so every wave
+  // issues one A load per chunk and the wait counts are uniform). 16-byte
+  // unit u of row r sits at slot u ^ ((r >> 2) & 3): the 16 rows of a
+  // fragment read fall on distinct banks.
+  const int g = wave % FM;
+  const int ar = g * 16 + lane / 4;
+  const int aunit = (lane % 4) ^ ((lane >> 4) & 3);
+  const __amdgpu_buffer_rsrc_t rsrc_a =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(p.a), (short)0, 0x7ffffff0, kSmBufWord3);
+  const uint32_t voff_a = (uint32_t)((ar < p.m ? ar : p.m - 1) * p.lda + aunit * 16);
+  // The tile's weights through a buffer resource: the chunk offset goes in
+  // the scalar operand and the lane offset is fixed, so no address VGPR is
+  // computed per load (a 64-bit address written into a ring register with an
+  // older load pending made the compiler drain the ring).
+  const __amdgpu_buffer_rsrc_t rsrc_b = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)((const uint8_t*)p.w + (tv ? tile : 0) * p.kc * 1024), (short)0, (int)(p.kc * 1024), kSmBufWord3);
+  const int voff_b = lane * 16;
+  const int frag = (lane % 16) * 64 + (((lane / 16) ^ ((lane % 16) >> 2)) * 16);
+
+  v4i bq[D];
+  v4i acc[FM];
+#pragma unroll
+  for (int i = 0; i < FM; ++i) acc[i] = v4i{0, 0, 0, 0};
+
+  // pair t: A stage and weight chunk of the split's chunk t (past the end:
+  // the last chunk again, never consumed)
+  auto issue = [&](int t, auto slot_c) {
+    constexpr int slot = decltype(slot_c)::value;
+    const int64_t c = c0 + (t < nch ? t : nch - 1);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_a, (sm_lds_ptr)(sa + slot * ABYTES + g * 1024), 16, voff_a,
+                                             (int)(c * 64), 0, 0);
+    // keep each pair in issue order (A, then the weights): the wait counts
+    // below, and the compiler's own for the weight registers, assume it
+    __builtin_amdgcn_sched_barrier(0);
+    bq[slot] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rsrc_b, voff_b, (int)(c * 1024), 2));
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  [&]<int... S>(std::integer_sequence<int, S...>) {
+    (issue(S, std::integral_constant<int, S>{}), ...);
+  }(std::make_integer_sequence<int, D - 1>{});
+
+  auto body = [&](int t, auto slot_c) {
+    constexpr int slot = decltype(slot_c)::value;
+    // this wave's pair t has landed (pairs t+1 .. t+D-2 may not); after the
+    // barrier every wave's A stage t has, and no wave reads stage t-1 any more
+    sm_wait_vmcnt<2 * (D - 2)>();
+    __builtin_amdgcn_s_barrier();
+    issue(t + D - 1, std::integral_constant<int, (slot + D - 1) % D>{});
+    v4i af[FM];
+#pragma unroll
+    for (int i = 0; i < FM; ++i) af[i] = *(const v4i*)(sa + slot * ABYTES + i * 1024 + frag);
+#pragma unroll
+    for (int i = 0; i < FM; ++i) acc[i] = mfma(af[i], bq[slot], acc[i]);
+  };
+  // whole rings of D chunks, then the rest: no conditional step inside the
+  // loop, so the compiler's wait counts at the loop header match the steady
+  // state (a conditional step made it wait for all but the newest pair)
+  int t0 = 0;
+  for (; t0 + D <= nch; t0 += D) {
+    [&]<int... S>(std::integer_sequence<int, S...>) {
+      (body(t0 + S, std::integral_constant<int, S>{}), ...);
+    }(std::make_integer_sequence<int, D>{});
+  }
+  [&]<int... S>(std::integer_sequence<int, S...>) {
+    ((t0 + S < nch ? body(t0 + S, std::integral_constant<int, S>{}) : void()), ...);
+  }(std::make_integer_sequence<int, D>{});
+  sm_wait_vmcnt<0>();
+
+  if (!tv) return;
+  const int64_t ch = tile * 16 + lane % 16;
+  if (ch >= p.n) return;
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int row = i * 16 + (lane / 16) * 4 + q;
+      if (row >= p.m) continue;
+      if (p.partial)
+        p.partial[((int64_t)blockIdx.y * p.m + row) * p.n + ch] = acc[i][q];
+      else
+        sm_store(p, row, ch, acc[i][q]);
+    }
+#endif
+}
+
+// Adds the splits' partial sums (split order) and applies the epilogue; one
+// thread per output element, grid-stride.
+__global__ __launch_bounds__(256) void smallm_reduce_kernel(SmallMArgs p, int splits) {
+  const int64_t total = (int64_t)p.m * p.n;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (int64_t)gridDim.x * blockDim.x) {
+    int32_t acc = 0;
+    for (int s = 0; s < splits; ++s) acc += p.partial[(int64_t)s * total + e];
+    sm_store(p, (int)(e / p.n), e % p.n, acc);
+  }
+}
+
+}  // namespace
+
+int64_t smallm_splits(int64_t m, int64_t k, int64_t n) {
+  if (m <= 0 || m > kSmallMRows || k <= 0 || n <= 0) return 0;
+  const int64_t kc = ceil_div(k, 64);
+  const int64_t groups = ceil_div(ceil_div(n, 16), kSmWaves);
+  // workgroups (groups x splits) up to the target, at least 8 chunks per split
+  static const int64_t target = [] {
+    const char* v = getenv("FCMOE_SMALLM_WGS");
+    return v && v[0] ? (int64_t)atoll(v) : (int64_t)256;
+  }();
+  int64_t s = target / groups;
+  const int64_t smax = kc / 8 > 1 ? kc / 8 : 1;
+  if (s > smax) s = smax;
+  if (s < 1) s = 1;
+  const int64_t cps = ceil_div(kc, s);
+  return ceil_div(kc, cps);
+}
+
+size_t smallm_workspace_bytes(int64_t m, int64_t k, int64_t n) {
+  const int64_t s = smallm_splits(m, k, n);
+  return s > 1 ? (size_t)(s * m * n) * sizeof(int32_t) : 0;
+}
+
+int smallm_i8gemm_launch(const int8_t* a, int64_t lda, int64_t m, int64_t k, const void* w_packed,
+                         const float* scale_row, const float* scale_col, int64_t n, const float* bias, void* out,
+                         int out_bf16, int32_t* partial, size_t partial_bytes, hipStream_t stream) {
+  const int64_t splits = smallm_splits(m, k, n);
+  if (splits <= 0) return fail(FCMOE_EINVAL, "small-M i8gemm: shape outside its domain");
+  if (lda % 64 || lda < round_up(k, 64) || (int64_t)m * lda >= 0x7ffffff0)
+    return fail(FCMOE_EINVAL, "small-M i8gemm: bad row stride");
+  if (splits > 1 && (!partial || partial_bytes < smallm_workspace_bytes(m, k, n)))
+    return fail(FCMOE_ESPACE, "small-M i8gemm: partial-sum workspace too small");
+  SmallMArgs p{};
+  p.a = a;
+  p.lda = lda;
+  p.m = (int)m;
+  p.kc = ceil_div(k, 64);
+  p.cps = ceil_div(p.kc, splits);
+  p.w = w_packed;
+  p.n = n;
+  p.n_tiles = ceil_div(n, 16);
+  p.scale_row = scale_row;
+  p.scale_col = scale_col;
+  p.bias = bias;
+  p.out = out;
+  p.out_bf16 = out_bf16;
+  p.ldo = n;
+  p.partial = splits > 1 ? partial : nullptr;
+  const dim3 grid((unsigned)ceil_div(p.n_tiles, kSmWaves), (unsigned)splits), block(kSmWaves * kWave);
+  const int fm = (int)ceil_div(m, 16);
+  if (fm == 1)
+    hipLaunchKernelGGL(smallm_i8_kernel<1>, grid, block, 0, stream, p);
+  else if (fm == 2)
+    hipLaunchKernelGGL(smallm_i8_kernel<2>, grid, block, 0, stream, p);
+  else
+    hipLaunchKernelGGL(smallm_i8_kernel<4>, grid, block, 0, stream, p);
+  int rc = check_launch("smallm_i8gemm");
+  if (rc || splits == 1) return rc;
+  const int64_t total = m * n;
+  const unsigned blocks = (unsigned)(ceil_div(total, 256) < 4096 ? ceil_div(total, 256) : 4096);
+  hipLaunchKernelGGL(smallm_reduce_kernel, dim3(blocks), dim3(256), 0, stream, p, (int)splits);
+  return check_launch("smallm_reduce");
+}
+
+}  // namespace fcmoe

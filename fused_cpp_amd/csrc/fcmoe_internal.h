@@ -197,6 +197,17 @@ __device__ __forceinline__ bool plan_open(const GemmParams& p) {
 }
 
 int gemm_launch(int epi, int bm, const GemmParams& p, int64_t max_tiles, hipStream_t stream);
+
+// i8gemm at few rows (fcmoe_gemm_smallm.hip): m <= kSmallMRows, all rows per
+// wave, weights read once, K split over about one workgroup per CU.
+// smallm_splits: the K splits for a shape (0 outside the domain);
+// smallm_workspace_bytes: the splits' int32 partial sums (0 with one split).
+constexpr int64_t kSmallMRows = 64;
+int64_t smallm_splits(int64_t m, int64_t k, int64_t n);
+size_t smallm_workspace_bytes(int64_t m, int64_t k, int64_t n);
+int smallm_i8gemm_launch(const int8_t* a, int64_t lda, int64_t m, int64_t k, const void* w_packed,
+                         const float* scale_row, const float* scale_col, int64_t n, const float* bias, void* out,
+                         int out_bf16, int32_t* partial, size_t partial_bytes, hipStream_t stream);
 // LDS-staged kernel for bm in {128, 192, 256} (fcmoe_gemm_lds.hip); gemm_launch
 // dispatches to it unless FCMOE_GEMM_LDS=0.
 int gemm_lds_launch(int epi, int bm, const GemmParams& p, int64_t max_tiles, hipStream_t stream);

@@ -471,7 +471,7 @@ void i8gemm_dynamic_scaled_mm(at::Tensor output, at::Tensor input, at::Tensor pa
     TORCH_CHECK(bias->dim() == 1 && bias->size(0) == n, "i8gemm.dynamic_scaled_mm: bias must be shape [", n, "]");
     b = bias->to(input.device(), at::kFloat).contiguous();
   }
-  at::Tensor ws = workspace(fcmoe_i8gemm_workspace_bytes(m, k), input);
+  at::Tensor ws = workspace(fcmoe_i8gemm_workspace_bytes(m, k, n), input);
   pybind11::gil_scoped_release release;
   check_rc(fcmoe_i8gemm(input.data_ptr(), input.scalar_type() == at::kFloat ? 1 : 0, m, k, packed_weight.data_ptr(),
                         weight_scale.data_ptr<float>(), n, b.defined() ? b.data_ptr<float>() : nullptr,
@@ -499,7 +499,7 @@ void i8gemm_dynamic_scaled_mm_pair(at::Tensor out1, at::Tensor out2, at::Tensor 
                 " scale must be contiguous float32 [N]");
   }
   if (m == 0) return;
-  at::Tensor ws = workspace(fcmoe_i8gemm_workspace_bytes(m, k), input);
+  at::Tensor ws = workspace(fcmoe_i8gemm_pair_workspace_bytes(m, k, n1, n2), input);
   pybind11::gil_scoped_release release;
   check_rc(fcmoe_i8gemm_pair((const uint16_t*)input.data_ptr(), m, k, w1.data_ptr(), s1.data_ptr<float>(), n1,
                              w2.data_ptr(), s2.data_ptr<float>(), n2, (uint16_t*)out1.data_ptr(),

@@ -180,8 +180,10 @@ int fcmoe_w8a16_forward(const fcmoe_moe_args* args, hipStream_t stream);
  * n_groups 1), out = (float)acc * x_scale * w_scale[n] (+ bias[n]) stored as
  * bf16 (out_is_bf16) or fp32 [m, n]. Replaces i8gemm_dynamic_scaled_mm
  * (csrc/i8gemm.cpp:318-452) behind i8gemm.dynamic_scaled_mm
- * (src/fused_cpp/i8gemm.py:88-137). */
-size_t fcmoe_i8gemm_workspace_bytes(int64_t m, int64_t k);
+ * (src/fused_cpp/i8gemm.py:88-137). Workspace: fcmoe_i8gemm_workspace_bytes(m,
+ * k, n): at m <= 64 rows it includes the K splits' int32 partial sums
+ * (splits x m x n, none when one split covers K), so it depends on n. */
+size_t fcmoe_i8gemm_workspace_bytes(int64_t m, int64_t k, int64_t n);
 int fcmoe_i8gemm(const void* x, int x_is_f32, int64_t m, int64_t k, const void* w_packed, const float* w_scale,
                  int64_t n, const float* bias, void* out, int out_is_bf16, void* workspace, size_t workspace_bytes,
                  hipStream_t stream);
@@ -190,7 +192,10 @@ int fcmoe_i8gemm(const void* x, int x_is_f32, int64_t m, int64_t k, const void* 
  * activation quantisation (ties to even; scale = max|x|/127): out1 [m, n1]
  * and out2 [m, n2], no bias. Replaces i8gemm_dynamic_scaled_mm_pair
  * (csrc/i8gemm.cpp:453-570) behind i8gemm.dynamic_scaled_mm_pair
- * (src/fused_cpp/i8gemm.py:151-189). Workspace: fcmoe_i8gemm_workspace_bytes(m, k). */
+ * (src/fused_cpp/i8gemm.py:151-189). Workspace: fcmoe_i8gemm_pair_workspace_bytes
+ * (room for the larger of the two GEMMs' partial sums; they run one after
+ * the other on `stream`). */
+size_t fcmoe_i8gemm_pair_workspace_bytes(int64_t m, int64_t k, int64_t n1, int64_t n2);
 int fcmoe_i8gemm_pair(const uint16_t* x, int64_t m, int64_t k, const void* w1_packed, const float* w1_scale,
                       int64_t n1, const void* w2_packed, const float* w2_scale, int64_t n2, uint16_t* out1,
                       uint16_t* out2, void* workspace, size_t workspace_bytes, hipStream_t stream);

@@ -349,6 +349,40 @@ def test_i8gemm_bit_exact(gpu, oracle_lib, m, k, n, out_dtype):
         np.testing.assert_array_equal(got.numpy().view(np.uint32), ref.view(np.uint32))
 
 
+@pytest.mark.parametrize("m,k,n,bias,out_dtype", [
+    (1, 64, 16, True, torch.bfloat16),      # one row, one chunk, one tile
+    (7, 1000, 100, True, torch.float32),    # ragged K (padded chunk) and N (partial tile and workgroup)
+    (16, 8192, 1000, False, torch.bfloat16),  # K split 16 ways (partial sums + reduce launch)
+    (33, 1536, 4096, True, torch.bfloat16),   # three row fragments, a few splits
+    (64, 8192, 7168, False, torch.bfloat16),  # wo_b-like width, 5 splits
+    (64, 2048, 24576, False, torch.float32),  # many channel groups, one split
+])
+def test_i8gemm_small_m_split_k_bit_exact(gpu, oracle_lib, m, k, n, bias, out_dtype):
+    """i8gemm at <= 64 rows runs the small-M kernel (all rows per wave, K split
+    over the grid with int32 partial sums): bit-exact against the oracle, with
+    extreme int8 values and rows of zeros (scale 1)."""
+    from fused_cpp_amd import i8gemm
+
+    g = torch.Generator().manual_seed(m * 7 + k + n)
+    weight = torch.randint(-127, 128, (n, k), dtype=torch.int8, generator=g)
+    weight[0, :] = -128
+    weight_scale = torch.rand(n, dtype=torch.float32, generator=g) * 0.01 + 0.001
+    b = torch.randn(n, dtype=torch.float32, generator=g) if bias else None
+    x = (torch.randn(m, k, generator=g) * 3).to(torch.bfloat16)
+    x[0, : min(k, 5)] = 127.0
+    if m > 2:
+        x[2] = 0.0
+    packed = i8gemm.prepare(weight, weight_scale)
+    out = i8gemm.dynamic_scaled_mm(x.to(gpu), packed, bias=b.to(gpu) if bias else None, out_dtype=out_dtype)
+    ref = oracle_lib.i8gemm(x.view(torch.int16).numpy().view(np.uint16), weight.numpy(), weight_scale.numpy(),
+                            b.numpy() if bias else None, out_dtype == torch.bfloat16)
+    got = out.cpu()
+    if out_dtype == torch.bfloat16:
+        np.testing.assert_array_equal(got.view(torch.int16).numpy().view(np.uint16), ref)
+    else:
+        np.testing.assert_array_equal(got.numpy().view(np.uint32), ref.view(np.uint32))
+
+
 @pytest.mark.parametrize("kind", ["bf16", "w8a16"])
 def test_forward_activation_rows_beyond_2gib(gpu, oracle_lib, kind):
     """Maximum sizes: 150000 x 7168 bf16 token rows (2.15 GB) exceed the 2 GiB a

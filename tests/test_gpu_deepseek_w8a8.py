@@ -71,7 +71,8 @@ def test_wo_b_alias_out_and_bf16_prepare_quantises_like_the_oracle(gpu, oracle_l
     assert actual is out and torch.equal(actual, expected)
 
 
-@pytest.mark.parametrize("m,k,n1,n2", [(24, 64, 96, 128), (2, 64, 13, 21), (7, 7168, 1536, 512), (300, 1024, 80, 48)])
+@pytest.mark.parametrize("m,k,n1,n2", [(24, 64, 96, 128), (2, 64, 13, 21), (7, 7168, 1536, 512), (300, 1024, 80, 48),
+                                      (40, 2048, 2048, 512)])
 def test_pair_equals_two_single_projections(gpu, m, k, n1, n2):
     """tests/test_deepseek_v4_w8a8.py:62-96 (incl. logical N tails) plus DSv3 Q-projection widths."""
     from fused_cpp_amd.deepseek_v4_w8a8 import (deepseek_v4_w8a8_linear, deepseek_v4_w8a8_linear_pair,
@@ -90,6 +91,26 @@ def test_pair_equals_two_single_projections(gpu, m, k, n1, n2):
     assert torch.equal(b, deepseek_v4_w8a8_linear(x.to(gpu), second))
     assert torch.equal(a.cpu(), _expected(x, w1, s1))
     assert torch.equal(b.cpu(), _expected(x, w2, s2))
+
+
+def test_pair_with_split_counts_differing_equals_singles(gpu):
+    """64 rows: the first GEMM (32768 channels: 256 workgroups of 8 tiles)
+    runs unsplit, the second (8192) splits K three ways and needs the
+    partial-sum workspace the first does not; the pair equals the two single
+    GEMMs bit for bit (each checked against the oracle elsewhere)."""
+    from fused_cpp_amd.deepseek_v4_w8a8 import (deepseek_v4_w8a8_linear, deepseek_v4_w8a8_linear_pair,
+                                                 prepare_deepseek_v4_w8a8_linear_quantized_weight)
+
+    g = torch.Generator().manual_seed(5)
+    m, k, n1, n2 = 64, 1536, 32768, 8192
+    x = (torch.randn((m, k), generator=g) * 0.2).to(torch.bfloat16).to(gpu)
+    first = prepare_deepseek_v4_w8a8_linear_quantized_weight(
+        torch.randint(-127, 128, (n1, k), dtype=torch.int8, generator=g), torch.rand((n1,), generator=g) * 0.002 + 0.001)
+    second = prepare_deepseek_v4_w8a8_linear_quantized_weight(
+        torch.randint(-127, 128, (n2, k), dtype=torch.int8, generator=g), torch.rand((n2,), generator=g) * 0.002 + 0.001)
+    a, b = deepseek_v4_w8a8_linear_pair(x, first, second)
+    assert torch.equal(a, deepseek_v4_w8a8_linear(x, first))
+    assert torch.equal(b, deepseek_v4_w8a8_linear(x, second))
 
 
 def test_pair_and_linear_reject_bad_shapes(gpu):

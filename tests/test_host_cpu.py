@@ -344,3 +344,19 @@ def test_bf16_half_ulp_bounds_bf16_rounding():
     assert (err <= half).all()
     assert (err / half).max() > 0.999
     assert H.bf16_half_ulp(np.array([1.0, 10.0, 0.75]))[1] == 2.0 ** -5
+
+
+def test_i8gemm_pair_workspace_covers_both_gemms():
+    """The pair's two GEMMs can split K differently (the split count depends
+    on N): its workspace must hold the larger partial-sum area, whichever GEMM
+    needs it (a pair sized for max(N) alone once left the second GEMM's partial
+    sums past the end of the workspace)."""
+    from fused_cpp_amd import cabi
+
+    L = cabi.lib()
+    for m in (1, 16, 33, 64, 65, 300):
+        for k in (64, 1536, 7168, 16384):
+            for n1, n2 in ((24576, 8192), (8192, 24576), (7168, 7168), (100, 65536), (32768, 512)):
+                pair = L.fcmoe_i8gemm_pair_workspace_bytes(m, k, n1, n2)
+                assert pair >= L.fcmoe_i8gemm_workspace_bytes(m, k, n1), (m, k, n1, n2)
+                assert pair >= L.fcmoe_i8gemm_workspace_bytes(m, k, n2), (m, k, n1, n2)

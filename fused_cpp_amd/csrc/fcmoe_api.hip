@@ -91,6 +91,8 @@ struct Bf16Layout {
   uint16_t* y;
   float* gate_up;
   float* route_out;
+  float* partial = nullptr;  // small-M GEMMs' partial sums (smallm_mlp)
+  size_t partial_bytes = 0;
 };
 
 int64_t tile_offset(const TileClasses& tc, int c) {
@@ -142,6 +144,15 @@ W8A8Layout w8a8_layout(const fcmoe_moe_args* a, Arena& ar) {
 // rows on the LDS-staged kernel (no 64-row W8A16 tile). The 192-row tile
 // takes experts of 129-192 rows off the 256-row one, which ran them at half
 // its rows (DSv3 shape, T = 4096 uniform: 4.63 -> 4.17 ms).
+// A BF16 forward over one packed expert with at most 64 routes (the shared
+// MLP, or a one-expert MoE, at decode batch sizes) runs its two GEMMs on the
+// small-M kernel (fcmoe_gemm_smallm.hip): every weight byte read once, K split
+// over about one workgroup per CU. The one-expert MoE and the shared MLP take
+// the same path, so they stay equal bit for bit.
+bool smallm_mlp(const fcmoe_moe_args* a, int64_t routes, bool w8) {
+  return !w8 && a->experts == 1 && routes >= 1 && routes <= kSmallMRows && a->activation != FCMOE_ACT_SWIGLUOAI;
+}
+
 constexpr int kClassBMW8[] = {16, 32, 128, 192, 256};
 constexpr int kNumClassesW8 = 5;
 Bf16Layout bf16_layout(const fcmoe_moe_args* a, Arena& ar, bool w8 = false) {
@@ -169,6 +180,13 @@ Bf16Layout bf16_layout(const fcmoe_moe_args* a, Arena& ar, bool w8 = false) {
   L.y = ar.take<uint16_t>(L.routes * L.ip);
   L.gate_up = a->activation == FCMOE_ACT_SWIGLUOAI ? ar.take<float>(L.routes * L.gu_ld) : nullptr;
   L.route_out = ar.take<float>(L.routes * a->hidden);
+  if (smallm_mlp(a, L.routes, w8)) {
+    const int64_t kc13 = ceil_div(a->hidden * 2, 64), kc2 = ceil_div(a->inter * 2, 64);
+    const int64_t p13 = smallm_bf16_splits(L.routes, kc13, 2 * ceil_div(a->inter, 16)) * 2 * a->inter;
+    const int64_t p2 = smallm_bf16_splits(L.routes, kc2, ceil_div(a->hidden, 16)) * a->hidden;
+    L.partial_bytes = (size_t)((p13 > p2 ? p13 : p2) * L.routes) * sizeof(float);
+    L.partial = ar.take<float>(L.partial_bytes / sizeof(float));
+  }
   return L;
 }
 
@@ -875,6 +893,45 @@ int bf16_family_forward(const fcmoe_moe_args* a, hipStream_t stream, bool w8) {
     if (rc) return rc;
   }
   const bool fused = a->activation != FCMOE_ACT_SWIGLUOAI;
+  if (smallm_mlp(a, L.routes, w8)) {
+    SmallMBf16 q{};
+    q.a = xa;
+    q.lda_bytes = L.hp * 2;
+    q.a_rows = a->tokens;
+    q.row_map = L.rb.row_token;
+    q.m = L.routes;
+    q.k_chunks = ceil_div(H * 2, 64);
+    q.w = a->w13;
+    q.n_groups = 2;
+    q.n_half = I;
+    q.bias = a->w13_bias;
+    q.out = L.y;
+    q.ldo = L.ip;
+    q.activation = a->activation;
+    q.partial = L.partial;
+    q.partial_bytes = L.partial_bytes;
+    q.m_dev = L.rb.counts;  // expert 0's routed rows
+    {
+      Stage st(FCMOE_STAGE_W13_CLASS0 + class_slot(16), stream);
+      if ((rc = smallm_bf16_launch(q, stream))) return rc;
+    }
+    q.a = L.y;
+    q.lda_bytes = L.ip * 2;
+    q.a_rows = L.routes;
+    q.row_map = nullptr;
+    q.k_chunks = ceil_div(I * 2, 64);
+    q.w = a->w2;
+    q.n_groups = 1;
+    q.n_half = H;
+    q.bias = a->w2_bias;
+    q.out = L.route_out;
+    q.ldo = H;
+    q.out_row = L.rb.sorted_routes;
+    {
+      Stage st(FCMOE_STAGE_W2_CLASS0 + class_slot(16), stream);
+      if ((rc = smallm_bf16_launch(q, stream))) return rc;
+    }
+  } else {
   GemmParams g13{};
   g13.a = xa;
   g13.lda = L.hp;
@@ -934,6 +991,7 @@ int bf16_family_forward(const fcmoe_moe_args* a, hipStream_t stream, bool w8) {
     return gemm_launch(w8 ? kEpiW2RouteW8 : kEpiW2RouteBf16, L.tc.bm[c], p, L.tc.bound[c], s);
   });
   if (rc) return rc;
+  }
   const int tree = (kt == 2 || kt == 4 || kt == 6 || kt == 8) ? 1 : 0;
   Stage st(FCMOE_STAGE_COMBINE, stream);
   return combine_launch(L.route_out, L.rb.route_weight, L.rb.route_pos, a->tokens, kt, H, tree, a->skip_weighted,

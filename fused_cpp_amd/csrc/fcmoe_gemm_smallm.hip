@@ -21,6 +21,14 @@
 //     launch applies the epilogue itself.
 // The epilogue is write_scaled_output's (csrc/i8gemm.cpp:148-164):
 // (float)acc * s_x * s_w left to right, + bias, then bf16 (RNE) or fp32.
+//
+// The same kernel runs the BF16 dense MLP at few rows (one packed expert, at
+// most 64 routes: the shared MLP at decode batch sizes) on
+// v_mfma_f32_16x16x32_bf16: A rows gathered through the route order's token
+// map, fp32 partial sums always written, and a reduce launch that adds the
+// splits in split order and applies the W13 activation (gate + bias,
+// up + bias, act_bf16_mode, bf16) or the W2 route store (+ bias, fp32 route
+// rows for the combine).
 #include <cstdlib>
 #include <utility>
 
@@ -42,20 +50,27 @@ __device__ __forceinline__ void sm_wait_vmcnt() {
 }
 
 struct SmallMArgs {
-  const int8_t* a;  // quantised rows [m, lda]
-  int64_t lda;      // bytes per row (a multiple of 64)
+  const void* a;               // rows [*, lda]: int8 (i8gemm) or bf16
+  int64_t lda;                 // bytes per row (a multiple of 64)
+  const int32_t* row_map;      // row r of the product reads A row row_map[r] (null: r)
   int m;
-  int64_t kc;       // 64-byte K chunks
-  int64_t cps;      // chunks per split (grid.y splits)
-  const void* w;    // packed [n_tiles][kc][64 lanes][16 B]
-  int64_t n, n_tiles;
-  const float* scale_row;  // [m]
-  const float* scale_col;  // [n]
-  const float* bias;       // [n] or null
+  int64_t kc;                  // 64-byte K chunks
+  int64_t cps;                 // chunks per split (grid.y splits)
+  const void* w;               // packed [n_groups][n_tiles][kc][64 lanes][16 B]
+  int64_t n_groups, n_tiles;   // weight tiles per group (total n_groups x n_tiles)
+  int64_t n_half;              // logical channels per group
+  int64_t n;                   // logical channels (n_groups x n_half): partial-sum row width
+  const float* scale_row;      // [m] (i8gemm)
+  const float* scale_col;      // [n] (i8gemm)
+  const float* bias;           // [n] or null
   void* out;
   int out_bf16;
   int64_t ldo;
-  int32_t* partial;  // [splits][m][n] when grid.y > 1, else null
+  void* partial;               // [splits][m][n] int32 (int8) / fp32 (bf16); null: direct i8gemm epilogue
+  const int32_t* out_row;      // route store: output row of product row r (the flat route)
+  int activation;              // W13 activation store: FCMOE_ACT_*
+  const int32_t* m_dev;        // rows actually routed (device; null: m): the MoE route
+                               // build drops invalid ids, so fewer than m rows may exist
 };
 
 __device__ __forceinline__ void sm_store(const SmallMArgs& p, int row, int64_t ch, int32_t acc) {
@@ -68,16 +83,17 @@ __device__ __forceinline__ void sm_store(const SmallMArgs& p, int row, int64_t c
     ((float*)p.out)[(int64_t)row * p.ldo + ch] = v;
 }
 
-template <int FM>
-__global__ __launch_bounds__(kSmWaves * kWave) void smallm_i8_kernel(SmallMArgs p) {
+template <bool I8, int FM>
+__global__ __launch_bounds__(kSmWaves * kWave) void smallm_kernel(SmallMArgs p) {
 #if __HIP_DEVICE_COMPILE__
   constexpr int D = kSmDepth;
   constexpr int ABYTES = FM * 1024;  // 16 FM rows x 64 bytes
+  typedef typename Acc<I8>::type AccT;
   __shared__ __attribute__((aligned(1024))) uint8_t sa[D * ABYTES];
   const int lane = threadIdx.x % kWave;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-  const int64_t tile = (int64_t)blockIdx.x * kSmWaves + wave;
-  const bool tv = tile < p.n_tiles;
+  const int64_t tile = (int64_t)blockIdx.x * kSmWaves + wave;  // packed tile (group-major)
+  const bool tv = tile < p.n_groups * p.n_tiles;
   const int64_t c0 = (int64_t)blockIdx.y * p.cps;
   const int64_t c1 = c0 + p.cps < p.kc ? c0 + p.cps : p.kc;
   // 32-bit chunk counters keep the loop's compares scalar (a 64-bit compare
@@ -92,9 +108,14 @@ __global__ __launch_bounds__(kSmWaves * kWave) void smallm_i8_kernel(SmallMArgs 
   const int g = wave % FM;
   const int ar = g * 16 + lane / 4;
   const int aunit = (lane % 4) ^ ((lane >> 4) & 3);
+  const int rows_valid = p.m_dev ? *p.m_dev : p.m;
+  const int arow_local = ar < rows_valid ? ar : (rows_valid > 0 ? rows_valid - 1 : 0);
+  // rows past the routed ones re-read the last routed row (or x row 0); their
+  // sums are never stored
+  const int64_t arow = p.row_map && rows_valid > 0 ? (int64_t)p.row_map[arow_local] : (int64_t)arow_local;
   const __amdgpu_buffer_rsrc_t rsrc_a =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(p.a), (short)0, 0x7ffffff0, kSmBufWord3);
-  const uint32_t voff_a = (uint32_t)((ar < p.m ? ar : p.m - 1) * p.lda + aunit * 16);
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p.a), (short)0, 0x7ffffff0, kSmBufWord3);
+  const uint32_t voff_a = (uint32_t)(arow * p.lda + aunit * 16);
   // The tile's weights through a buffer resource: the chunk offset goes in
   // the scalar operand and the lane offset is fixed, so no address VGPR is
   // computed per load (a 64-bit address written into a ring register with an
@@ -105,9 +126,9 @@ __global__ __launch_bounds__(kSmWaves * kWave) void smallm_i8_kernel(SmallMArgs 
   const int frag = (lane % 16) * 64 + (((lane / 16) ^ ((lane % 16) >> 2)) * 16);
 
   v4i bq[D];
-  v4i acc[FM];
+  AccT acc[FM];
 #pragma unroll
-  for (int i = 0; i < FM; ++i) acc[i] = v4i{0, 0, 0, 0};
+  for (int i = 0; i < FM; ++i) acc[i] = AccT{0, 0, 0, 0};
 
   // pair t: A stage and weight chunk of the split's chunk t (past the end:
   // the last chunk again, never consumed)
@@ -137,7 +158,12 @@ __global__ __launch_bounds__(kSmWaves * kWave) void smallm_i8_kernel(SmallMArgs 
 #pragma unroll
     for (int i = 0; i < FM; ++i) af[i] = *(const v4i*)(sa + slot * ABYTES + i * 1024 + frag);
 #pragma unroll
-    for (int i = 0; i < FM; ++i) acc[i] = mfma(af[i], bq[slot], acc[i]);
+    for (int i = 0; i < FM; ++i) {
+      if constexpr (I8)
+        acc[i] = mfma(af[i], bq[slot], acc[i]);
+      else
+        acc[i] = mfma(__builtin_bit_cast(v8bf, af[i]), __builtin_bit_cast(v8bf, bq[slot]), acc[i]);
+    }
   };
   // whole rings of D chunks, then the rest: no conditional step inside the
   // loop, so the compiler's wait counts at the loop header match the steady
@@ -154,18 +180,25 @@ __global__ __launch_bounds__(kSmWaves * kWave) void smallm_i8_kernel(SmallMArgs 
   sm_wait_vmcnt<0>();
 
   if (!tv) return;
-  const int64_t ch = tile * 16 + lane % 16;
-  if (ch >= p.n) return;
+  const int64_t grp = tile / p.n_tiles;
+  const int64_t cin = (tile - grp * p.n_tiles) * 16 + lane % 16;
+  if (cin >= p.n_half) return;
+  const int64_t ch = grp * p.n_half + cin;  // logical channel
 #pragma unroll
   for (int i = 0; i < FM; ++i)
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int row = i * 16 + (lane / 16) * 4 + q;
       if (row >= p.m) continue;
-      if (p.partial)
-        p.partial[((int64_t)blockIdx.y * p.m + row) * p.n + ch] = acc[i][q];
-      else
-        sm_store(p, row, ch, acc[i][q]);
+      const int64_t e = ((int64_t)blockIdx.y * p.m + row) * p.n + ch;
+      if constexpr (I8) {
+        if (p.partial)
+          ((int32_t*)p.partial)[e] = acc[i][q];
+        else
+          sm_store(p, row, ch, acc[i][q]);
+      } else {
+        ((float*)p.partial)[e] = acc[i][q];
+      }
     }
 #endif
 }
@@ -176,18 +209,59 @@ __global__ __launch_bounds__(256) void smallm_reduce_kernel(SmallMArgs p, int sp
   const int64_t total = (int64_t)p.m * p.n;
   for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (int64_t)gridDim.x * blockDim.x) {
     int32_t acc = 0;
-    for (int s = 0; s < splits; ++s) acc += p.partial[(int64_t)s * total + e];
+    for (int s = 0; s < splits; ++s) acc += ((const int32_t*)p.partial)[(int64_t)s * total + e];
     sm_store(p, (int)(e / p.n), e % p.n, acc);
+  }
+}
+
+// BF16 W13: y[r][f] = bf16(act(gate + bias, up + bias)) over the gate
+// channels f < n_half (up channel n_half + f), the splits' fp32 sums added in
+// split order; the arithmetic after the sums is the W13 activation
+// epilogue's (fcmoe_gemm_common.h).
+__global__ __launch_bounds__(256) void smallm_act_kernel(SmallMArgs p, int splits) {
+  const int64_t total = (int64_t)p.m * p.n_half, plane = (int64_t)p.m * p.n;
+  const float* part = (const float*)p.partial;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = e / p.n_half, f = e % p.n_half;
+    const int64_t eg = r * p.n + f, eu = eg + p.n_half;
+    float gate = part[eg], up = part[eu];
+    for (int s = 1; s < splits; ++s) {
+      gate = gate + part[s * plane + eg];
+      up = up + part[s * plane + eu];
+    }
+    if (p.bias) {
+      gate = gate + p.bias[f];
+      up = up + p.bias[p.n_half + f];
+    }
+    ((uint16_t*)p.out)[r * p.ldo + f] = f32_to_bf16(act_bf16_mode(gate, up, p.activation));
+  }
+}
+
+// BF16 W2: route_out[out_row[r]][h] = sum (+ bias[h]), the splits' fp32 sums
+// added in split order.
+__global__ __launch_bounds__(256) void smallm_route_kernel(SmallMArgs p, int splits) {
+  const int64_t total = (int64_t)p.m * p.n;
+  const float* part = (const float*)p.partial;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = e / p.n, h = e % p.n;
+    if (p.m_dev && r >= *p.m_dev) continue;  // a dropped route: no row to store
+    float v = part[e];
+    for (int s = 1; s < splits; ++s) v = v + part[s * total + e];
+    if (p.bias) v = v + p.bias[h];
+    ((float*)p.out)[(int64_t)p.out_row[r] * p.ldo + h] = v;
   }
 }
 
 }  // namespace
 
-int64_t smallm_splits(int64_t m, int64_t k, int64_t n) {
-  if (m <= 0 || m > kSmallMRows || k <= 0 || n <= 0) return 0;
-  const int64_t kc = ceil_div(k, 64);
-  const int64_t groups = ceil_div(ceil_div(n, 16), kSmWaves);
-  // workgroups (groups x splits) up to the target, at least 8 chunks per split
+namespace {
+
+// K splits for a product of m rows over kc chunks and `tiles` weight tiles
+// (0 outside the domain): workgroups (tile groups x splits) up to the target
+// (FCMOE_SMALLM_WGS, default 256: about one per CU), at least 8 chunks a split.
+int64_t splits_for(int64_t m, int64_t kc, int64_t tiles) {
+  if (m <= 0 || m > kSmallMRows || kc <= 0 || tiles <= 0) return 0;
+  const int64_t groups = ceil_div(tiles, kSmWaves);
   static const int64_t target = [] {
     const char* v = getenv("FCMOE_SMALLM_WGS");
     return v && v[0] ? (int64_t)atoll(v) : (int64_t)256;
@@ -198,6 +272,38 @@ int64_t smallm_splits(int64_t m, int64_t k, int64_t n) {
   if (s < 1) s = 1;
   const int64_t cps = ceil_div(kc, s);
   return ceil_div(kc, cps);
+}
+
+int launch_gemm(const SmallMArgs& p0, int64_t splits, bool i8, hipStream_t stream) {
+  SmallMArgs p = p0;
+  p.cps = ceil_div(p.kc, splits);
+  const dim3 grid((unsigned)ceil_div(p.n_groups * p.n_tiles, kSmWaves), (unsigned)splits), block(kSmWaves * kWave);
+  const int fm = (int)ceil_div(p.m, 16);
+  if (i8) {
+    if (fm == 1)
+      hipLaunchKernelGGL((smallm_kernel<true, 1>), grid, block, 0, stream, p);
+    else if (fm == 2)
+      hipLaunchKernelGGL((smallm_kernel<true, 2>), grid, block, 0, stream, p);
+    else
+      hipLaunchKernelGGL((smallm_kernel<true, 4>), grid, block, 0, stream, p);
+  } else {
+    if (fm == 1)
+      hipLaunchKernelGGL((smallm_kernel<false, 1>), grid, block, 0, stream, p);
+    else if (fm == 2)
+      hipLaunchKernelGGL((smallm_kernel<false, 2>), grid, block, 0, stream, p);
+    else
+      hipLaunchKernelGGL((smallm_kernel<false, 4>), grid, block, 0, stream, p);
+  }
+  return check_launch("smallm_gemm");
+}
+
+unsigned reduce_blocks(int64_t total) { return (unsigned)(ceil_div(total, 256) < 4096 ? ceil_div(total, 256) : 4096); }
+
+}  // namespace
+
+int64_t smallm_splits(int64_t m, int64_t k, int64_t n) {
+  if (k <= 0 || n <= 0) return 0;
+  return splits_for(m, ceil_div(k, 64), ceil_div(n, 16));
 }
 
 size_t smallm_workspace_bytes(int64_t m, int64_t k, int64_t n) {
@@ -219,10 +325,11 @@ int smallm_i8gemm_launch(const int8_t* a, int64_t lda, int64_t m, int64_t k, con
   p.lda = lda;
   p.m = (int)m;
   p.kc = ceil_div(k, 64);
-  p.cps = ceil_div(p.kc, splits);
   p.w = w_packed;
-  p.n = n;
+  p.n_groups = 1;
   p.n_tiles = ceil_div(n, 16);
+  p.n_half = n;
+  p.n = n;
   p.scale_row = scale_row;
   p.scale_col = scale_col;
   p.bias = bias;
@@ -230,20 +337,50 @@ int smallm_i8gemm_launch(const int8_t* a, int64_t lda, int64_t m, int64_t k, con
   p.out_bf16 = out_bf16;
   p.ldo = n;
   p.partial = splits > 1 ? partial : nullptr;
-  const dim3 grid((unsigned)ceil_div(p.n_tiles, kSmWaves), (unsigned)splits), block(kSmWaves * kWave);
-  const int fm = (int)ceil_div(m, 16);
-  if (fm == 1)
-    hipLaunchKernelGGL(smallm_i8_kernel<1>, grid, block, 0, stream, p);
-  else if (fm == 2)
-    hipLaunchKernelGGL(smallm_i8_kernel<2>, grid, block, 0, stream, p);
-  else
-    hipLaunchKernelGGL(smallm_i8_kernel<4>, grid, block, 0, stream, p);
-  int rc = check_launch("smallm_i8gemm");
+  int rc = launch_gemm(p, splits, true, stream);
   if (rc || splits == 1) return rc;
-  const int64_t total = m * n;
-  const unsigned blocks = (unsigned)(ceil_div(total, 256) < 4096 ? ceil_div(total, 256) : 4096);
-  hipLaunchKernelGGL(smallm_reduce_kernel, dim3(blocks), dim3(256), 0, stream, p, (int)splits);
+  hipLaunchKernelGGL(smallm_reduce_kernel, dim3(reduce_blocks(m * n)), dim3(256), 0, stream, p, (int)splits);
   return check_launch("smallm_reduce");
+}
+
+int64_t smallm_bf16_splits(int64_t m, int64_t k_chunks, int64_t tiles) { return splits_for(m, k_chunks, tiles); }
+
+int smallm_bf16_launch(const SmallMBf16& q, hipStream_t stream) {
+  const int64_t tiles = q.n_groups * ceil_div(q.n_half, 16);
+  const int64_t splits = splits_for(q.m, q.k_chunks, tiles);
+  if (splits <= 0) return fail(FCMOE_EINVAL, "small-M BF16 GEMM: shape outside its domain");
+  if (q.lda_bytes % 64 || q.lda_bytes < q.k_chunks * 64 || q.a_rows * q.lda_bytes >= 0x7ffffff0)
+    return fail(FCMOE_EINVAL, "small-M BF16 GEMM: bad row stride");
+  const int64_t n = q.n_groups * q.n_half;
+  if (!q.partial || q.partial_bytes < (size_t)(splits * q.m * n) * sizeof(float))
+    return fail(FCMOE_ESPACE, "small-M BF16 GEMM: partial-sum workspace too small");
+  SmallMArgs p{};
+  p.a = q.a;
+  p.lda = q.lda_bytes;
+  p.row_map = q.row_map;
+  p.m = (int)q.m;
+  p.kc = q.k_chunks;
+  p.w = q.w;
+  p.n_groups = q.n_groups;
+  p.n_tiles = ceil_div(q.n_half, 16);
+  p.n_half = q.n_half;
+  p.n = n;
+  p.bias = q.bias;
+  p.out = q.out;
+  p.ldo = q.ldo;
+  p.partial = q.partial;
+  p.out_row = q.out_row;
+  p.activation = q.activation;
+  p.m_dev = q.m_dev;
+  int rc = launch_gemm(p, splits, false, stream);
+  if (rc) return rc;
+  if (q.out_row) {
+    hipLaunchKernelGGL(smallm_route_kernel, dim3(reduce_blocks(q.m * n)), dim3(256), 0, stream, p, (int)splits);
+  } else {
+    hipLaunchKernelGGL(smallm_act_kernel, dim3(reduce_blocks(q.m * q.n_half)), dim3(256), 0, stream, p,
+                       (int)splits);
+  }
+  return check_launch("smallm_bf16_reduce");
 }
 
 }  // namespace fcmoe

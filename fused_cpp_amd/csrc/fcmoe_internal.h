@@ -208,6 +208,29 @@ size_t smallm_workspace_bytes(int64_t m, int64_t k, int64_t n);
 int smallm_i8gemm_launch(const int8_t* a, int64_t lda, int64_t m, int64_t k, const void* w_packed,
                          const float* scale_row, const float* scale_col, int64_t n, const float* bias, void* out,
                          int out_bf16, int32_t* partial, size_t partial_bytes, hipStream_t stream);
+// The BF16 dense MLP at few rows on the same kernel: W13 (out_row null: the
+// activation store into y, bf16 [m, ldo]) or W2 (the fp32 route store into
+// out at row out_row[r]). k_chunks: 64-byte K chunks; weights packed bf16
+// with n_groups groups of n_half channels.
+struct SmallMBf16 {
+  const void* a;           // bf16 rows
+  int64_t lda_bytes;
+  int64_t a_rows;          // rows A may address
+  const int32_t* row_map;  // product row r reads A row row_map[r] (null: r)
+  int64_t m, k_chunks;
+  const void* w;
+  int64_t n_groups, n_half;
+  const float* bias;
+  void* out;
+  int64_t ldo;
+  const int32_t* out_row;
+  int activation;
+  float* partial;
+  size_t partial_bytes;
+  const int32_t* m_dev;    // rows actually routed (device), at most m; null: m
+};
+int64_t smallm_bf16_splits(int64_t m, int64_t k_chunks, int64_t tiles);
+int smallm_bf16_launch(const SmallMBf16& q, hipStream_t stream);
 // LDS-staged kernel for bm in {128, 192, 256} (fcmoe_gemm_lds.hip); gemm_launch
 // dispatches to it unless FCMOE_GEMM_LDS=0.
 int gemm_lds_launch(int epi, int bm, const GemmParams& p, int64_t max_tiles, hipStream_t stream);

@@ -198,7 +198,7 @@ def test_bf16_clamped_swiglu_matches_reference(gpu, oracle_lib):
     w2 = H.bits_to_f32(H.bf16_bits((rng.standard_normal((E, Hd, F)) * 0.02).astype(np.float32)))
     ids = np.concatenate([np.full(c, e) for e, c in enumerate(counts)]).reshape(-1, 1).astype(np.int32)
     w = np.ones((T, 1), np.float32)
-    packed = moe.prepare_fused_moe_bf16_tiled_weights(_bf16(w13, gpu), _bf16(w2, gpu), fuse_silu=True)
+    packed = moe.prepare_fused_moe_bf16_tiled_weights(_bf16(w13, gpu), _bf16(w2, gpu))
     args = (_bf16(x, gpu), packed, torch.from_numpy(w).to(gpu), torch.from_numpy(ids).to(gpu))
     unclamped = moe.fused_moe_bf16_tiled(*args)
     zero = moe.fused_moe_bf16_tiled(*args, swiglu_limit=0.0)
@@ -237,7 +237,7 @@ def test_bf16_plumbing_config_within_north_star_tolerance(gpu, oracle_lib, T, Hd
     w13 = H.bits_to_f32(H.bf16_bits((rng.standard_normal((E, 2 * F, Hd)) * 0.02).astype(np.float32)))
     w2 = H.bits_to_f32(H.bf16_bits((rng.standard_normal((E, Hd, F)) * 0.02).astype(np.float32)))
     ids, w = H.softmax_topk(rng.standard_normal((T, E)).astype(np.float32), k)
-    packed = moe.prepare_fused_moe_bf16_tiled_weights(_bf16(w13, gpu), _bf16(w2, gpu), fuse_silu=True)
+    packed = moe.prepare_fused_moe_bf16_tiled_weights(_bf16(w13, gpu), _bf16(w2, gpu))
     out = moe.fused_moe_bf16_tiled(_bf16(x, gpu), packed, torch.from_numpy(w).to(gpu), torch.from_numpy(ids).to(gpu))
     _close(out, oracle_lib.bf16_moe_reference(x, w13, w2, w, ids))
 
@@ -302,6 +302,49 @@ def test_routed_shared_equals_explicit_combined_route(gpu):
     w_c = torch.from_numpy(np.concatenate([w * np.float32(2.5), np.ones((19, 1), np.float32)], 1)).to(gpu)
     b = moe.fused_moe_bf16_tiled(xt, prepared.packed, w_c, ids_c)
     assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("T,Hd,F,activation,bias", [(1, 7168, 2048, "silu", False), (17, 200, 72, "gelu", True),
+                                                    (64, 7168, 2048, "silu", True), (40, 96, 40, "silu", False)])
+def test_bf16_single_expert_small_rows_within_tolerance(gpu, oracle_lib, T, Hd, F, activation, bias):
+    """One packed expert and at most 64 routes run both GEMMs on the small-M
+    kernel (split K, fp32 partial sums added in split order, the activation
+    and route stores in the reduce launches): the shared MLP and a one-expert
+    MoE against the fp32 reference, with biases, ragged H/F (zero-padded K),
+    and routes to an expert another rank holds (global_num_experts=2, id 1:
+    dropped, contributing nothing)."""
+    from fused_cpp_amd import moe
+
+    rng = np.random.default_rng(T * 31 + Hd)
+    x = H.bits_to_f32(H.bf16_bits(rng.standard_normal((T, Hd)).astype(np.float32)))
+    w13 = H.bits_to_f32(H.bf16_bits((rng.standard_normal((1, 2 * F, Hd)) * 0.02).astype(np.float32)))
+    w2 = H.bits_to_f32(H.bf16_bits((rng.standard_normal((1, Hd, F)) * 0.02).astype(np.float32)))
+    b13 = (rng.standard_normal((1, 2 * F)) * 0.1).astype(np.float32) if bias else None
+    b2 = (rng.standard_normal((1, Hd)) * 0.1).astype(np.float32) if bias else None
+    tb = lambda a: torch.from_numpy(a).to(gpu) if a is not None else None  # noqa: E731
+    packed = moe.prepare_fused_moe_bf16_tiled_weights(_bf16(w13, gpu), _bf16(w2, gpu))
+    w = rng.random((T, 1)).astype(np.float32) + 0.5
+    ids = np.zeros((T, 1), np.int32)
+    out = moe.fused_moe_bf16_tiled(_bf16(x, gpu), packed, tb(w), tb(ids), w13_bias=tb(b13), w2_bias=tb(b2),
+                                   activation=activation)
+    ref = oracle_lib.bf16_moe_reference(x, w13, w2, w, ids, w13_bias=b13, w2_bias=b2, activation=activation,
+                                        round_intermediate=True)
+    _close(out, ref)
+    if activation == "silu" and not bias:
+        sm = moe.prepare_shared_mlp_bf16_tiled_weights(_bf16(w13[0], gpu), _bf16(w2[0], gpu))
+        one = moe.fused_moe_bf16_tiled(_bf16(x, gpu), packed, torch.ones((T, 1), device=gpu),
+                                       torch.zeros((T, 1), dtype=torch.int32, device=gpu))
+        assert torch.equal(moe.shared_mlp_bf16_tiled(_bf16(x, gpu), sm), one)
+    if T > 2:
+        ids[::3] = 1  # routed to the other rank's expert
+        out = moe.fused_moe_bf16_tiled(_bf16(x, gpu), packed, tb(w), tb(ids), w13_bias=tb(b13), w2_bias=tb(b2),
+                                       activation=activation, global_num_experts=2)
+        keep = ids[:, 0] == 0
+        ref = oracle_lib.bf16_moe_reference(x[keep], w13, w2, w[keep], ids[keep], w13_bias=b13, w2_bias=b2,
+                                            activation=activation, round_intermediate=True)
+        got = out.float().cpu().numpy()
+        assert not got[~keep].any()
+        _close(out[torch.from_numpy(np.nonzero(keep)[0]).to(gpu)], ref)
 
 
 @pytest.mark.parametrize("rows", [1, 13, 97])

@@ -774,8 +774,10 @@ SECONDARY = [("c2_t1", "c2", 1, False), ("c2_t2", "c2", 2, False), ("c2_t8", "c2
 OP_SECONDARY = [("i8gemm_pair_q_m64", "pair", 64, 1536, (24576, 8192)),
                 ("i8gemm_pair_q_m4096", "pair", 4096, 1536, (24576, 8192)),
                 ("i8gemm_wo_b_m64", "single", 64, 16384, (7168,)),
+                ("i8gemm_wo_b_m128", "single", 128, 16384, (7168,)),
                 ("i8gemm_wo_b_m4096", "single", 4096, 16384, (7168,)),
-                ("shared_mlp_t64", "shared_mlp", 64, 7168, (2048,))]
+                ("shared_mlp_t64", "shared_mlp", 64, 7168, (2048,)),
+                ("shared_mlp_t128", "shared_mlp", 128, 7168, (2048,))]
 
 
 def _time_op(fn, steps: int, warmup: int):
@@ -839,7 +841,7 @@ def measure_op(wl: str, op: str, M: int, K: int, Ns, args, device, want_cpu: boo
 
     g = torch.Generator(device=device).manual_seed(99)
     x = torch.randn((M, K), generator=g, device=device).to(torch.bfloat16)
-    steps = max(args.steps, 100 if M <= 64 else 0)
+    steps = max(args.steps, 100 if M <= 128 else 0)
     entry = {"workload": wl}
     if op == "shared_mlp":
         I = Ns[0]

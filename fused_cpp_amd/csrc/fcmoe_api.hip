@@ -144,7 +144,7 @@ W8A8Layout w8a8_layout(const fcmoe_moe_args* a, Arena& ar) {
 // rows on the LDS-staged kernel (no 64-row W8A16 tile). The 192-row tile
 // takes experts of 129-192 rows off the 256-row one, which ran them at half
 // its rows (DSv3 shape, T = 4096 uniform: 4.63 -> 4.17 ms).
-// A BF16 forward over one packed expert with at most 64 routes (the shared
+// A BF16 forward over one packed expert with at most 128 routes (the shared
 // MLP, or a one-expert MoE, at decode batch sizes) runs its two GEMMs on the
 // small-M kernel (fcmoe_gemm_smallm.hip): every weight byte read once, K split
 // over about one workgroup per CU. The one-expert MoE and the shared MLP take
@@ -1116,7 +1116,18 @@ int i8gemm_run(const I8Layout& L, int64_t k, const void* w_packed, const float* 
   g.scale_col = w_scale;
   g.bias = bias;
   g.out_bf16 = out_is_bf16;
+  g.cus = persistent_wgs();
+  // One expert of m rows: only its class (rows in (bm[c-1], bm[c]], the last
+  // class above) gets tiles, so the other classes' launches are not enqueued
+  // (5 empty launches cost the 4096-row pair ~0.04 ms).
+  int only = L.tc.n - 1;
+  for (int c = 0; c < L.tc.n; ++c)
+    if (L.m <= L.tc.bm[c]) {
+      only = c;
+      break;
+    }
   for (int c = 0; c < L.tc.n; ++c) {
+    if (c != only) continue;
     GemmParams p = g;
     p.tiles = L.tiles + 2 * tile_offset(L.tc, c);
     p.tile_count = L.tile_count + c;

@@ -272,6 +272,66 @@ __device__ __forceinline__ void staged_epilogue(const GemmParams& p, const v4i (
               *(__attribute__((address_space(3))) const float*)(rp + lane * 4);
       }
     }
+  } else if constexpr (EPI == kEpiI8Gemm) {
+    // write_scaled_output, csrc/i8gemm.cpp:148-164: (float)acc * s_x * s_w
+    // left to right, + bias, then bf16 (RNE) or fp32. Staged as fp32 rows;
+    // stored as 16-byte pieces of 8 bf16 or 4 fp32 channels where the row
+    // stride and the channel count allow it, else channel by channel.
+    constexpr int RS = FN * 64 + 16;  // bytes per staged row (FN*16 fp32 + pad)
+    float cs[FN], cb[FN];
+    const int64_t c0 = gtile[0] * 16;  // one channel group: the wave's channels are c0 .. c0 + 16 FN - 1
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const int64_t ch = c0 + j * 16 + col;
+      cs[j] = m.cs[(m.cbase + j) * 16 + col];
+      cb[j] = p.bias && tvalid[j] && ch < p.n ? p.bias[ch] : 0.0f;
+    }
+    const int per = p.out_bf16 ? 8 : 4;  // channels per 16-byte piece
+    const bool vec = p.ldo % per == 0 && ((uintptr_t)p.out & 15) == 0;
+    const int upr = FN * 16 / per;       // pieces per staged row
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      const int rbase = row_base + i * 16;
+      if (rbase >= rows) break;  // fragments past the expert's rows (wave-uniform)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int r = rbase + rq + q;
+        const float rs = m.rs[r < rows ? r : rows - 1];
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+          float v = (float)acc[i][j][q] * rs * cs[j];
+          if (p.bias) v = v + cb[j];
+          *(__attribute__((address_space(3))) float*)(slice + (rq + q) * RS + (j * 16 + col) * 4) = v;
+        }
+      }
+      for (int idx = lane; idx < 16 * upr; idx += kWave) {
+        const int row = idx / upr, u = idx % upr;
+        const int r = rbase + row;
+        const int64_t ch = c0 + (int64_t)u * per;
+        if (r >= rows || ch >= p.n) continue;
+        const int64_t o = (int64_t)(pos0 + r) * p.ldo + ch;
+        const __attribute__((address_space(3))) float* src =
+            (const __attribute__((address_space(3))) float*)(slice + row * RS + u * per * 4);
+        if (vec && ch + per <= p.n) {
+          if (p.out_bf16) {
+            uint32_t w[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              w[e] = (uint32_t)f32_to_bf16(src[2 * e]) | ((uint32_t)f32_to_bf16(src[2 * e + 1]) << 16);
+            *(v4i*)((uint16_t*)p.out + o) = v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+          } else {
+            *(v4i*)((float*)p.out + o) = *(const __attribute__((address_space(3))) v4i*)src;
+          }
+        } else {
+          for (int e = 0; e < per && ch + e < p.n; ++e) {
+            if (p.out_bf16)
+              ((uint16_t*)p.out)[o + e] = f32_to_bf16(src[e]);
+            else
+              ((float*)p.out)[o + e] = src[e];
+          }
+        }
+      }
+    }
   } else {  // kEpiW2RouteI8: store_w2, csrc/moe/arm/i8mm_w8a8/kernels.cpp:248-257
     constexpr int RS = FN * 64 + 16;  // bytes per staged row (FN*16 fp32 + pad)
     constexpr int UPR = FN * 4;       // 16-byte units per row
@@ -742,7 +802,7 @@ __device__ __forceinline__ void lds_gemm_body(const GemmParams& p, int n_blocks,
 #pragma unroll
   for (int j = 0; j < FN; ++j) gtile[j] = tile_of(wn, j, &tvalid[j]);
   const EpiMeta meta{(lds_cfloat_ptr)meta_rs, (lds_cint_ptr)meta_orow, (lds_cfloat_ptr)meta_cs, wn * FN};
-  if constexpr (EPI == kEpiW13SwigluI8 || EPI == kEpiW2RouteI8) {
+  if constexpr (EPI == kEpiW13SwigluI8 || EPI == kEpiW2RouteI8 || EPI == kEpiI8Gemm) {
     static_assert(WAVES * staged_slice_bytes<FN>(EPI) <= SA * A_BYTES + SB * B_BYTES, "staging slices fit the stages");
     // every wave is past its last chunk's fragment reads: the stages are free
     __builtin_amdgcn_s_barrier();
@@ -846,8 +906,23 @@ int launch_lds_bm(int bm, const GemmParams& p, int64_t max_tiles, hipStream_t st
       // ran slower that way (C3 0.530 -> 0.586 ms) and keeps 8 waves.
       if constexpr (epi_pair(EPI))
         return launch_lds_cfg<I8, EPI, 8, 6, 2, 3, 0, 64, 2, 2>(p, max_tiles, stream);
-      else
-        return launch_lds_cfg<I8, EPI, 8, 6, 2, 3, 0, 128>(p, max_tiles, stream);
+      // i8gemm (one expert, the row tiles known on the host): 256 x 256
+      // workgroups where they need fewer rounds of the CUs than 256 x 384
+      // ones, weighing a round by its channels and the 128 x 64 wave tile's
+      // ~6% lower MFMA rate (the LDS loop probe: 3.87 vs 4.12 POPS). DeepSeek
+      // V4's wo_b ([7168, 16384]) on 256 CUs: 448 items in 2 rounds instead
+      // of 304 in 2, at 1024 / 2048 / 4096 rows 0.295 / 0.337 / 0.636 ->
+      // 0.224 / 0.290 / 0.562 ms. The pair's Q projection (K = 1536) gains
+      // nothing either way; 4-wave workgroups two per CU were no faster.
+      if constexpr (EPI == kEpiI8Gemm) {
+        if (p.cus > 0 && p.n_groups == 1) {
+          const int64_t r384 = ceil_div(max_tiles * ceil_div(p.n_tiles, 24), p.cus);
+          const int64_t r256 = ceil_div(max_tiles * ceil_div(p.n_tiles, 16), p.cus);
+          if (r256 * 16 * 106 < r384 * 24 * 100)
+            return launch_lds_cfg<I8, EPI, 8, 4, 2, 3, 0, 128, 2, 4>(p, max_tiles, stream);
+        }
+      }
+      return launch_lds_cfg<I8, EPI, 8, 6, 2, 3, 0, 128>(p, max_tiles, stream);
     default:
       return fail(FCMOE_EINVAL, "unsupported LDS tile rows");
   }

@@ -1,4 +1,4 @@
-// fcmoe_gemm_smallm.hip -- i8gemm at few rows (M <= 64), weight streaming.
+// fcmoe_gemm_smallm.hip -- i8gemm at few rows (M <= 128), weight streaming.
 //
 // At decode batch sizes an i8gemm is a weight stream: DeepSeek's attention
 // output projection at 64 rows reads 117 MB of int8 weights for 15 GOP. The
@@ -23,7 +23,7 @@
 // (float)acc * s_x * s_w left to right, + bias, then bf16 (RNE) or fp32.
 //
 // The same kernel runs the BF16 dense MLP at few rows (one packed expert, at
-// most 64 routes: the shared MLP at decode batch sizes) on
+// most 128 routes: the shared MLP at decode batch sizes) on
 // v_mfma_f32_16x16x32_bf16: A rows gathered through the route order's token
 // map, fp32 partial sums always written, and a reduce launch that adds the
 // splits in split order and applies the W13 activation (gate + bias,
@@ -88,6 +88,7 @@ __global__ __launch_bounds__(kSmWaves * kWave) void smallm_kernel(SmallMArgs p) 
 #if __HIP_DEVICE_COMPILE__
   constexpr int D = kSmDepth;
   constexpr int ABYTES = FM * 1024;  // 16 FM rows x 64 bytes
+  static_assert(FM <= kSmWaves, "one A load per wave and chunk covers every row fragment");
   typedef typename Acc<I8>::type AccT;
   __shared__ __attribute__((aligned(1024))) uint8_t sa[D * ABYTES];
   const int lane = threadIdx.x % kWave;
@@ -284,15 +285,19 @@ int launch_gemm(const SmallMArgs& p0, int64_t splits, bool i8, hipStream_t strea
       hipLaunchKernelGGL((smallm_kernel<true, 1>), grid, block, 0, stream, p);
     else if (fm == 2)
       hipLaunchKernelGGL((smallm_kernel<true, 2>), grid, block, 0, stream, p);
-    else
+    else if (fm <= 4)
       hipLaunchKernelGGL((smallm_kernel<true, 4>), grid, block, 0, stream, p);
+    else
+      hipLaunchKernelGGL((smallm_kernel<true, 8>), grid, block, 0, stream, p);
   } else {
     if (fm == 1)
       hipLaunchKernelGGL((smallm_kernel<false, 1>), grid, block, 0, stream, p);
     else if (fm == 2)
       hipLaunchKernelGGL((smallm_kernel<false, 2>), grid, block, 0, stream, p);
-    else
+    else if (fm <= 4)
       hipLaunchKernelGGL((smallm_kernel<false, 4>), grid, block, 0, stream, p);
+    else
+      hipLaunchKernelGGL((smallm_kernel<false, 8>), grid, block, 0, stream, p);
   }
   return check_launch("smallm_gemm");
 }

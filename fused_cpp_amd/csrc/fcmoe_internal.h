@@ -172,6 +172,9 @@ struct GemmParams {
   const int32_t* part_tiles;
   int32_t* part_queue;
   int part_exit;
+  // i8gemm: the device's CUs (0: unknown); the 256-row launch picks its
+  // workgroup width (384 or 256 channels) from the rounds of items it needs.
+  int cus;
 };
 
 // Whether a launch's plan gate lets it run (device side).
@@ -202,7 +205,7 @@ int gemm_launch(int epi, int bm, const GemmParams& p, int64_t max_tiles, hipStre
 // wave, weights read once, K split over about one workgroup per CU.
 // smallm_splits: the K splits for a shape (0 outside the domain);
 // smallm_workspace_bytes: the splits' int32 partial sums (0 with one split).
-constexpr int64_t kSmallMRows = 64;
+constexpr int64_t kSmallMRows = 128;
 int64_t smallm_splits(int64_t m, int64_t k, int64_t n);
 size_t smallm_workspace_bytes(int64_t m, int64_t k, int64_t n);
 int smallm_i8gemm_launch(const int8_t* a, int64_t lda, int64_t m, int64_t k, const void* w_packed,

@@ -305,9 +305,10 @@ def test_routed_shared_equals_explicit_combined_route(gpu):
 
 
 @pytest.mark.parametrize("T,Hd,F,activation,bias", [(1, 7168, 2048, "silu", False), (17, 200, 72, "gelu", True),
-                                                    (64, 7168, 2048, "silu", True), (40, 96, 40, "silu", False)])
+                                                    (64, 7168, 2048, "silu", True), (40, 96, 40, "silu", False),
+                                                    (97, 1000, 300, "gelu", True), (128, 7168, 2048, "silu", False)])
 def test_bf16_single_expert_small_rows_within_tolerance(gpu, oracle_lib, monkeypatch, T, Hd, F, activation, bias):
-    """One packed expert and at most 64 routes run both GEMMs on the small-M
+    """One packed expert and at most 128 routes run both GEMMs on the small-M
     kernel (split K, fp32 partial sums added in split order, the activation
     and route stores in the reduce launches): the shared MLP and a one-expert
     MoE against the fp32 reference, with biases, ragged H/F (zero-padded K),
@@ -371,9 +372,17 @@ def test_shared_mlp_equals_one_expert_moe(gpu, rows):
 
 @pytest.mark.parametrize("m,k,n,out_dtype", [(1, 7, 5, torch.float32), (4, 16, 8, torch.bfloat16),
                                              (9, 31, 13, torch.bfloat16), (24, 64, 96, torch.float32),
-                                             (24, 64, 96, torch.bfloat16), (300, 7168, 512, torch.bfloat16)])
+                                             (24, 64, 96, torch.bfloat16), (300, 7168, 512, torch.bfloat16),
+                                             (520, 2048, 1000, torch.float32),
+                                             (2048, 100, 8448, torch.bfloat16), (200, 640, 1001, torch.bfloat16),
+                                             (1000, 300, 998, torch.float32)])
 def test_i8gemm_bit_exact(gpu, oracle_lib, m, k, n, out_dtype):
-    """tests/test_i8gemm.py:40-94 shapes (+ a DSv3-width projection)."""
+    """tests/test_i8gemm.py:40-94 shapes (+ a DSv3-width projection; 256-row
+    tiles on 256-channel workgroups with a ragged last row tile and channel
+    block (520 rows); and 2048 x 8448, which on 256 CUs needs one round of
+    256 x 384 workgroups against two of 256 x 256 and takes the former; the
+    epilogue's 16-byte row pieces and its channel-by-channel fallback for row
+    strides that are not a multiple of the piece (1001, 998 channels))."""
     from fused_cpp_amd import i8gemm
 
     torch.manual_seed(0)
@@ -400,9 +409,12 @@ def test_i8gemm_bit_exact(gpu, oracle_lib, m, k, n, out_dtype):
     (33, 1536, 4096, True, torch.bfloat16),   # three row fragments, a few splits
     (64, 8192, 7168, False, torch.bfloat16),  # wo_b-like width, 5 splits
     (64, 2048, 24576, False, torch.float32),  # many channel groups, one split
+    (65, 3000, 700, True, torch.float32),     # five row fragments (the 8-fragment kernel, rows past m)
+    (100, 7168, 2048, False, torch.bfloat16),
+    (128, 16384, 1024, True, torch.bfloat16),  # the largest small-M product
 ])
 def test_i8gemm_small_m_split_k_bit_exact(gpu, oracle_lib, m, k, n, bias, out_dtype):
-    """i8gemm at <= 64 rows runs the small-M kernel (all rows per wave, K split
+    """i8gemm at <= 128 rows runs the small-M kernel (all rows per wave, K split
     over the grid with int32 partial sums): bit-exact against the oracle, with
     extreme int8 values and rows of zeros (scale 1)."""
     from fused_cpp_amd import i8gemm

@@ -1094,7 +1094,21 @@ def main() -> int:
     ap.add_argument("--probe", action="store_true",
                     help="only run the library's measurement probes (streaming ceiling, MFMA loop rates, MFMA "
                          "beside streaming waves, release-fence cost) and print them as one JSON line")
+    ap.add_argument("--ops", action="store_true",
+                    help="only run the operator entries (i8gemm, i8gemm pair, shared MLP at the DeepSeek V4 "
+                         "shapes) and print them as one JSON line")
     args = ap.parse_args()
+    if args.ops:
+        if args.gpus != 1:
+            print(json.dumps({"error": "this build measures one GPU only: run with --gpus 1"}))
+            return 2
+        import torch
+
+        device = torch.device("cuda", 0)
+        ops = [dict(measure_op(wl, op, M, K, Ns, args, device, want_cpu=not args.no_cpu_baseline), name=wl)
+               for wl, op, M, K, Ns in OP_SECONDARY]
+        print(json.dumps({"ops": ops}), flush=True)
+        return 0
     if args.probe:
         return probes()
     if args.int_mm_reference:

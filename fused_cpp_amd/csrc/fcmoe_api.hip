@@ -1132,7 +1132,9 @@ int i8gemm_run(const I8Layout& L, int64_t k, const void* w_packed, const float* 
     p.tiles = L.tiles + 2 * tile_offset(L.tc, c);
     p.tile_count = L.tile_count + c;
     Stage st(FCMOE_STAGE_W13_CLASS0 + class_slot(L.tc.bm[c]), stream);
-    const int rc = gemm_launch(kEpiI8Gemm, L.tc.bm[c], p, L.tc.bound[c], stream);
+    // its tiles exactly: one below the last class, ceil(m / bm) in it
+    const int64_t tiles = c == L.tc.n - 1 ? ceil_div(L.m, L.tc.bm[c]) : 1;
+    const int rc = gemm_launch(kEpiI8Gemm, L.tc.bm[c], p, tiles, stream);
     if (rc) return rc;
   }
   return FCMOE_OK;

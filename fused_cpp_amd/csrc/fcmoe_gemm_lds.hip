@@ -912,8 +912,11 @@ int launch_lds_bm(int bm, const GemmParams& p, int64_t max_tiles, hipStream_t st
       // ~6% lower MFMA rate (the LDS loop probe: 3.87 vs 4.12 POPS). DeepSeek
       // V4's wo_b ([7168, 16384]) on 256 CUs: 448 items in 2 rounds instead
       // of 304 in 2, at 1024 / 2048 / 4096 rows 0.295 / 0.337 / 0.636 ->
-      // 0.224 / 0.290 / 0.562 ms. The pair's Q projection (K = 1536) gains
-      // nothing either way; 4-wave workgroups two per CU were no faster.
+      // 0.224 / 0.290 / 0.562 ms. The pair's [24576, 1536] takes 256 x 384
+      // (1024 items in 4 rounds, not 1536 in 6) and its [8192, 1536] 256 x
+      // 256: 0.317 -> 0.294 ms at 4096 rows, against 0.310 / 0.294 with
+      // either width for both. max_tiles must be the exact row-tile count.
+      // 4-wave workgroups two per CU were no faster.
       if constexpr (EPI == kEpiI8Gemm) {
         if (p.cus > 0 && p.n_groups == 1) {
           const int64_t r384 = ceil_div(max_tiles * ceil_div(p.n_tiles, 24), p.cus);

@@ -775,6 +775,7 @@ OP_SECONDARY = [("i8gemm_pair_q_m64", "pair", 64, 1536, (24576, 8192)),
                 ("i8gemm_pair_q_m4096", "pair", 4096, 1536, (24576, 8192)),
                 ("i8gemm_wo_b_m64", "single", 64, 16384, (7168,)),
                 ("i8gemm_wo_b_m128", "single", 128, 16384, (7168,)),
+                ("i8gemm_wo_b_m512", "single", 512, 16384, (7168,)),
                 ("i8gemm_wo_b_m4096", "single", 4096, 16384, (7168,)),
                 ("shared_mlp_t64", "shared_mlp", 64, 7168, (2048,)),
                 ("shared_mlp_t128", "shared_mlp", 128, 7168, (2048,))]

@@ -23,6 +23,7 @@ thread_local std::string g_error;
 // index of a size here is its stage-timing slot. i8gemm and the diagnostic
 // grouped GEMM use all six.
 constexpr int kClassBM[] = {16, 32, 64, 128, 192, 256};
+constexpr int kI8ClassBM[] = {256};  // i8gemm above kSmallMRows rows
 constexpr int kNumClasses = 6;
 // Decode: when an expert averages at most this many routed rows, everything
 // (the shared expert too, in several 16-row tiles) runs in the single BM=16
@@ -1059,7 +1060,9 @@ I8Layout i8_layout(int64_t m, int64_t k, size_t partial_bytes, Arena& ar) {
   I8Layout L;
   L.m = m;
   L.kp = round_up(k, 64);
-  L.tc = make_tile_classes(kClassBM, decode_rows(m, 1) ? 1 : kNumClasses, m, 1);
+  // above the small-M kernel's rows the one expert takes 256-row tiles (the
+  // 192-row tile has no register room for split K)
+  L.tc = make_tile_classes(kI8ClassBM, 1, m, 1);
   L.xq = ar.take<int8_t>(m * L.kp);
   L.xs = ar.take<float>(m);
   L.counts = ar.take<int32_t>(1);
@@ -1074,14 +1077,46 @@ I8Layout i8_layout(int64_t m, int64_t k, size_t partial_bytes, Arena& ar) {
 }
 }  // namespace
 
+namespace {
+// K splits of an i8gemm above the small-M kernel's rows, on the LDS-staged
+// tiles: when its items (row tiles x channel blocks of the 256 x 384 / 192 x
+// 512 tiles) fill less than half of the CUs, K is cut into ranges of an even
+// number of chunks, at least 16, so that about one item runs per CU; the
+// splits' int32 sums go to the workspace and a reduce launch applies the
+// epilogue. Returns the splits (1: none) and the chunks per split.
+int64_t i8gemm_lds_splits(int64_t m, int64_t k, int64_t n, int64_t* cps_out) {
+  const int64_t kc = ceil_div(k, 64), nt = ceil_div(n, 16);
+  if (cps_out) *cps_out = kc;
+  if (m <= kSmallMRows) return 1;
+  // only the LDS-staged tiles take K ranges (A and the weights under 2 GiB)
+  if (m * kc * 64 >= kLdsMaxABytes || fcmoe_packed_expert_bytes(1, n, k, 1) >= kLdsMaxABytes) return 1;
+  const int64_t items = m <= 192 ? ceil_div(nt, 32) : ceil_div(m, 256) * ceil_div(nt, 24);
+  int64_t s = persistent_wgs() / items;  // (2 or 4 times as many: slower at 300-4096 rows)
+  if (s > kc / 16) s = kc / 16;
+  if (s < 2) return 1;
+  int64_t cps = ceil_div(kc, s);
+  cps += cps & 1;
+  if (cps_out) *cps_out = cps;
+  return ceil_div(kc, cps);
+}
+
+// Partial-sum bytes of one i8gemm: the small-M kernel's, or the LDS tiles'
+// K splits.
+size_t i8gemm_partial_bytes(int64_t m, int64_t k, int64_t n) {
+  if (m <= kSmallMRows) return smallm_workspace_bytes(m, k, n);
+  const int64_t s = i8gemm_lds_splits(m, k, n, nullptr);
+  return s > 1 ? (size_t)(s * m * n) * sizeof(int32_t) : 0;
+}
+}  // namespace
+
 extern "C" size_t fcmoe_i8gemm_workspace_bytes(int64_t m, int64_t k, int64_t n) {
   Arena ar;
-  i8_layout(m, k, smallm_workspace_bytes(m, k, n), ar);
+  i8_layout(m, k, i8gemm_partial_bytes(m, k, n), ar);
   return ar.used + 256;
 }
 
 extern "C" size_t fcmoe_i8gemm_pair_workspace_bytes(int64_t m, int64_t k, int64_t n1, int64_t n2) {
-  const size_t p1 = smallm_workspace_bytes(m, k, n1), p2 = smallm_workspace_bytes(m, k, n2);
+  const size_t p1 = i8gemm_partial_bytes(m, k, n1), p2 = i8gemm_partial_bytes(m, k, n2);
   Arena ar;
   i8_layout(m, k, p1 > p2 ? p1 : p2, ar);
   return ar.used + 256;
@@ -1117,6 +1152,16 @@ int i8gemm_run(const I8Layout& L, int64_t k, const void* w_packed, const float* 
   g.bias = bias;
   g.out_bf16 = out_is_bf16;
   g.cus = persistent_wgs();
+  int64_t cps = 0;
+  const int64_t splits = i8gemm_lds_splits(L.m, k, n, &cps);
+  if (splits > 1) {
+    if (!L.partial || L.partial_bytes < (size_t)(splits * L.m * n) * sizeof(int32_t))
+      return fail(FCMOE_ESPACE, "i8gemm: split-K partial-sum workspace too small");
+    g.k_total = g.k_chunks;
+    g.k_chunks = cps;
+    g.split_out = L.partial;
+    g.split_rows = L.m;
+  }
   // One expert of m rows: only its class (rows in (bm[c-1], bm[c]], the last
   // class above) gets tiles, so the other classes' launches are not enqueued
   // (5 empty launches cost the 4096-row pair ~0.04 ms).
@@ -1136,6 +1181,8 @@ int i8gemm_run(const I8Layout& L, int64_t k, const void* w_packed, const float* 
     const int64_t tiles = c == L.tc.n - 1 ? ceil_div(L.m, L.tc.bm[c]) : 1;
     const int rc = gemm_launch(kEpiI8Gemm, L.tc.bm[c], p, tiles, stream);
     if (rc) return rc;
+    if (splits > 1)
+      return i8gemm_reduce_launch(L.partial, splits, L.m, n, L.xs, w_scale, bias, out, out_is_bf16, stream);
   }
   return FCMOE_OK;
 }
@@ -1168,7 +1215,7 @@ extern "C" int fcmoe_i8gemm(const void* x, int x_is_f32, int64_t m, int64_t k, c
   if (m == 0) return FCMOE_OK;
   if (m > INT32_MAX / 2) return fail(FCMOE_EINVAL, "i8gemm: too many rows");
   I8Layout L;
-  int rc = i8gemm_prologue(x, x_is_f32, m, k, smallm_workspace_bytes(m, k, n), workspace, workspace_bytes, &L, stream);
+  int rc = i8gemm_prologue(x, x_is_f32, m, k, i8gemm_partial_bytes(m, k, n), workspace, workspace_bytes, &L, stream);
   if (rc) return rc;
   return i8gemm_run(L, k, w_packed, w_scale, n, bias, out, out_is_bf16, stream);
 }
@@ -1182,7 +1229,7 @@ extern "C" int fcmoe_i8gemm_pair(const uint16_t* x, int64_t m, int64_t k, const 
   if (m > INT32_MAX / 2) return fail(FCMOE_EINVAL, "i8gemm_pair: too many rows");
   if (!x || !out1 || !out2) return fail(FCMOE_EINVAL, "i8gemm_pair: NULL tensor");
   I8Layout L;
-  const size_t p1 = smallm_workspace_bytes(m, k, n1), p2 = smallm_workspace_bytes(m, k, n2);
+  const size_t p1 = i8gemm_partial_bytes(m, k, n1), p2 = i8gemm_partial_bytes(m, k, n2);
   int rc = i8gemm_prologue(x, 0, m, k, p1 > p2 ? p1 : p2, workspace, workspace_bytes, &L, stream);
   if (rc) return rc;
   if ((rc = i8gemm_run(L, k, w1_packed, w1_scale, n1, nullptr, out1, 1, stream))) return rc;

@@ -286,8 +286,11 @@ __device__ __forceinline__ void staged_epilogue(const GemmParams& p, const v4i (
       cs[j] = m.cs[(m.cbase + j) * 16 + col];
       cb[j] = p.bias && tvalid[j] && ch < p.n ? p.bias[ch] : 0.0f;
     }
-    const int per = p.out_bf16 ? 8 : 4;  // channels per 16-byte piece
-    const bool vec = p.ldo % per == 0 && ((uintptr_t)p.out & 15) == 0;
+    // split K: this split's raw int32 sums, [split_rows, n] at split_out + split * split_rows * n
+    const bool raw = p.k_total > 0;
+    int32_t* const rout = raw ? p.split_out + (int64_t)blockIdx.y * p.split_rows * p.n : nullptr;
+    const int per = p.out_bf16 && !raw ? 8 : 4;  // channels per 16-byte piece
+    const bool vec = raw ? p.n % 4 == 0 : p.ldo % per == 0 && ((uintptr_t)p.out & 15) == 0;
     const int upr = FN * 16 / per;       // pieces per staged row
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
@@ -301,7 +304,8 @@ __device__ __forceinline__ void staged_epilogue(const GemmParams& p, const v4i (
         for (int j = 0; j < FN; ++j) {
           float v = (float)acc[i][j][q] * rs * cs[j];
           if (p.bias) v = v + cb[j];
-          *(__attribute__((address_space(3))) float*)(slice + (rq + q) * RS + (j * 16 + col) * 4) = v;
+          *(__attribute__((address_space(3))) float*)(slice + (rq + q) * RS + (j * 16 + col) * 4) =
+              raw ? __int_as_float(acc[i][j][q]) : v;
         }
       }
       for (int idx = lane; idx < 16 * upr; idx += kWave) {
@@ -309,10 +313,16 @@ __device__ __forceinline__ void staged_epilogue(const GemmParams& p, const v4i (
         const int r = rbase + row;
         const int64_t ch = c0 + (int64_t)u * per;
         if (r >= rows || ch >= p.n) continue;
-        const int64_t o = (int64_t)(pos0 + r) * p.ldo + ch;
+        const int64_t o = (int64_t)(pos0 + r) * (raw ? p.n : p.ldo) + ch;
         const __attribute__((address_space(3))) float* src =
             (const __attribute__((address_space(3))) float*)(slice + row * RS + u * per * 4);
-        if (vec && ch + per <= p.n) {
+        if (raw) {
+          if (vec && ch + per <= p.n) {
+            *(v4i*)(rout + o) = *(const __attribute__((address_space(3))) v4i*)src;
+          } else {
+            for (int e = 0; e < per && ch + e < p.n; ++e) rout[o + e] = __float_as_int(src[e]);
+          }
+        } else if (vec && ch + per <= p.n) {
           if (p.out_bf16) {
             uint32_t w[4];
 #pragma unroll
@@ -514,7 +524,15 @@ __device__ __forceinline__ void lds_gemm_body(const GemmParams& p, int n_blocks,
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int wm = wave / WNW;
   const int wn = wave % WNW;
-  const int64_t kc = p.k_chunks;
+  // K range: all k_chunks chunks, or (split K, k_total > 0) split blockIdx.y's
+  // range of k_chunks chunks out of k_total (the host sizes the splits so
+  // that every range is non-empty and, with two-chunk A stages, starts even)
+  // (compiled for the i8gemm epilogue only: the other tiles' register
+  // budgets have no room for it)
+  constexpr bool SPLIT = EPI == kEpiI8Gemm && !PERSIST;
+  const int64_t ktot = SPLIT && p.k_total > 0 ? p.k_total : p.k_chunks;
+  const int64_t kbeg = SPLIT && p.k_total > 0 ? (int64_t)blockIdx.y * p.k_chunks : 0;
+  const int64_t kc = p.k_chunks < ktot - kbeg ? p.k_chunks : ktot - kbeg;
   const int64_t total_tiles = (int64_t)p.n_groups * p.n_tiles;
 
   // channel tile (index within the expert) of wave column wn_, slot j
@@ -567,7 +585,7 @@ __device__ __forceinline__ void lds_gemm_body(const GemmParams& p, int n_blocks,
     while (t >= LB) t -= LB;
     bool valid;
     const int64_t gt = tile_of(t / FN, t % FN, &valid);
-    voff_b[u] = (uint32_t)__builtin_amdgcn_readfirstlane((int)((valid ? gt : 0) * kc * 1024));
+    voff_b[u] = (uint32_t)__builtin_amdgcn_readfirstlane((int)((valid ? gt : 0) * ktot * 1024));
     lds_b[u] = t * 1024;
   }
   // Past the end a ring re-loads the last chunk (never read).
@@ -578,15 +596,15 @@ __device__ __forceinline__ void lds_gemm_body(const GemmParams& p, int n_blocks,
   const bool a_hi = AWIDE && ((lane % 8) ^ ((((wave & 1) << 2) | (lane >> 4)) & 7)) >= 4;
   auto issue_a = [&](int64_t c, int stage) {
     const int64_t cc = c < a_stages ? c : a_stages - 1;
-    const int soff = (int)(cc * AW);
-    const bool fold = APAIR && 2 * cc + 1 >= kc;
+    const int soff = (int)(kbeg * 64 + cc * AW);
+    const bool fold = APAIR && kbeg + 2 * cc + 1 >= ktot;
 #pragma unroll
     for (int u = 0; u < LPA; ++u)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_a, (lds_ptr_t)(smem + stage * A_BYTES + lds_a[u]), 16,
                                                fold && a_hi ? voff_a[u] - 64 : voff_a[u], soff, 0, 0);
   };
   auto issue_b = [&](int64_t c, int stage) {
-    const int soff = (int)((c < kc ? c : kc - 1) * 1024);
+    const int soff = (int)((kbeg + (c < kc ? c : kc - 1)) * 1024);
 #pragma unroll
     for (int u = 0; u < LPB; ++u)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_b, (lds_ptr_t)(smem_b + stage * B_BYTES + lds_b[u]), 16,
@@ -849,6 +867,9 @@ int launch_lds_cfg(const GemmParams& p, int64_t max_tiles, hipStream_t stream) {
   const int64_t items = max_tiles * n_blocks + (partial ? kXcds : 0);
   if (items > INT32_MAX) return fail(FCMOE_EINVAL, "grouped gemm grid too large");
   const int64_t grid = PERSIST && items > p.persist ? p.persist : items;
+  // split K (non-persistent launches only): one grid row per K range
+  const int64_t splits = !PERSIST && p.k_total > 0 ? ceil_div(p.k_total, p.k_chunks) : 1;
+  if (splits > 65535) return fail(FCMOE_EINVAL, "grouped gemm: too many K splits");
   // 32-bit buffer offsets: A rows and one expert's packed weights
   if (p.w_expert_bytes >= 0x7ffffff0) return fail(FCMOE_EINVAL, "expert weights exceed 2 GiB");
   static const int gm = [] {
@@ -867,8 +888,9 @@ int launch_lds_cfg(const GemmParams& p, int64_t max_tiles, hipStream_t stream) {
                        dim3((unsigned)grid), dim3(WMW * WNW * kWave), 0, stream, p, (int)n_blocks, partial,
                        gm_launch, (int)items);
   else
-    hipLaunchKernelGGL((grouped_gemm_lds_kernel<I8, EPI, FM, FN, SA, SB, BPOL, AW, WMW, WNW>), dim3((unsigned)grid),
-                       dim3(WMW * WNW * kWave), 0, stream, p, (int)n_blocks, partial, gm, (int)items);
+    hipLaunchKernelGGL((grouped_gemm_lds_kernel<I8, EPI, FM, FN, SA, SB, BPOL, AW, WMW, WNW>),
+                       dim3((unsigned)grid, (unsigned)splits), dim3(WMW * WNW * kWave), 0, stream, p, (int)n_blocks,
+                       partial, gm, (int)items);
   return check_launch("grouped_gemm_lds");
 }
 
@@ -891,7 +913,9 @@ int launch_lds_bm(int bm, const GemmParams& p, int64_t max_tiles, hipStream_t st
       // from 2.33 to 2.10 ms: fewer L2 requests per A byte leave more of the
       // CU's outstanding-request budget to the weight stream. The bf16
       // epilogues would spill with them and keep 64-byte A stages.
-      if constexpr (I8)
+      if constexpr (EPI == kEpiI8Gemm)  // i8gemm takes 256-row tiles above the small-M kernel's rows
+        return fail(FCMOE_EINVAL, "i8gemm has no 192-row tile");
+      else if constexpr (I8)
         return launch_lds_cfg<I8, EPI, 6, 8, 2, 3, kNT, 128>(p, max_tiles, stream);
       else
         return launch_lds_cfg<I8, EPI, 6, 8, 3, 3, kNT, 64>(p, max_tiles, stream);
@@ -919,8 +943,9 @@ int launch_lds_bm(int bm, const GemmParams& p, int64_t max_tiles, hipStream_t st
       // 4-wave workgroups two per CU were no faster.
       if constexpr (EPI == kEpiI8Gemm) {
         if (p.cus > 0 && p.n_groups == 1) {
-          const int64_t r384 = ceil_div(max_tiles * ceil_div(p.n_tiles, 24), p.cus);
-          const int64_t r256 = ceil_div(max_tiles * ceil_div(p.n_tiles, 16), p.cus);
+          const int64_t sp = p.k_total > 0 ? ceil_div(p.k_total, p.k_chunks) : 1;  // K splits
+          const int64_t r384 = ceil_div(max_tiles * ceil_div(p.n_tiles, 24) * sp, p.cus);
+          const int64_t r256 = ceil_div(max_tiles * ceil_div(p.n_tiles, 16) * sp, p.cus);
           if (r256 * 16 * 106 < r384 * 24 * 100)
             return launch_lds_cfg<I8, EPI, 8, 4, 2, 3, 0, 128, 2, 4>(p, max_tiles, stream);
         }

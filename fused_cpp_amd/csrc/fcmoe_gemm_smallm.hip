@@ -348,6 +348,24 @@ int smallm_i8gemm_launch(const int8_t* a, int64_t lda, int64_t m, int64_t k, con
   return check_launch("smallm_reduce");
 }
 
+int i8gemm_reduce_launch(const int32_t* partial, int64_t splits, int64_t m, int64_t n, const float* scale_row,
+                         const float* scale_col, const float* bias, void* out, int out_bf16, hipStream_t stream) {
+  if (splits < 1 || m <= 0 || n <= 0 || m * n > INT32_MAX) return fail(FCMOE_EINVAL, "i8gemm reduce: bad shape");
+  SmallMArgs p{};
+  p.m = (int)m;
+  p.n = n;
+  p.n_half = n;
+  p.scale_row = scale_row;
+  p.scale_col = scale_col;
+  p.bias = bias;
+  p.out = out;
+  p.out_bf16 = out_bf16;
+  p.ldo = n;
+  p.partial = const_cast<int32_t*>(partial);
+  hipLaunchKernelGGL(smallm_reduce_kernel, dim3(reduce_blocks(m * n)), dim3(256), 0, stream, p, (int)splits);
+  return check_launch("i8gemm_reduce");
+}
+
 int64_t smallm_bf16_splits(int64_t m, int64_t k_chunks, int64_t tiles) { return splits_for(m, k_chunks, tiles); }
 
 int smallm_bf16_launch(const SmallMBf16& q, hipStream_t stream) {

@@ -175,6 +175,13 @@ struct GemmParams {
   // i8gemm: the device's CUs (0: unknown); the 256-row launch picks its
   // workgroup width (384 or 256 channels) from the rounds of items it needs.
   int cus;
+  // i8gemm split K (LDS kernel): k_total > 0 splits the k_total chunks into
+  // ranges of k_chunks (grid.y = split); split s writes its raw int32 sums to
+  // split_out + s * m * n ([m, n] row-major, m = split_rows), and a reduce
+  // launch adds the splits and applies the epilogue.
+  int64_t k_total;
+  int32_t* split_out;
+  int64_t split_rows;
 };
 
 // Whether a launch's plan gate lets it run (device side).
@@ -207,6 +214,10 @@ int gemm_launch(int epi, int bm, const GemmParams& p, int64_t max_tiles, hipStre
 // smallm_workspace_bytes: the splits' int32 partial sums (0 with one split).
 constexpr int64_t kSmallMRows = 128;
 int64_t smallm_splits(int64_t m, int64_t k, int64_t n);
+// Adds splits x [m, n] int32 partial sums in split order and applies the
+// i8gemm epilogue (write_scaled_output) into out [m, n].
+int i8gemm_reduce_launch(const int32_t* partial, int64_t splits, int64_t m, int64_t n, const float* scale_row,
+                         const float* scale_col, const float* bias, void* out, int out_bf16, hipStream_t stream);
 size_t smallm_workspace_bytes(int64_t m, int64_t k, int64_t n);
 int smallm_i8gemm_launch(const int8_t* a, int64_t lda, int64_t m, int64_t k, const void* w_packed,
                          const float* scale_row, const float* scale_col, int64_t n, const float* bias, void* out,

@@ -72,9 +72,10 @@ def test_wo_b_alias_out_and_bf16_prepare_quantises_like_the_oracle(gpu, oracle_l
 
 
 @pytest.mark.parametrize("m,k,n1,n2", [(24, 64, 96, 128), (2, 64, 13, 21), (7, 7168, 1536, 512), (300, 1024, 80, 48),
-                                      (40, 2048, 2048, 512)])
+                                      (40, 2048, 2048, 512), (300, 8192, 7168, 512)])
 def test_pair_equals_two_single_projections(gpu, m, k, n1, n2):
-    """tests/test_deepseek_v4_w8a8.py:62-96 (incl. logical N tails) plus DSv3 Q-projection widths."""
+    """tests/test_deepseek_v4_w8a8.py:62-96 (incl. logical N tails) plus DSv3 Q-projection widths
+    (and 300 rows at K = 8192, where the two GEMMs split K 6 and 8 ways)."""
     from fused_cpp_amd.deepseek_v4_w8a8 import (deepseek_v4_w8a8_linear, deepseek_v4_w8a8_linear_pair,
                                                  prepare_deepseek_v4_w8a8_linear_quantized_weight)
 

@@ -181,8 +181,11 @@ int fcmoe_w8a16_forward(const fcmoe_moe_args* args, hipStream_t stream);
  * bf16 (out_is_bf16) or fp32 [m, n]. Replaces i8gemm_dynamic_scaled_mm
  * (csrc/i8gemm.cpp:318-452) behind i8gemm.dynamic_scaled_mm
  * (src/fused_cpp/i8gemm.py:88-137). Workspace: fcmoe_i8gemm_workspace_bytes(m,
- * k, n): at m <= 128 rows it includes the K splits' int32 partial sums
- * (splits x m x n, none when one split covers K), so it depends on n. */
+ * k, n): it includes the K splits' int32 partial sums (splits x m x n; none
+ * when one split covers K), so it depends on n; above 128 rows the split
+ * count also depends on the current device's CU count, so query it with the
+ * device current that the call will run on (a smaller workspace is refused
+ * with FCMOE_ESPACE). */
 size_t fcmoe_i8gemm_workspace_bytes(int64_t m, int64_t k, int64_t n);
 int fcmoe_i8gemm(const void* x, int x_is_f32, int64_t m, int64_t k, const void* w_packed, const float* w_scale,
                  int64_t n, const float* bias, void* out, int out_is_bf16, void* workspace, size_t workspace_bytes,

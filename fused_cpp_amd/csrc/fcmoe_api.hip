@@ -145,7 +145,7 @@ W8A8Layout w8a8_layout(const fcmoe_moe_args* a, Arena& ar) {
 // rows on the LDS-staged kernel (no 64-row W8A16 tile). The 192-row tile
 // takes experts of 129-192 rows off the 256-row one, which ran them at half
 // its rows (DSv3 shape, T = 4096 uniform: 4.63 -> 4.17 ms).
-// A BF16 forward over one packed expert with at most 128 routes (the shared
+// A BF16 forward over one packed expert with at most 256 routes (the shared
 // MLP, or a one-expert MoE, at decode batch sizes) runs its two GEMMs on the
 // small-M kernel (fcmoe_gemm_smallm.hip): every weight byte read once, K split
 // over about one workgroup per CU. The one-expert MoE and the shared MLP take
@@ -1079,8 +1079,8 @@ I8Layout i8_layout(int64_t m, int64_t k, size_t partial_bytes, Arena& ar) {
 
 namespace {
 // K splits of an i8gemm above the small-M kernel's rows, on the LDS-staged
-// tiles: when its items (row tiles x channel blocks of the 256 x 384 / 192 x
-// 512 tiles) fill less than half of the CUs, K is cut into ranges of an even
+// 256-row tiles: when its items (row tiles x 384-channel blocks) fill less
+// than half of the CUs, K is cut into ranges of an even
 // number of chunks, at least 16, so that about one item runs per CU; the
 // splits' int32 sums go to the workspace and a reduce launch applies the
 // epilogue. Returns the splits (1: none) and the chunks per split.
@@ -1090,7 +1090,7 @@ int64_t i8gemm_lds_splits(int64_t m, int64_t k, int64_t n, int64_t* cps_out) {
   if (m <= kSmallMRows) return 1;
   // only the LDS-staged tiles take K ranges (A and the weights under 2 GiB)
   if (m * kc * 64 >= kLdsMaxABytes || fcmoe_packed_expert_bytes(1, n, k, 1) >= kLdsMaxABytes) return 1;
-  const int64_t items = m <= 192 ? ceil_div(nt, 32) : ceil_div(m, 256) * ceil_div(nt, 24);
+  const int64_t items = ceil_div(m, 256) * ceil_div(nt, 24);
   int64_t s = persistent_wgs() / items;  // (2 or 4 times as many: slower at 300-4096 rows)
   if (s > kc / 16) s = kc / 16;
   if (s < 2) return 1;

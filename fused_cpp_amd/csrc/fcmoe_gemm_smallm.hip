@@ -1,4 +1,4 @@
-// fcmoe_gemm_smallm.hip -- i8gemm at few rows (M <= 128), weight streaming.
+// fcmoe_gemm_smallm.hip -- i8gemm at few rows (M <= 256), weight streaming.
 //
 // At decode batch sizes an i8gemm is a weight stream: DeepSeek's attention
 // output projection at 64 rows reads 117 MB of int8 weights for 15 GOP. The
@@ -23,7 +23,7 @@
 // (float)acc * s_x * s_w left to right, + bias, then bf16 (RNE) or fp32.
 //
 // The same kernel runs the BF16 dense MLP at few rows (one packed expert, at
-// most 128 routes: the shared MLP at decode batch sizes) on
+// most 256 routes: the shared MLP at decode batch sizes) on
 // v_mfma_f32_16x16x32_bf16: A rows gathered through the route order's token
 // map, fp32 partial sums always written, and a reduce launch that adds the
 // splits in split order and applies the W13 activation (gate + bias,
@@ -88,7 +88,9 @@ __global__ __launch_bounds__(kSmWaves * kWave) void smallm_kernel(SmallMArgs p) 
 #if __HIP_DEVICE_COMPILE__
   constexpr int D = kSmDepth;
   constexpr int ABYTES = FM * 1024;  // 16 FM rows x 64 bytes
-  static_assert(FM <= kSmWaves, "one A load per wave and chunk covers every row fragment");
+  constexpr int LA = (FM + kSmWaves - 1) / kSmWaves;  // A loads per wave and chunk
+  static_assert(FM <= kSmWaves || FM % kSmWaves == 0, "the waves' A loads cover every row fragment once");
+  constexpr int OPS = LA + 1;  // vector-memory ops per (A stage, weight chunk) pair
   typedef typename Acc<I8>::type AccT;
   __shared__ __attribute__((aligned(1024))) uint8_t sa[D * ABYTES];
   const int lane = threadIdx.x % kWave;
@@ -101,22 +103,27 @@ __global__ __launch_bounds__(kSmWaves * kWave) void smallm_kernel(SmallMArgs p) 
   // took a VGPR with a load in flight and drained the ring every 8 chunks)
   const int nch = (int)(c1 - c0);  // >= 1 (the host sizes the splits)
 
-  // A stage load of this wave: rows 16 g + lane / 4 with g = wave % FM (waves
-  // beyond FM repeat a load: same bytes to the same place, so every wave
-  // issues one A load per chunk and the wait counts are uniform). 16-byte
-  // unit u of row r sits at slot u ^ ((r >> 2) & 3): the 16 rows of a
-  // fragment read fall on distinct banks.
-  const int g = wave % FM;
-  const int ar = g * 16 + lane / 4;
+  // A stage loads of this wave: fragments g = (wave + 8 u) % FM, u < LA, rows
+  // 16 g + lane / 4 (with FM < 8, waves beyond FM repeat a load: same bytes to
+  // the same place, so every wave issues LA A loads per chunk and the wait
+  // counts are uniform). 16-byte unit u of row r sits at slot u ^ ((r >> 2) &
+  // 3): the 16 rows of a fragment read fall on distinct banks.
   const int aunit = (lane % 4) ^ ((lane >> 4) & 3);
   const int rows_valid = p.m_dev ? *p.m_dev : p.m;
-  const int arow_local = ar < rows_valid ? ar : (rows_valid > 0 ? rows_valid - 1 : 0);
-  // rows past the routed ones re-read the last routed row (or x row 0); their
-  // sums are never stored
-  const int64_t arow = p.row_map && rows_valid > 0 ? (int64_t)p.row_map[arow_local] : (int64_t)arow_local;
   const __amdgpu_buffer_rsrc_t rsrc_a =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p.a), (short)0, 0x7ffffff0, kSmBufWord3);
-  const uint32_t voff_a = (uint32_t)(arow * p.lda + aunit * 16);
+  int g[LA];
+  uint32_t voff_a[LA];
+#pragma unroll
+  for (int u = 0; u < LA; ++u) {
+    g[u] = (wave + kSmWaves * u) % FM;
+    const int ar = g[u] * 16 + lane / 4;
+    const int arow_local = ar < rows_valid ? ar : (rows_valid > 0 ? rows_valid - 1 : 0);
+    // rows past the routed ones re-read the last routed row (or x row 0);
+    // their sums are never stored
+    const int64_t arow = p.row_map && rows_valid > 0 ? (int64_t)p.row_map[arow_local] : (int64_t)arow_local;
+    voff_a[u] = (uint32_t)(arow * p.lda + aunit * 16);
+  }
   // The tile's weights through a buffer resource: the chunk offset goes in
   // the scalar operand and the lane offset is fixed, so no address VGPR is
   // computed per load (a 64-bit address written into a ring register with an
@@ -136,8 +143,10 @@ __global__ __launch_bounds__(kSmWaves * kWave) void smallm_kernel(SmallMArgs p) 
   auto issue = [&](int t, auto slot_c) {
     constexpr int slot = decltype(slot_c)::value;
     const int64_t c = c0 + (t < nch ? t : nch - 1);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_a, (sm_lds_ptr)(sa + slot * ABYTES + g * 1024), 16, voff_a,
-                                             (int)(c * 64), 0, 0);
+#pragma unroll
+    for (int u = 0; u < LA; ++u)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_a, (sm_lds_ptr)(sa + slot * ABYTES + g[u] * 1024), 16,
+                                               voff_a[u], (int)(c * 64), 0, 0);
     // keep each pair in issue order (A, then the weights): the wait counts
     // below, and the compiler's own for the weight registers, assume it
     __builtin_amdgcn_sched_barrier(0);
@@ -152,7 +161,7 @@ __global__ __launch_bounds__(kSmWaves * kWave) void smallm_kernel(SmallMArgs p) 
     constexpr int slot = decltype(slot_c)::value;
     // this wave's pair t has landed (pairs t+1 .. t+D-2 may not); after the
     // barrier every wave's A stage t has, and no wave reads stage t-1 any more
-    sm_wait_vmcnt<2 * (D - 2)>();
+    sm_wait_vmcnt<OPS * (D - 2)>();
     __builtin_amdgcn_s_barrier();
     issue(t + D - 1, std::integral_constant<int, (slot + D - 1) % D>{});
     v4i af[FM];
@@ -287,8 +296,10 @@ int launch_gemm(const SmallMArgs& p0, int64_t splits, bool i8, hipStream_t strea
       hipLaunchKernelGGL((smallm_kernel<true, 2>), grid, block, 0, stream, p);
     else if (fm <= 4)
       hipLaunchKernelGGL((smallm_kernel<true, 4>), grid, block, 0, stream, p);
-    else
+    else if (fm <= 8)
       hipLaunchKernelGGL((smallm_kernel<true, 8>), grid, block, 0, stream, p);
+    else
+      hipLaunchKernelGGL((smallm_kernel<true, 16>), grid, block, 0, stream, p);
   } else {
     if (fm == 1)
       hipLaunchKernelGGL((smallm_kernel<false, 1>), grid, block, 0, stream, p);
@@ -296,8 +307,10 @@ int launch_gemm(const SmallMArgs& p0, int64_t splits, bool i8, hipStream_t strea
       hipLaunchKernelGGL((smallm_kernel<false, 2>), grid, block, 0, stream, p);
     else if (fm <= 4)
       hipLaunchKernelGGL((smallm_kernel<false, 4>), grid, block, 0, stream, p);
-    else
+    else if (fm <= 8)
       hipLaunchKernelGGL((smallm_kernel<false, 8>), grid, block, 0, stream, p);
+    else
+      hipLaunchKernelGGL((smallm_kernel<false, 16>), grid, block, 0, stream, p);
   }
   return check_launch("smallm_gemm");
 }

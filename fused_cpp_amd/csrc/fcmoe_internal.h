@@ -212,7 +212,7 @@ int gemm_launch(int epi, int bm, const GemmParams& p, int64_t max_tiles, hipStre
 // wave, weights read once, K split over about one workgroup per CU.
 // smallm_splits: the K splits for a shape (0 outside the domain);
 // smallm_workspace_bytes: the splits' int32 partial sums (0 with one split).
-constexpr int64_t kSmallMRows = 128;
+constexpr int64_t kSmallMRows = 256;
 int64_t smallm_splits(int64_t m, int64_t k, int64_t n);
 // Adds splits x [m, n] int32 partial sums in split order and applies the
 // i8gemm epilogue (write_scaled_output) into out [m, n].

@@ -182,7 +182,7 @@ int fcmoe_w8a16_forward(const fcmoe_moe_args* args, hipStream_t stream);
  * (csrc/i8gemm.cpp:318-452) behind i8gemm.dynamic_scaled_mm
  * (src/fused_cpp/i8gemm.py:88-137). Workspace: fcmoe_i8gemm_workspace_bytes(m,
  * k, n): it includes the K splits' int32 partial sums (splits x m x n; none
- * when one split covers K), so it depends on n; above 128 rows the split
+ * when one split covers K), so it depends on n; above 256 rows the split
  * count also depends on the current device's CU count, so query it with the
  * device current that the call will run on (a smaller workspace is refused
  * with FCMOE_ESPACE). */

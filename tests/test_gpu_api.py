@@ -306,9 +306,10 @@ def test_routed_shared_equals_explicit_combined_route(gpu):
 
 @pytest.mark.parametrize("T,Hd,F,activation,bias", [(1, 7168, 2048, "silu", False), (17, 200, 72, "gelu", True),
                                                     (64, 7168, 2048, "silu", True), (40, 96, 40, "silu", False),
-                                                    (97, 1000, 300, "gelu", True), (128, 7168, 2048, "silu", False)])
+                                                    (97, 1000, 300, "gelu", True), (128, 7168, 2048, "silu", False),
+                                                    (200, 7168, 2048, "silu", True), (256, 520, 130, "gelu", False)])
 def test_bf16_single_expert_small_rows_within_tolerance(gpu, oracle_lib, monkeypatch, T, Hd, F, activation, bias):
-    """One packed expert and at most 128 routes run both GEMMs on the small-M
+    """One packed expert and at most 256 routes run both GEMMs on the small-M
     kernel (split K, fp32 partial sums added in split order, the activation
     and route stores in the reduce launches): the shared MLP and a one-expert
     MoE against the fp32 reference, with biases, ragged H/F (zero-padded K),
@@ -375,7 +376,7 @@ def test_shared_mlp_equals_one_expert_moe(gpu, rows):
                                              (24, 64, 96, torch.bfloat16), (300, 7168, 512, torch.bfloat16),
                                              (520, 2048, 1000, torch.float32),
                                              (2048, 100, 8448, torch.bfloat16), (200, 640, 1001, torch.bfloat16),
-                                             (1000, 300, 998, torch.float32), (129, 3000, 700, torch.float32),
+                                             (1000, 300, 998, torch.float32), (300, 3000, 700, torch.float32),
                                              (700, 8192, 520, torch.bfloat16)])
 def test_i8gemm_bit_exact(gpu, oracle_lib, m, k, n, out_dtype):
     """tests/test_i8gemm.py:40-94 shapes (+ a DSv3-width projection; 256-row
@@ -385,7 +386,7 @@ def test_i8gemm_bit_exact(gpu, oracle_lib, m, k, n, out_dtype):
     epilogue's 16-byte row pieces and its channel-by-channel fallback for row
     strides that are not a multiple of the piece (1001, 998 channels); and K
     split over the grid where the items fill few CUs (300 rows: 7 splits; 520:
-    2; 129 rows at 47 chunks: 2 splits, the last of odd length; 700 rows: 16),
+    2; 300 rows at 47 chunks: 2 splits, the last of odd length; 700 rows: 16),
     int32 partial sums reduced in split order)."""
     from fused_cpp_amd import i8gemm
 
@@ -415,10 +416,12 @@ def test_i8gemm_bit_exact(gpu, oracle_lib, m, k, n, out_dtype):
     (64, 2048, 24576, False, torch.float32),  # many channel groups, one split
     (65, 3000, 700, True, torch.float32),     # five row fragments (the 8-fragment kernel, rows past m)
     (100, 7168, 2048, False, torch.bfloat16),
-    (128, 16384, 1024, True, torch.bfloat16),  # the largest small-M product
+    (128, 16384, 1024, True, torch.bfloat16),
+    (129, 5000, 300, False, torch.float32),   # 16 row fragments: two A loads per wave and chunk
+    (256, 16384, 7168, True, torch.bfloat16),  # the largest small-M product
 ])
 def test_i8gemm_small_m_split_k_bit_exact(gpu, oracle_lib, m, k, n, bias, out_dtype):
-    """i8gemm at <= 128 rows runs the small-M kernel (all rows per wave, K split
+    """i8gemm at <= 256 rows runs the small-M kernel (all rows per wave, K split
     over the grid with int32 partial sums): bit-exact against the oracle, with
     extreme int8 values and rows of zeros (scale 1)."""
     from fused_cpp_amd import i8gemm

@@ -377,7 +377,7 @@ def test_shared_mlp_equals_one_expert_moe(gpu, rows):
                                              (520, 2048, 1000, torch.float32),
                                              (2048, 100, 8448, torch.bfloat16), (200, 640, 1001, torch.bfloat16),
                                              (1000, 300, 998, torch.float32), (300, 3000, 700, torch.float32),
-                                             (700, 8192, 520, torch.bfloat16)])
+                                             (700, 8192, 520, torch.bfloat16), (257, 4096, 300, torch.bfloat16)])
 def test_i8gemm_bit_exact(gpu, oracle_lib, m, k, n, out_dtype):
     """tests/test_i8gemm.py:40-94 shapes (+ a DSv3-width projection; 256-row
     tiles on 256-channel workgroups with a ragged last row tile and channel
@@ -386,7 +386,8 @@ def test_i8gemm_bit_exact(gpu, oracle_lib, m, k, n, out_dtype):
     epilogue's 16-byte row pieces and its channel-by-channel fallback for row
     strides that are not a multiple of the piece (1001, 998 channels); and K
     split over the grid where the items fill few CUs (300 rows: 7 splits; 520:
-    2; 300 rows at 47 chunks: 2 splits, the last of odd length; 700 rows: 16),
+    2; 300 rows at 47 chunks: 2 splits, the last of odd length; 700 rows: 16;
+    257 rows: 4 splits, the second row tile one row),
     int32 partial sums reduced in split order)."""
     from fused_cpp_amd import i8gemm
 

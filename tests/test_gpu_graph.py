@@ -136,6 +136,33 @@ def test_router_and_i8gemm_graph_replays(gpu):
     _replay_matches_eager(fn, make, static)
 
 
+@pytest.mark.parametrize("m,k,n", [(64, 8192, 1000), (300, 4096, 700), (520, 256, 300)])
+def test_i8gemm_split_k_graph_replays(gpu, m, k, n):
+    """i8gemm and the pair with their K-split partial sums and reduce launches
+    (small-M kernel at 64 rows; the LDS tiles split 4 ways at 300 rows; no
+    split at 520 rows and K = 256) captured and replayed."""
+    from fused_cpp_amd import i8gemm
+
+    g = torch.Generator().manual_seed(m + k + n)
+    w1 = torch.randint(-127, 128, (n, k), dtype=torch.int8, generator=g)
+    w2 = torch.randint(-127, 128, (n // 2 + 3, k), dtype=torch.int8, generator=g)
+    p1 = i8gemm.prepare(w1, torch.rand(n, generator=g) * 0.01 + 0.001)
+    p2 = i8gemm.prepare(w2, torch.rand(n // 2 + 3, generator=g) * 0.01 + 0.001)
+    bias = torch.randn(n, device=gpu)
+
+    def make(r):
+        return (torch.randn(m, k, device=gpu).to(torch.bfloat16),)
+
+    static = list(make(-1))
+
+    def fn(xx):
+        out = i8gemm.dynamic_scaled_mm(xx, p1, bias=bias, out_dtype=torch.float32)
+        a, b = i8gemm.dynamic_scaled_mm_pair(xx, p1, p2)
+        return torch.cat([out.reshape(-1), a.float().reshape(-1), b.float().reshape(-1)])
+
+    _replay_matches_eager(fn, make, static)
+
+
 @pytest.mark.parametrize("min_tiles", ["32", "0", "1000000"])
 def test_w8a8_prefill_mixed_plan_graph_replays(gpu, min_tiles):
     """Skewed prefill routing where the device picks the mixed launch plan

@@ -370,10 +370,21 @@ __global__ void pad_rows_kernel(const uint16_t* x, int64_t rows, int64_t cols, i
   for (int64_t r = blockIdx.y; r < rows; r += gridDim.y) dst[r * ld + c] = c < cols ? x[r * cols + c] : (uint16_t)0;
 }
 
-__global__ void single_expert_counts_kernel(int32_t* counts, int32_t* offsets, int32_t m) {
-  counts[0] = m;
-  offsets[0] = 0;
-  offsets[1] = m;
+// The one expert of an i8gemm above the small-M kernel's rows: its count,
+// offsets and the tile list of its one class (tiles of bm rows), in one launch.
+__global__ __launch_bounds__(256) void single_expert_tiles_kernel(int32_t* counts, int32_t* offsets, int32_t* tiles,
+                                                                  int32_t* tile_count, int32_t m, int32_t bm) {
+  const int32_t nt = (m + bm - 1) / bm;
+  for (int32_t j = blockIdx.x * blockDim.x + threadIdx.x; j < nt; j += gridDim.x * blockDim.x) {
+    tiles[2 * j] = 0;
+    tiles[2 * j + 1] = j * bm;
+  }
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    counts[0] = m;
+    offsets[0] = 0;
+    offsets[1] = m;
+    tile_count[0] = nt;
+  }
 }
 
 }  // namespace
@@ -1201,9 +1212,11 @@ int i8gemm_prologue(const void* x, int x_is_f32, int64_t m, int64_t k, size_t pa
     if ((rc = quant_rows_launch(x, x_is_f32, m, k, 1, L->xq, L->kp, L->xs, stream))) return rc;
   }
   if (smallm_splits(m, k, 1) > 0) return FCMOE_OK;  // the small-M GEMM needs no tile list
-  hipLaunchKernelGGL(single_expert_counts_kernel, dim3(1), dim3(1), 0, stream, L->counts, L->offsets, (int32_t)m);
-  if ((rc = check_launch("i8gemm counts"))) return rc;
-  return tiles_from_counts_launch(L->counts, 1, L->tc, L->tiles, L->tile_count, stream);
+  if (L->tc.n != 1 || L->tc.bound[0] < ceil_div(m, L->tc.bm[0])) return fail(FCMOE_EINVAL, "i8gemm: tile classes");
+  const int64_t nt = ceil_div(m, L->tc.bm[0]);
+  hipLaunchKernelGGL(single_expert_tiles_kernel, dim3((unsigned)std::min<int64_t>(ceil_div(nt, 256), 1024)), dim3(256),
+                     0, stream, L->counts, L->offsets, L->tiles, L->tile_count, (int32_t)m, (int32_t)L->tc.bm[0]);
+  return check_launch("i8gemm tiles");
 }
 
 }  // namespace

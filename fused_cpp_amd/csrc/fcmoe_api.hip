@@ -884,7 +884,11 @@ int bf16_family_forward(const fcmoe_moe_args* a, hipStream_t stream, bool w8) {
   const int64_t kmul = w8 ? 64 : 32;
   const int64_t H = a->hidden, I = a->inter;
 
-  {
+  // The dense shared MLP on the small-M kernel (one expert, no routed slot):
+  // every token's one route is row t with weight 1, so no route build runs
+  // (the route views of fcmoe_bf16_stage_views are then not written).
+  const bool dense = smallm_mlp(a, L.routes, w8) && a->top_k == 0 && a->shared_expert_id == 0;
+  if (!dense) {
     Stage st(FCMOE_STAGE_ROUTE, stream);
     rc = route_launch(a->topk_ids, a->ids_is_i64, a->topk_weights, a->tokens, a->top_k, a->experts,
                       a->valid_experts, a->shared_expert_id, a->routed_scaling,
@@ -910,7 +914,7 @@ int bf16_family_forward(const fcmoe_moe_args* a, hipStream_t stream, bool w8) {
     q.a = xa;
     q.lda_bytes = L.hp * 2;
     q.a_rows = a->tokens;
-    q.row_map = L.rb.row_token;
+    q.row_map = dense ? nullptr : L.rb.row_token;
     q.m = L.routes;
     q.k_chunks = ceil_div(H * 2, 64);
     q.w = a->w13;
@@ -922,7 +926,7 @@ int bf16_family_forward(const fcmoe_moe_args* a, hipStream_t stream, bool w8) {
     q.activation = a->activation;
     q.partial = L.partial;
     q.partial_bytes = L.partial_bytes;
-    q.m_dev = L.rb.counts;  // expert 0's routed rows
+    q.m_dev = dense ? nullptr : L.rb.counts;  // expert 0's routed rows
     {
       Stage st(FCMOE_STAGE_W13_CLASS0 + class_slot(16), stream);
       if ((rc = smallm_bf16_launch(q, stream))) return rc;
@@ -939,10 +943,19 @@ int bf16_family_forward(const fcmoe_moe_args* a, hipStream_t stream, bool w8) {
     q.out = L.route_out;
     q.ldo = H;
     q.out_row = L.rb.sorted_routes;
+    if (kt == 1) {  // the W2 reduce also merges the token's one route
+      q.merge_out = a->out;
+      q.route_pos = dense ? nullptr : L.rb.route_pos;
+      q.route_weight = dense ? nullptr : L.rb.route_weight;
+      q.tokens = a->tokens;
+      q.skip_weighted = a->skip_weighted;
+      q.invalid_count = dense ? a->invalid_count : nullptr;
+    }
     {
       Stage st(FCMOE_STAGE_W2_CLASS0 + class_slot(16), stream);
       if ((rc = smallm_bf16_launch(q, stream))) return rc;
     }
+    if (kt == 1) return FCMOE_OK;
   } else {
   GemmParams g13{};
   g13.a = xa;

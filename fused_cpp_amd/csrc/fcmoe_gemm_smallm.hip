@@ -262,6 +262,35 @@ __global__ __launch_bounds__(256) void smallm_route_kernel(SmallMArgs p, int spl
   }
 }
 
+// BF16 W2 with one route per token: token t's route row (product row
+// route_pos[t], -1: dropped; row t with weight 1 when route_pos is null) = the
+// splits' fp32 sums in split order (+ bias[h]), stored to route_out[t] (the
+// flat route) and merged in place of the combine launch, with its arithmetic
+// for one slot: acc = fma(row, weight, 0), or the row itself with
+// skip_weighted, 0 for a dropped route; out = bf16(acc).
+__global__ __launch_bounds__(256) void smallm_route_merge_kernel(SmallMArgs p, int splits, const int32_t* route_pos,
+                                                                 const float* route_weight, int skip_weighted,
+                                                                 uint16_t* out, int64_t tokens,
+                                                                 int32_t* invalid_count) {
+  const int64_t total = tokens * p.n, plane = (int64_t)p.m * p.n;
+  const float* part = (const float*)p.partial;
+  if (invalid_count && blockIdx.x == 0 && threadIdx.x == 0) *invalid_count = 0;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t t = e / p.n, h = e % p.n;
+    const int pos = route_pos ? route_pos[t] : (int)t;
+    float acc = 0.0f;
+    if (pos >= 0) {
+      const int64_t i = (int64_t)pos * p.n + h;
+      float v = part[i];
+      for (int s = 1; s < splits; ++s) v = v + part[s * plane + i];
+      if (p.bias) v = v + p.bias[h];
+      ((float*)p.out)[t * p.ldo + h] = v;
+      acc = skip_weighted ? v : __builtin_fmaf(v, route_weight ? route_weight[t] : 1.0f, 0.0f);
+    }
+    out[e] = f32_to_bf16(acc);
+  }
+}
+
 }  // namespace
 
 namespace {
@@ -410,7 +439,11 @@ int smallm_bf16_launch(const SmallMBf16& q, hipStream_t stream) {
   p.m_dev = q.m_dev;
   int rc = launch_gemm(p, splits, false, stream);
   if (rc) return rc;
-  if (q.out_row) {
+  if (q.merge_out) {
+    hipLaunchKernelGGL(smallm_route_merge_kernel, dim3(reduce_blocks(q.tokens * n)), dim3(256), 0, stream, p,
+                       (int)splits, q.route_pos, q.route_weight, q.skip_weighted, q.merge_out, q.tokens,
+                       q.invalid_count);
+  } else if (q.out_row) {
     hipLaunchKernelGGL(smallm_route_kernel, dim3(reduce_blocks(q.m * n)), dim3(256), 0, stream, p, (int)splits);
   } else {
     hipLaunchKernelGGL(smallm_act_kernel, dim3(reduce_blocks(q.m * q.n_half)), dim3(256), 0, stream, p,

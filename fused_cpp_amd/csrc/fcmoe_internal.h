@@ -242,6 +242,18 @@ struct SmallMBf16 {
   float* partial;
   size_t partial_bytes;
   const int32_t* m_dev;    // rows actually routed (device), at most m; null: m
+  // W2 with one route per token (merge_out set): the reduce launch also does
+  // the merge of that one route, out[t] = bf16(fma(row, weight, 0)) (or the
+  // row itself with skip_weighted; 0 for a dropped route), so no combine
+  // launch follows. Product row route_pos[t] is token t's route row (null:
+  // row t, weight 1: the dense shared MLP, which runs no route build and
+  // whose merge launch also zeroes invalid_count when that is set).
+  uint16_t* merge_out;
+  const int32_t* route_pos;
+  const float* route_weight;
+  int64_t tokens;
+  int skip_weighted;
+  int32_t* invalid_count;
 };
 int64_t smallm_bf16_splits(int64_t m, int64_t k_chunks, int64_t tiles);
 int smallm_bf16_launch(const SmallMBf16& q, hipStream_t stream);

@@ -230,7 +230,9 @@ int fcmoe_w8a8_stage_views(const fcmoe_moe_args* args, const int32_t** sorted_ro
  * position, -1 for a dropped route), route_weight [R] (the combined weight
  * each route row is merged with: routed weight x routed_scaling, 1.0 for the
  * shared slot) and route_out [R, hidden] fp32 (the W2 rows the top-k merge of
- * csrc/moe/arm/sve_bf16/route_merge.cpp:47-126 reads). */
+ * csrc/moe/arm/sve_bf16/route_merge.cpp:47-126 reads). A dense shared MLP
+ * (top_k 0, one expert, shared id 0) of at most 256 tokens runs no route
+ * build: its route_pos and route_weight views are then not written. */
 int fcmoe_bf16_stage_views(const fcmoe_moe_args* args, int w8a16, const int32_t** route_pos,
                            const float** route_weight, const float** route_out);
 

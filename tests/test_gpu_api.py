@@ -314,7 +314,9 @@ def test_bf16_single_expert_small_rows_within_tolerance(gpu, oracle_lib, monkeyp
     and route stores in the reduce launches): the shared MLP and a one-expert
     MoE against the fp32 reference, with biases, ragged H/F (zero-padded K),
     and out-of-range ids with the id check off (dropped by the route build,
-    contributing nothing: the kernel sees fewer routed rows than routes)."""
+    contributing nothing: the kernel sees fewer routed rows than routes). With
+    one route per token the W2 reduce launch also merges it (no combine
+    launch), skip_weighted included."""
     from fused_cpp_amd import moe
 
     rng = np.random.default_rng(T * 31 + Hd)
@@ -348,17 +350,27 @@ def test_bf16_single_expert_small_rows_within_tolerance(gpu, oracle_lib, monkeyp
         got = out.float().cpu().numpy()
         assert not got[~keep].any()
         _close(out[torch.from_numpy(np.nonzero(keep)[0]).to(gpu)], ref)
+        # skip_weighted: the route row itself, the weights ignored
+        out = moe.fused_moe_bf16_tiled(_bf16(x, gpu), packed, tb(w), tb(ids), w13_bias=tb(b13), w2_bias=tb(b2),
+                                       activation=activation, skip_weighted=True)
+        ref = oracle_lib.bf16_moe_reference(x[keep], w13, w2, w[keep], ids[keep], w13_bias=b13, w2_bias=b2,
+                                            activation=activation, skip_weighted=True, round_intermediate=True)
+        assert not out.float().cpu().numpy()[~keep].any()
+        _close(out[torch.from_numpy(np.nonzero(keep)[0]).to(gpu)], ref)
 
 
-@pytest.mark.parametrize("rows", [1, 13, 97])
-def test_shared_mlp_equals_one_expert_moe(gpu, rows):
-    """tests/test_shared_mlp_bf16_tiled.py:37-71: exact."""
+@pytest.mark.parametrize("rows,hd,f", [(1, 192, 96), (13, 192, 96), (97, 192, 96), (50, 200, 72), (300, 192, 96)])
+def test_shared_mlp_equals_one_expert_moe(gpu, rows, hd, f):
+    """tests/test_shared_mlp_bf16_tiled.py:37-71: exact. Up to 256 rows the
+    shared MLP runs no route build (row t, weight 1) and the one-expert MoE
+    does: equal bit for bit, also with H not a multiple of 32 (padded rows);
+    300 rows take the tiled path."""
     from fused_cpp_amd import moe
 
     rng = np.random.default_rng(20260816 + rows)
-    x = rng.standard_normal((rows, 192)).astype(np.float32) * 0.01
-    w13 = rng.standard_normal((192, 192)).astype(np.float32) * 0.01
-    w2 = rng.standard_normal((192, 96)).astype(np.float32) * 0.01
+    x = rng.standard_normal((rows, hd)).astype(np.float32) * 0.01
+    w13 = rng.standard_normal((2 * f, hd)).astype(np.float32) * 0.01
+    w2 = rng.standard_normal((hd, f)).astype(np.float32) * 0.01
     packed = moe.prepare_shared_mlp_bf16_tiled_weights(_bf16(w13, gpu), _bf16(w2, gpu))
     xt = _bf16(x, gpu)
     cand = moe.shared_mlp_bf16_tiled(xt, packed, num_threads=8)

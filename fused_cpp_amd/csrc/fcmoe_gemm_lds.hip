@@ -571,9 +571,16 @@ __device__ __forceinline__ void lds_gemm_body(const GemmParams& p, int n_blocks,
     // fragment read fall on distinct banks.
     const int r = AWIDE ? g * 8 + lane / 8 : g * 16 + lane / 4;
     const int unit = AWIDE ? (lane % 8) ^ ((r >> 1) & 7) : (lane % 4) ^ ((lane >> 4) & 3);
-    const int pos = pos0 + (r < rows ? r : rows - 1);  // rows past the tile re-read the last row
+    const int pos = pos0 + (r < rows ? r : rows - 1);
     const int64_t arow = p.row_map ? (int64_t)p.row_map[pos] : (int64_t)pos;
-    voff_a[u] = (uint32_t)(arow * lda_bytes + unit * 16);
+    // Rows past the tile's rows load from past the buffer resource's range
+    // (num_records 0x7ffffff0; 0x80000040, and 0x80000000 after the fold's
+    // -64 below, stay past it, as does either plus a K offset < 2^31): the
+    // load still counts in vmcnt (every wave's wait counts stay uniform) but
+    // moves no data, and the stage gets zeros there, which no epilogue
+    // stores. (They used to re-read the last row: L2 hits, but intake of a CU
+    // whose vector-memory path the stage loads share.)
+    voff_a[u] = r < rows ? (uint32_t)(arow * lda_bytes + unit * 16) : 0x80000040u;
     lds_a[u] = g * 1024;
   }
   // B: a load's tile is the same for the whole wave, so its offset goes in

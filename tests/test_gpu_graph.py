@@ -115,6 +115,40 @@ def test_bf16_and_w8a16_forward_graph_replays(gpu):
         _replay_matches_eager(lambda xx, ww, ii: op(xx, weights, ww, ii), make, static)
 
 
+@pytest.mark.parametrize("T", [1, 64, 200])
+def test_bf16_shared_mlp_and_one_expert_graph_replays(gpu, T):
+    """The small-M BF16 forward under capture: the dense shared MLP (no route
+    build; its merge launch zeroes the invalid-id count) and a one-expert MoE
+    (route build, the W2 reduce merging each token's route)."""
+    from fused_cpp_amd import moe
+
+    rng = np.random.default_rng(T)
+    Hd, F = 1024, 512
+    tb = lambda b: torch.from_numpy(b.view(np.int16)).to(gpu).view(torch.bfloat16)  # noqa: E731
+    w13 = H.bf16_bits((rng.standard_normal((2 * F, Hd)) * 0.02).astype(np.float32))
+    w2 = H.bf16_bits((rng.standard_normal((Hd, F)) * 0.02).astype(np.float32))
+    sm = moe.prepare_shared_mlp_bf16_tiled_weights(tb(w13), tb(w2))
+    ones = torch.ones((T, 1), device=gpu)
+    zeros = torch.zeros((T, 1), dtype=torch.int32, device=gpu)
+
+    def make(r):
+        return (tb(H.bf16_bits(rng.standard_normal((T, Hd)).astype(np.float32))),
+                torch.from_numpy(rng.random((T, 1)).astype(np.float32) + 0.5).to(gpu))
+
+    static = list(make(-1))
+
+    def fn(xx, ww):
+        a = moe.shared_mlp_bf16_tiled(xx, sm)
+        b = moe.fused_moe_bf16_tiled(xx, sm, ww, zeros)
+        c = moe.fused_moe_bf16_tiled(xx, sm, ones, zeros)
+        return torch.cat([a.float().reshape(-1), b.float().reshape(-1), c.float().reshape(-1)])
+
+    _replay_matches_eager(fn, make, static)
+    out = fn(*static)
+    n = T * Hd
+    assert torch.equal(out[:n], out[2 * n:])  # shared MLP == one-expert MoE with weight 1
+
+
 def test_router_and_i8gemm_graph_replays(gpu):
     from fused_cpp_amd import i8gemm, router
 

@@ -11,6 +11,9 @@
 #include <torch/extension.h>
 
 #include <algorithm>
+#include <climits>
+#include <thread>
+#include <unordered_map>
 #include <string>
 #include <tuple>
 
@@ -273,11 +276,84 @@ at::Tensor output_for(const at::Tensor& input, c10::optional<at::Tensor> out) {
   return o;
 }
 
-void maybe_check_invalid(const at::Tensor& invalid, bool validate) {
-  if (!validate) return;
-  const int32_t bad = invalid.item<int32_t>();
-  TORCH_CHECK(bad == 0, "topk_ids out of range: ", bad, " id(s) outside the valid expert range");
+// The synchronous invalid-id error of the reference (kernels.cpp:586 raises
+// before computing). The route launch (the first of a forward) writes the
+// count of ids outside the valid range; the host must see it before the call
+// returns. Reading it from device memory (`.item()`) would wait for the whole
+// forward, so the host could not enqueue the next call while this one runs.
+// Instead the count goes to a per-thread, per-device slot of coherent pinned
+// host memory, which the host polls: the call returns as soon as the route
+// launch has finished, the rest of the forward still running on the stream.
+// Under graph capture (nothing runs) and for empty batches (no route launch)
+// the device tensor is used and read as before.
+constexpr int32_t kPendingCount = INT32_MIN;
+
+int32_t* pinned_count_slot() {
+  thread_local std::unordered_map<int, int32_t*> slots;  // held until the thread ends (one 64-byte block each)
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+  int32_t*& slot = slots[dev];
+  if (!slot) {
+    void* p = nullptr;
+    if (hipHostMalloc(&p, 64, hipHostMallocCoherent | hipHostMallocPortable) != hipSuccess) return nullptr;
+    slot = (int32_t*)p;
+  }
+  return slot;
 }
+
+struct InvalidCheck {
+  bool validate = false;
+  int32_t* host = nullptr;  // pinned slot being polled (else: device tensor)
+  at::Tensor dev;
+
+  // Sets args->invalid_count for one forward on the current stream.
+  InvalidCheck(bool v, const at::Tensor& input, fcmoe_moe_args* a) : validate(v) {
+    if (!validate) {
+      a->invalid_count = nullptr;
+      return;
+    }
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    const bool capturing = hipStreamIsCapturing(current_stream(), &cs) == hipSuccess && cs != hipStreamCaptureStatusNone;
+    if (!capturing && input.size(0) > 0) host = pinned_count_slot();
+    if (host) {
+      __atomic_store_n(host, kPendingCount, __ATOMIC_RELEASE);
+      void* dp = nullptr;
+      TORCH_CHECK(hipHostGetDevicePointer(&dp, host, 0) == hipSuccess, "pinned invalid-id count not mapped");
+      a->invalid_count = (int32_t*)dp;
+    } else {
+      dev = at::zeros({1}, input.options().dtype(at::kInt));
+      a->invalid_count = dev.data_ptr<int32_t>();
+    }
+  }
+
+  // After the forward was enqueued: raise if any id was out of range.
+  void finish() {
+    if (!validate) return;
+    int32_t bad = 0;
+    if (host) {
+      pybind11::gil_scoped_release release;
+      hipStream_t s = current_stream();
+      for (int i = 0;; ++i) {
+        bad = __atomic_load_n(host, __ATOMIC_ACQUIRE);
+        if (bad != kPendingCount) break;
+        if (i % 64 == 63) {
+          const hipError_t q = hipStreamQuery(s);
+          if (q == hipSuccess) {  // the stream drained: the count is final (no route launch ran: no id checked)
+            bad = __atomic_load_n(host, __ATOMIC_ACQUIRE);
+            if (bad == kPendingCount) bad = 0;
+            break;
+          }
+          TORCH_CHECK(q == hipErrorNotReady, "fused MoE: stream error while waiting for the id check: ",
+                      hipGetErrorString(q));
+          std::this_thread::yield();
+        }
+      }
+    } else {
+      bad = dev.item<int32_t>();
+    }
+    TORCH_CHECK(bad == 0, "topk_ids out of range: ", bad, " id(s) outside the valid expert range");
+  }
+};
 
 // W8A8 forward (csrc/moe/arm/i8mm_w8a8/kernels.cpp:463-694).
 at::Tensor w8a8_forward(at::Tensor input, at::Tensor w13, int64_t w13_k, int64_t w13_n, at::Tensor s13,
@@ -294,7 +370,6 @@ at::Tensor w8a8_forward(at::Tensor input, at::Tensor w13, int64_t w13_k, int64_t
                   w2.size(1) == fcmoe_packed_expert_bytes(1, w2_n, w2_k, 1),
               "W8A8 packed weight strides are invalid");
   at::Tensor output = output_for(input, out);
-  at::Tensor invalid = at::empty({1}, input.options().dtype(at::kInt));  // written by the route kernel
   fcmoe_moe_args a = base_args(input, topk_weights, topk_ids, e, shared_id, routed_scale, global_num_experts, output);
   a.inter = w2_k;
   a.w13 = w13.data_ptr();
@@ -302,7 +377,7 @@ at::Tensor w8a8_forward(at::Tensor input, at::Tensor w13, int64_t w13_k, int64_t
   a.w13_scale = s13.data_ptr<float>();
   a.w2_scale = s2.data_ptr<float>();
   a.activation = FCMOE_ACT_SILU_CLAMP10;
-  a.invalid_count = invalid.data_ptr<int32_t>();
+  InvalidCheck invalid(validate_ids, input, &a);
   at::Tensor ws = workspace(fcmoe_w8a8_workspace_bytes(&a), input);
   a.workspace = ws.data_ptr();
   a.workspace_bytes = ws.numel();
@@ -310,7 +385,7 @@ at::Tensor w8a8_forward(at::Tensor input, at::Tensor w13, int64_t w13_k, int64_t
     pybind11::gil_scoped_release release;
     check_rc(fcmoe_w8a8_forward(&a, current_stream()), "fused_moe_w8a8");
   }
-  maybe_check_invalid(invalid, validate_ids);
+  invalid.finish();
   return output;
 }
 
@@ -373,7 +448,6 @@ at::Tensor bf16_forward(at::Tensor input, at::Tensor w13, int64_t w13_k, int64_t
   at::Tensor output = output_for(input, out);
   at::Tensor b13 = bias_f32(w13_bias, e, w13_n, input);
   at::Tensor b2 = bias_f32(w2_bias, e, w2_n, input);
-  at::Tensor invalid = at::empty({1}, input.options().dtype(at::kInt));  // written by the route kernel
   fcmoe_moe_args a = base_args(input, topk_weights, topk_ids, e, shared_id, routed_scale, global_num_experts, output);
   a.inter = w2_k;
   a.w13 = w13.data_ptr();
@@ -382,7 +456,7 @@ at::Tensor bf16_forward(at::Tensor input, at::Tensor w13, int64_t w13_k, int64_t
   a.w2_bias = b2.defined() ? b2.data_ptr<float>() : nullptr;
   a.activation = activation_code(activation);
   a.skip_weighted = skip_weighted ? 1 : 0;
-  a.invalid_count = invalid.data_ptr<int32_t>();
+  InvalidCheck invalid(validate_ids, input, &a);
   at::Tensor ws = workspace(fcmoe_bf16_workspace_bytes(&a), input);
   a.workspace = ws.data_ptr();
   a.workspace_bytes = ws.numel();
@@ -390,7 +464,7 @@ at::Tensor bf16_forward(at::Tensor input, at::Tensor w13, int64_t w13_k, int64_t
     pybind11::gil_scoped_release release;
     check_rc(fcmoe_bf16_forward(&a, current_stream()), "fused_moe_bf16");
   }
-  maybe_check_invalid(invalid, validate_ids);
+  invalid.finish();
   return output;
 }
 
@@ -411,7 +485,6 @@ at::Tensor w8a16_forward(at::Tensor input, at::Tensor w13, int64_t w13_k, int64_
                   w2.size(1) == fcmoe_packed_expert_bytes(1, w2_n, w2_k, 1),
               "W8A16 packed weight strides are invalid");
   at::Tensor output = output_for(input, out);
-  at::Tensor invalid = at::empty({1}, input.options().dtype(at::kInt));  // written by the route kernel
   fcmoe_moe_args a = base_args(input, topk_weights, topk_ids, e, shared_id, routed_scale, global_num_experts, output);
   a.inter = w2_k;
   a.w13 = w13.data_ptr();
@@ -420,7 +493,7 @@ at::Tensor w8a16_forward(at::Tensor input, at::Tensor w13, int64_t w13_k, int64_
   a.w2_scale = s2.data_ptr<float>();
   a.activation = activation_code(activation);
   a.skip_weighted = skip_weighted ? 1 : 0;
-  a.invalid_count = invalid.data_ptr<int32_t>();
+  InvalidCheck invalid(validate_ids, input, &a);
   at::Tensor ws = workspace(fcmoe_w8a16_workspace_bytes(&a), input);
   a.workspace = ws.data_ptr();
   a.workspace_bytes = ws.numel();
@@ -428,7 +501,7 @@ at::Tensor w8a16_forward(at::Tensor input, at::Tensor w13, int64_t w13_k, int64_
     pybind11::gil_scoped_release release;
     check_rc(fcmoe_w8a16_forward(&a, current_stream()), "fused_moe_w8a16");
   }
-  maybe_check_invalid(invalid, validate_ids);
+  invalid.finish();
   return output;
 }
 

@@ -130,6 +130,34 @@ def test_w8a8_invalid_ids_raise(gpu):
         moe.fused_moe_w8a8_tiled(xt, plain, torch.from_numpy(w).to(gpu), bad)
 
 
+@pytest.mark.parametrize("T", [1, 40, 600])
+def test_w8a8_id_check_alternating_calls(gpu, monkeypatch, T):
+    """The id check (a pinned host count the host polls while the forward
+    runs) across calls: valid, invalid, valid again, behind queued GPU work;
+    one token (decode head), the small route and the 3-kernel route (1200
+    routes). Results with the check equal those without it, bit for bit."""
+    from fused_cpp_amd import moe
+
+    case = H.w8a8_case(11 + T, T, 256, 128, 5, 2)
+    x, ids, w, *_ = case
+    plain = _w8a8_weights(case, False, gpu)
+    xt = torch.from_numpy(x.view(np.int16)).to(gpu).view(torch.bfloat16)
+    wt = torch.from_numpy(w).to(gpu)
+    good = torch.from_numpy(ids).to(gpu)
+    bad = good.clone()
+    bad[T - 1, 1] = 5
+    monkeypatch.setenv("FUSED_CPP_AMD_VALIDATE_IDS", "0")
+    ref = _bits(moe.fused_moe_w8a8_tiled(xt, plain, wt, good))
+    monkeypatch.setenv("FUSED_CPP_AMD_VALIDATE_IDS", "1")
+    big = torch.randn(4096, 4096, device=gpu)
+    for rep in range(3):
+        _ = big @ big  # queued ahead of the forward: the host waits for the route launch, not the stream
+        assert np.array_equal(_bits(moe.fused_moe_w8a8_tiled(xt, plain, wt, good)), ref), rep
+        with pytest.raises(RuntimeError, match="1 id\\(s\\) outside"):
+            moe.fused_moe_w8a8_tiled(xt, plain, wt, bad)
+    torch.cuda.synchronize()
+
+
 def test_w8a8_empty_input(gpu):
     from fused_cpp_amd import moe
 

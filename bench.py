@@ -978,7 +978,8 @@ def probe_lib():
     P, I, I64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64
     for name, args in {"fcmoe_probe_stream": [P, I64, I, I, I, I, P, P], "fcmoe_probe_mfma": [I, I, I, I, P, P],
                        "fcmoe_probe_mix": [P, I64, I, I, I, I, P, P], "fcmoe_probe_fence": [P, I64, I, I, I, P, P, P],
-                       "fcmoe_probe_ring": [P, I64, P, I64, I, I, I, I, P, P]}.items():
+                       "fcmoe_probe_ring": [P, I64, P, I64, I, I, I, I, P, P],
+                       "fcmoe_probe_loop_dma": [P, I64, I, I, P, P]}.items():
         fn = getattr(lib, name)
         fn.restype, fn.argtypes = I, args
     return lib
@@ -1065,6 +1066,14 @@ def probes() -> int:
             out["ring"].append({"workgroups": wgs, "lookahead": la, "a_kib_per_chunk": 8 * na, "barrier": bool(bar),
                                 "us": round(ms * 1e3, 1), "weights_TBps": round(wb / ms / 1e9, 3),
                                 "GBps_per_cu": round((wb + ab) / ms / 1e6 / wgs, 1)})
+    out["loop_dma"] = []
+    iters = 4000
+    for mode in (0, 1, 2, 3, 7):
+        ms = best_ms(lambda: L.fcmoe_probe_loop_dma(src.data_ptr(), 1 << 20, mode, iters, sink.data_ptr(), stream))
+        ops = 256 * 8 * iters * 32 * 32768
+        out["loop_dma"].append({"barrier": bool(mode & 1), "lds_dma_kib_per_cu": 32 if mode & 2 else 0,
+                                "wait_before_barrier": bool(mode & 4), "us": round(ms * 1e3, 1),
+                                "POPS": round(ops / ms / 1e12, 3)})
     print(json.dumps({"probes": out}))
     return 0
 

@@ -49,7 +49,15 @@ extern "C" {
  *   arows_bytes < 16 MiB is refused. The LDS ring has 2 stages whatever the
  *   lookahead (6 stages of this mix would need 288 KiB): with lookahead 4 or
  *   6 chunks still in flight land on stages that later chunks also target.
- *   Nothing reads the ring, so this times the loads, not a usable ring. */
+ *   Nothing reads the ring, so this times the loads, not a usable ring.
+ * _loop_dma: the prefill GEMM's K loop without HBM: 256 workgroups of 8
+ *   waves, each wave a 128 x 64 tile (per iteration 6 LDS fragment reads
+ *   ahead of the MFMAs, then one A read per row of 4 MFMAs, as the 256-row
+ *   persistent tile). mode bit 0: one workgroup barrier per iteration; bit 1:
+ *   each wave issues 4 buffer_load ... lds of 1 KiB per iteration (32 KiB per
+ *   CU, from a 64 KiB window of src per XCD, i.e. L2 hits) into LDS the loop
+ *   does not read; bit 2: before the barrier, wait for the previous
+ *   iteration's loads. src_bytes >= 1 MiB. */
 int fcmoe_probe_stream(const void* src, int64_t src_bytes, int workgroups, int waves, int mode, int lds_pad_bytes,
                        int* sink, hipStream_t stream);
 int fcmoe_probe_mfma(int tile, int waves, int workgroups, int iters, int* sink, hipStream_t stream);
@@ -59,6 +67,7 @@ int fcmoe_probe_fence(const void* src, int64_t src_bytes, int workgroups, int wa
                       void* rows, hipStream_t stream);
 int fcmoe_probe_ring(const void* src, int64_t src_bytes, const void* arows, int64_t arows_bytes, int workgroups,
                      int lookahead, int a_loads, int barrier, int* sink, hipStream_t stream);
+int fcmoe_probe_loop_dma(const void* src, int64_t src_bytes, int mode, int iters, int* sink, hipStream_t stream);
 
 #ifdef __cplusplus
 }

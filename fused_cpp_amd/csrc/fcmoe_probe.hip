@@ -228,6 +228,65 @@ int launch_mfma(int workgroups, int iters, int* sink, hipStream_t stream) {
   return check_launch("probe_mfma");
 }
 
+
+// The 256-row persistent tile's K loop (128 x 64 per wave, 8 waves) on LDS
+// data, with optional per-iteration barrier and LDS-DMA traffic (see
+// fcmoe_probe_loop_dma).
+__global__ __launch_bounds__(512) void probe_loop_dma_kernel(const uint8_t* src, int mode, int iters, int* sink) {
+#if __HIP_DEVICE_COMPILE__
+  constexpr int FM = 8, FN = 4;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[96 * 1024 + 64 * 1024];
+  const int lane = threadIdx.x % kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  for (int i = threadIdx.x; i < 96 * 1024 / 16; i += blockDim.x) ((v4i*)smem)[i] = v4i{i, 1, 2, 3};
+  __syncthreads();
+  v4i acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = v4i{0, 0, 0, 0};
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)src, (short)0, 1 << 20, 0x00020000);
+  const int base = __builtin_amdgcn_readfirstlane((int)(blockIdx.x % 8) * 65536);
+  const uint8_t* sa = smem + (wave / 4) * 32768 + lane * 16;
+  const uint8_t* sb = smem + 65536 + (wave % 4) * FN * 1024 + lane * 16;
+  for (int it = 0; it < iters; ++it) {
+    if (mode & 4) __builtin_amdgcn_s_waitcnt((4 & 15) | (7 << 4) | (15 << 8));  // vmcnt(4): the previous iteration's loads
+    if (mode & 1) __builtin_amdgcn_s_barrier();
+    if (mode & 2) {
+      const int off = __builtin_amdgcn_readfirstlane(base + ((it * 8 + wave) & 15) * 4096);
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rs, (probe_lds_ptr)(smem + 96 * 1024 + (it & 1) * 32768 + (wave * 4 + u) * 1024), 16, lane * 16,
+            off + u * 1024, 0, 0);
+    }
+    const int ro = (it & 3) * 8192;
+    v4i bf[FN], af[3];
+    af[0] = *(const v4i*)(sa + ro);
+#pragma unroll
+    for (int j = 0; j < FN; ++j) bf[j] = *(const v4i*)(sb + j * 1024);
+    af[1] = *(const v4i*)(sa + ro + 1024);
+    __builtin_amdgcn_sched_group_barrier(0x100, FN + 2, 0);
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      if (i + 2 < FM) af[(i + 2) % 3] = *(const v4i*)(sa + ro + (i + 2) * 1024);
+#pragma unroll
+      for (int j = 0; j < FN; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i % 3], bf[j], acc[i][j], 0, 0, 0);
+      if (i + 2 < FM) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, FN, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  __builtin_amdgcn_s_waitcnt((0 & 15) | (7 << 4) | (15 << 8));
+  v4i t = {0, 0, 0, 0};
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) t += acc[i][j];
+  if (t[0] == 0x7fffabcd) sink[threadIdx.x] = t[1] + smem[96 * 1024 + lane];
+#endif
+}
+
 }  // namespace
 }  // namespace fcmoe
 
@@ -313,4 +372,13 @@ extern "C" int fcmoe_probe_ring(const void* src, int64_t src_bytes, const void* 
     default: return fail(FCMOE_EINVAL, "probe_ring: unsupported lookahead / A loads / barrier");
   }
   return check_launch("probe_ring");
+}
+
+extern "C" int fcmoe_probe_loop_dma(const void* src, int64_t src_bytes, int mode, int iters, int* sink,
+                                    hipStream_t stream) {
+  if (!src || !sink || src_bytes < (1 << 20) || iters <= 0 || mode < 0 || mode > 7)
+    return fcmoe::fail(FCMOE_EINVAL, "probe_loop_dma: bad arguments");
+  hipLaunchKernelGGL(fcmoe::probe_loop_dma_kernel, dim3(256), dim3(512), 0, stream, (const uint8_t*)src, mode, iters,
+                     sink);
+  return fcmoe::check_launch("probe_loop_dma");
 }

@@ -64,6 +64,9 @@ def lib() -> ctypes.CDLL:
                                        _P, _P, _P, _P, _P, _P]
         l.orc_w8a8_expert_range.restype = _I64
         l.orc_w8a8_expert_range.argtypes = [_P, _P, _P, _I64, _I64, _I64, _P, _P, _P, _P, _I64, _I64, _P]
+        l.orc_w8a8_w13_rows.argtypes = [_P, _I64, _I64, _P, _P, _P, _P, _P]
+        l.orc_w8a8_w2_rows.argtypes = [_P, _I64, _I64, _P, _P, _P]
+        l.orc_w8a8_merge.argtypes = [_P, _P, _I64, _I64, _I64, _P]
         l.orc_gemm_i8_rows.argtypes = [_P, _I64, _P, _I64, _P, _I64, _I64, _P]
         l.orc_i8gemm.argtypes = [_P, _I, _I64, _I64, _P, _P, _I64, _P, _I, _P]
         l.orc_bf16_activation.argtypes = [_P, _I64, _I64, _I, _P]
@@ -210,6 +213,54 @@ def w8a8_forward(x_bits, ids, topk_w, w13, s13, w2, s2, *, shared_id: int = -1, 
         _ptr(w2), _ptr(s2), shared_id, routed_scale, _ptr(out), _ptr(d.get("acc13")), _ptr(d.get("y")),
         _ptr(d.get("q2")), _ptr(d.get("s2row")), _ptr(d.get("acc2")), _ptr(d.get("route_out")))
     return (out, d) if dumps else out
+
+
+def w8a8_w13_rows(acc13, xs, s13e, want_y: bool = False):
+    """The W8A8 stages after W13 for rows of one expert (kernels.cpp:230-246,
+    211-228): acc13 [rows, 2I] int32, xs [rows] token scales, s13e [2I] ->
+    (q2 [rows, I] int8, s2row [rows] fp32[, y bf16 bits])."""
+    acc13 = _c(acc13, np.int32)
+    rows, two_i = acc13.shape
+    inter = two_i // 2
+    q2 = np.empty((rows, inter), np.int8)
+    s2row = np.empty(rows, np.float32)
+    y = np.empty((rows, inter), np.uint16) if want_y else None
+    lib().orc_w8a8_w13_rows(_ptr(acc13), rows, inter, _ptr(_c(xs, np.float32)), _ptr(_c(s13e, np.float32)), _ptr(y),
+                            _ptr(q2), _ptr(s2row))
+    return (q2, s2row, y) if want_y else (q2, s2row)
+
+
+def w8a8_w2_rows(acc2, s2row, s2e, out=None):
+    """store_w2 (kernels.cpp:248-257) for rows of one expert: acc2 [rows, H] int32 -> fp32 route rows."""
+    acc2 = _c(acc2, np.int32)
+    rows, hidden = acc2.shape
+    if out is None:
+        out = np.empty((rows, hidden), np.float32)
+    assert out.dtype == np.float32 and out.flags.c_contiguous and out.shape == (rows, hidden)
+    lib().orc_w8a8_w2_rows(_ptr(acc2), rows, hidden, _ptr(_c(s2row, np.float32)), _ptr(_c(s2e, np.float32)),
+                           _ptr(out))
+    return out
+
+
+def w8a8_route_weights(topk_w, shared: bool, routed_scale: float) -> np.ndarray:
+    """Per flat route merge weights as orc_w8a8_forward forms them (bf16_tiled.py:1007-1013):
+    routed weights x routed_scale with a shared slot of weight 1, else the weights as given."""
+    topk_w = _c(topk_w, np.float32)
+    if not shared:
+        return topk_w.reshape(-1).copy()
+    t, k = topk_w.shape
+    rw = np.ones((t, k + 1), np.float32)
+    rw[:, :k] = topk_w * np.float32(routed_scale)
+    return rw.reshape(-1)
+
+
+def w8a8_merge(route_out, rw, tokens: int, kt: int) -> np.ndarray:
+    """Ordered-FMA merge (kernels.cpp:674-688): route_out [T*kt, H] fp32 by flat route -> bf16 bits [T, H]."""
+    route_out = _c(route_out, np.float32)
+    hidden = route_out.shape[1]
+    out = np.empty((tokens, hidden), np.uint16)
+    lib().orc_w8a8_merge(_ptr(route_out), _ptr(_c(rw, np.float32)), tokens, kt, hidden, _ptr(out))
+    return out
 
 
 def w8a8_expert_range(x_bits, sorted_routes, offsets, kt, w13, s13, w2, s2, e_begin, e_end, route_out):

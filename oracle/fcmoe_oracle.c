@@ -201,6 +201,67 @@ static inline uint16_t w13_value(int32_t acc_g, int32_t acc_u, float xs, float s
   return orc_f32_to_bf16(v);
 }
 
+/* One route row after its W13 GEMM: w13_epilogue (kernels.cpp:230-246) over
+ * the I gate/up pairs, then quantize_bf16_row of the bf16 row (:211-228,
+ * :650-657). */
+static void w13_row(const int32_t* a13, int I, float xs, const float* se, uint16_t* y, int8_t* q2, float* s2r) {
+  for (int f = 0; f < I; ++f) y[f] = w13_value(a13[f], a13[I + f], xs, se[f], se[I + f], 10.0f);
+  orc_quant_row_away(y, I, q2, s2r);
+}
+
+/* store_w2 (kernels.cpp:248-257): route row = (float)acc * (s_row * s_w). */
+static inline float w2_value(int32_t acc, float s2r, float sw) { return (float)acc * (s2r * sw); }
+
+/* Merge (kernels.cpp:674-688): per token and channel acc = fma(route, w, acc)
+ * over the kt slots in slot order, then bf16. */
+static void merge_rows(const float* route_out, const float* rw, int64_t tokens, int64_t kt, int64_t hidden,
+                       uint16_t* out) {
+  int64_t t;
+#pragma omp parallel for schedule(static)
+  for (t = 0; t < tokens; ++t) {
+    for (int64_t h = 0; h < hidden; ++h) {
+      float acc = 0.0f;
+      for (int64_t s = 0; s < kt; ++s) {
+        const int64_t r = t * kt + s;
+        acc = fmaf(route_out[r * hidden + h], rw[r], acc);
+      }
+      out[t * hidden + h] = orc_f32_to_bf16(acc);
+    }
+  }
+}
+
+/* The forward's stages after each GEMM, for checking a whole layer whose
+ * int32 accumulators come from an exact integer GEMM elsewhere (the same
+ * arithmetic as orc_w8a8_forward, which calls the same helpers):
+ * orc_w8a8_w13_rows: rows route rows of one expert, acc13 [rows, 2I], xs [rows]
+ *   (the rows' token scales), s13e [2I] -> q2 [rows, I], s2row [rows]
+ *   (y [rows, I] bf16 bits when not NULL);
+ * orc_w8a8_w2_rows: acc2 [rows, H], s2row [rows], s2e [H] -> route_out [rows, H];
+ * orc_w8a8_merge: route_out [T * kt, H] by flat route, rw [T * kt] -> out [T, H]. */
+void orc_w8a8_w13_rows(const int32_t* acc13, int64_t rows, int64_t inter, const float* xs, const float* s13e,
+                       uint16_t* y_out, int8_t* q2, float* s2row) {
+  int64_t j;
+#pragma omp parallel for schedule(static)
+  for (j = 0; j < rows; ++j) {
+    uint16_t* y = y_out ? y_out + j * inter : (uint16_t*)malloc((size_t)inter * sizeof(uint16_t));
+    w13_row(acc13 + j * 2 * inter, (int)inter, xs[j], s13e, y, q2 + j * inter, s2row + j);
+    if (!y_out) free(y);
+  }
+}
+
+void orc_w8a8_w2_rows(const int32_t* acc2, int64_t rows, int64_t hidden, const float* s2row, const float* s2e,
+                      float* route_out) {
+  int64_t j;
+#pragma omp parallel for schedule(static)
+  for (j = 0; j < rows; ++j)
+    for (int64_t h = 0; h < hidden; ++h) route_out[j * hidden + h] = w2_value(acc2[j * hidden + h], s2row[j], s2e[h]);
+}
+
+void orc_w8a8_merge(const float* route_out, const float* rw, int64_t tokens, int64_t kt, int64_t hidden,
+                    uint16_t* out) {
+  merge_rows(route_out, rw, tokens, kt, hidden, out);
+}
+
 /* Full W8A8 fused-MoE forward, csrc/moe/arm/i8mm_w8a8/kernels.cpp:463-694:
  * per route row: quantize_bf16_row(x[token]) -> W13 int32 GEMM -> w13_epilogue
  * (clamped SwiGLU, bf16) -> quantize_bf16_row -> W2 int32 GEMM -> store_w2
@@ -240,17 +301,15 @@ void orc_w8a8_forward(const uint16_t* x, const int64_t* ids, const float* topk_w
       if (e < 0 || e >= experts) continue;
       const int8_t* we = w13 + (size_t)e * 2 * I * H;
       for (int n = 0; n < 2 * I; ++n) a13[n] = dot_i8(xq, we + (size_t)n * H, H);
-      const float* se = s13 + (size_t)e * 2 * I;
-      for (int f = 0; f < I; ++f) y[f] = w13_value(a13[f], a13[I + f], xs, se[f], se[I + f], 10.0f);
       float s2r;
-      orc_quant_row_away(y, I, q2, &s2r);
+      w13_row(a13, I, xs, s13 + (size_t)e * 2 * I, y, q2, &s2r);
       const int8_t* w2e = w2 + (size_t)e * H * I;
       const float* s2e = s2 + (size_t)e * H;
       float* ro = route_out + r * hidden;
       for (int h = 0; h < H; ++h) {
         int32_t acc = dot_i8(q2, w2e + (size_t)h * I, I);
         if (d_acc2) d_acc2[r * hidden + h] = acc;
-        ro[h] = (float)acc * (s2r * s2e[h]);
+        ro[h] = w2_value(acc, s2r, s2e[h]);
       }
       if (d_acc13) memcpy(d_acc13 + r * 2 * I, a13, (size_t)(2 * I) * sizeof(int32_t));
       if (d_y) memcpy(d_y + r * I, y, (size_t)I * sizeof(uint16_t));
@@ -260,16 +319,7 @@ void orc_w8a8_forward(const uint16_t* x, const int64_t* ids, const float* topk_w
     free(xq); free(a13); free(y); free(q2);
   }
   /* Merge: kernels.cpp:674-688 -- acc = fma(route, w, acc) in slot order. */
-  for (t = 0; t < tokens; ++t) {
-    for (int h = 0; h < H; ++h) {
-      float acc = 0.0f;
-      for (int64_t s = 0; s < kt; ++s) {
-        const int64_t r = t * kt + s;
-        acc = fmaf(route_out[r * hidden + h], rw[r], acc);
-      }
-      out[t * hidden + h] = orc_f32_to_bf16(acc);
-    }
-  }
+  merge_rows(route_out, rw, tokens, kt, hidden, out);
   if (d_route) memcpy(d_route, route_out, (size_t)(routes * hidden) * sizeof(float));
   free(route_out);
   free(rw);
@@ -302,13 +352,11 @@ int64_t orc_w8a8_expert_range(const uint16_t* x, const int64_t* sorted_routes, c
       orc_quant_row_away(x + t * hidden, H, xq, &xs);
       const int8_t* we = w13 + (size_t)e * 2 * I * H;
       for (int n = 0; n < 2 * I; ++n) a13[n] = dot_i8(xq, we + (size_t)n * H, H);
-      const float* se = s13 + (size_t)e * 2 * I;
-      for (int f = 0; f < I; ++f) y[f] = w13_value(a13[f], a13[I + f], xs, se[f], se[I + f], 10.0f);
-      orc_quant_row_away(y, I, q2, &s2r);
+      w13_row(a13, I, xs, s13 + (size_t)e * 2 * I, y, q2, &s2r);
       const int8_t* w2e = w2 + (size_t)e * H * I;
       const float* s2e = s2 + (size_t)e * H;
       float* ro = route_out + r * hidden;
-      for (int h = 0; h < H; ++h) ro[h] = (float)dot_i8(q2, w2e + (size_t)h * I, I) * (s2r * s2e[h]);
+      for (int h = 0; h < H; ++h) ro[h] = w2_value(dot_i8(q2, w2e + (size_t)h * I, I), s2r, s2e[h]);
       free(xq); free(a13); free(y); free(q2);
     }
   }

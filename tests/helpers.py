@@ -305,3 +305,41 @@ def gpu_bf16_forward(x, ids, w, w13, w2, device, *, shared_id: int = -1, scale: 
 
     return (out.cpu().numpy().view(np.uint16), grab(views[0], R, torch.int32), grab(views[1], R, torch.float32),
             grab(views[2], R * hidden, torch.float32).reshape(R, hidden))
+
+
+def w8a8_layer_staged(x_bits, ids, topk_w, experts: int, shared_id: int, routed_scale: float, gemm13, gemm2,
+                      s13_of, s2_of):
+    """The oracle's W8A8 layer (orc_w8a8_forward) with its two GEMMs supplied
+    by the caller: every other step (token quantisation, W13 epilogue and
+    requant, store_w2, ordered merge) is the oracle's own C code. gemm13(e,
+    a [rows, H] int8) and gemm2(e, q2 [rows, I] int8) must return the exact
+    int32 accumulators [rows, N] of expert e (any exact integer GEMM gives
+    the same values); s13_of(e) / s2_of(e) return its channel scales. Routes
+    with ids outside [0, experts) contribute nothing, as in the oracle."""
+    import oracle
+
+    T, k = ids.shape
+    shared = shared_id >= 0
+    kt = k + (1 if shared else 0)
+    xq, xs = oracle.quant_rows_away(x_bits)
+    route_expert = np.concatenate([ids, np.full((T, 1), shared_id)], 1) if shared else ids
+    route_expert = route_expert.reshape(-1)
+    hidden = x_bits.shape[1]
+    route_out = np.zeros((T * kt, hidden), np.float32)
+    valid = (route_expert >= 0) & (route_expert < experts)
+    order = np.argsort(np.where(valid, route_expert, experts), kind="stable")
+    bounds = np.searchsorted(route_expert[order], np.arange(experts + 1)) if valid.any() else None
+    for e in range(experts):
+        if bounds is None:
+            break
+        r = order[bounds[e]:bounds[e + 1]]
+        r = r[route_expert[r] == e]
+        if r.size == 0:
+            continue
+        tok = r // kt
+        acc13 = gemm13(e, xq[tok])
+        q2, s2row = oracle.w8a8_w13_rows(acc13, xs[tok], s13_of(e))
+        acc2 = gemm2(e, q2)
+        route_out[r] = oracle.w8a8_w2_rows(acc2, s2row, s2_of(e))
+    rw = oracle.w8a8_route_weights(topk_w, shared, routed_scale)
+    return oracle.w8a8_merge(route_out, rw, T, kt)

@@ -409,3 +409,21 @@ def test_bf16_merge_ordered_chain_is_fused(oracle_lib, kt):
     np.testing.assert_array_equal(got, oracle_lib.f32_to_bf16_bits(acc))
     if kt > 1:
         assert not np.array_equal(acc, unfused)
+
+
+@pytest.mark.parametrize("shared", [False, True])
+def test_oracle_staged_layer_equals_forward(oracle_lib, shared):
+    """The oracle's stage entry points (W13 epilogue + requant, store_w2,
+    merge) around an exact int64 numpy GEMM give orc_w8a8_forward's output bit
+    for bit, invalid ids included: they are the same code, factored out, which
+    the whole-layer GPU checks at the BASELINE shapes use with a device GEMM."""
+    x, ids, w, q13, s13, q2, s2 = H.w8a8_case(77, 23, 192, 96, 7, 3)
+    ids = ids.copy()
+    ids[3, 1] = 7   # out of range: dropped
+    ids[5, 0] = -1
+    sid = 6 if shared else -1
+    ref = oracle_lib.w8a8_forward(x, ids, w, q13, s13, q2, s2, shared_id=sid, routed_scale=2.5)
+    g13 = lambda e, a: (a.astype(np.int64) @ q13[e].astype(np.int64).T).astype(np.int32)  # noqa: E731
+    g2 = lambda e, a: (a.astype(np.int64) @ q2[e].astype(np.int64).T).astype(np.int32)  # noqa: E731
+    got = H.w8a8_layer_staged(x, ids, w, 7, sid, 2.5, g13, g2, lambda e: s13[e], lambda e: s2[e])
+    np.testing.assert_array_equal(got, ref)

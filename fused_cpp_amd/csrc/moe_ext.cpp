@@ -326,6 +326,13 @@ struct InvalidCheck {
     }
   }
 
+  // A forward that failed part-way may still have its route launch queued:
+  // let the stream drain before the slot can be reused by the next call.
+  void check_rc(int rc, const char* what) {
+    if (rc != FCMOE_OK && host) (void)hipStreamSynchronize(current_stream());
+    ::check_rc(rc, what);
+  }
+
   // After the forward was enqueued: raise if any id was out of range.
   void finish() {
     if (!validate) return;
@@ -383,7 +390,7 @@ at::Tensor w8a8_forward(at::Tensor input, at::Tensor w13, int64_t w13_k, int64_t
   a.workspace_bytes = ws.numel();
   {
     pybind11::gil_scoped_release release;
-    check_rc(fcmoe_w8a8_forward(&a, current_stream()), "fused_moe_w8a8");
+    invalid.check_rc(fcmoe_w8a8_forward(&a, current_stream()), "fused_moe_w8a8");
   }
   invalid.finish();
   return output;
@@ -462,7 +469,7 @@ at::Tensor bf16_forward(at::Tensor input, at::Tensor w13, int64_t w13_k, int64_t
   a.workspace_bytes = ws.numel();
   {
     pybind11::gil_scoped_release release;
-    check_rc(fcmoe_bf16_forward(&a, current_stream()), "fused_moe_bf16");
+    invalid.check_rc(fcmoe_bf16_forward(&a, current_stream()), "fused_moe_bf16");
   }
   invalid.finish();
   return output;
@@ -499,7 +506,7 @@ at::Tensor w8a16_forward(at::Tensor input, at::Tensor w13, int64_t w13_k, int64_
   a.workspace_bytes = ws.numel();
   {
     pybind11::gil_scoped_release release;
-    check_rc(fcmoe_w8a16_forward(&a, current_stream()), "fused_moe_w8a16");
+    invalid.check_rc(fcmoe_w8a16_forward(&a, current_stream()), "fused_moe_w8a16");
   }
   invalid.finish();
   return output;

@@ -43,8 +43,8 @@ def validate_ids_default() -> bool:
     """Range-check topk_ids in each call, as the reference does on the host
     (csrc/moe/arm/i8mm_w8a8/kernels.cpp:583-587): the route launch writes the
     count of invalid ids to pinned host memory, which the call polls until the
-    route launch has run (the rest of the forward keeps running; measured
-    cost: 3 us per call at one token, none at 64). Set
+    route launch has written it (the rest of the forward keeps running; no
+    measurable cost per call at one token or at 64). Set
     FUSED_CPP_AMD_VALIDATE_IDS=0 to skip the check.
     The read is skipped while the current stream is being captured into a
     HIP graph (a host read cannot be captured; invalid ids then contribute

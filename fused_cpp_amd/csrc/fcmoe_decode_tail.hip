@@ -224,7 +224,7 @@ __global__ __launch_bounds__(kWave) void decode_head_kernel(DecodeHeadArgs a) {
       a.sorted_routes[pos] = s;
       a.row_token[pos] = 0;
     }
-    if (s == 0) *a.invalid = n_invalid;
+    if (s == 0) store_count(a.invalid, n_invalid);
   }
   if (!ok_s) return;
 

@@ -97,6 +97,13 @@ template <int CTRL>
 __device__ __forceinline__ float dpp_f(float v) {
   return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, true));
 }
+// The invalid-id count: a relaxed store at system scope (a vector store that
+// goes through to memory), so that a host polling pinned memory for it sees
+// it while the kernel is still running rather than at the kernel's end.
+__device__ __forceinline__ void store_count(int32_t* p, int32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
 __device__ __forceinline__ float max16(float v) {
   v = fmaxf(v, dpp_f<0xB1>(v));   // quad_perm [1,0,3,2]
   v = fmaxf(v, dpp_f<0x4E>(v));   // quad_perm [2,3,0,1]

@@ -274,7 +274,7 @@ __global__ __launch_bounds__(256) void smallm_route_merge_kernel(SmallMArgs p, i
                                                                  int32_t* invalid_count) {
   const int64_t total = tokens * p.n, plane = (int64_t)p.m * p.n;
   const float* part = (const float*)p.partial;
-  if (invalid_count && blockIdx.x == 0 && threadIdx.x == 0) *invalid_count = 0;
+  if (invalid_count && blockIdx.x == 0 && threadIdx.x == 0) store_count(invalid_count, 0);
   for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (int64_t)gridDim.x * blockDim.x) {
     const int64_t t = e / p.n, h = e % p.n;
     const int pos = route_pos ? route_pos[t] : (int)t;

@@ -197,7 +197,7 @@ __device__ __forceinline__ void route_scan_body(int experts, int64_t chunks, int
     for (int64_t c = tid; c < chunks; c += kScanThreads) v += chunk_invalid[c];
     int total;
     block_exclusive_scan(v, &total);
-    if (tid == 0) *invalid = total;
+    if (tid == 0) store_count(invalid, total);
   }
   const int segs = kScanThreads / experts;  // >= 1: experts <= kScanThreads
   const int e = tid % experts, sg = tid / experts;
@@ -354,7 +354,7 @@ __device__ __forceinline__ void route_small_body(const RouteArgs& a, int routes,
       atomicAdd(&n_invalid, 1);
   }
   __syncthreads();
-  if (tid == 0) *invalid = n_invalid;  // the count is written, not accumulated
+  if (tid == 0) store_count(invalid, n_invalid);  // the count is written, not accumulated
   const bool owner = tid < a.experts;
   const int count = owner ? hist[tid] : 0;
   int total;

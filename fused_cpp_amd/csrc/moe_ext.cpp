@@ -11,6 +11,7 @@
 #include <torch/extension.h>
 
 #include <algorithm>
+#include <chrono>
 #include <climits>
 #include <thread>
 #include <unordered_map>
@@ -340,20 +341,29 @@ struct InvalidCheck {
     if (host) {
       pybind11::gil_scoped_release release;
       hipStream_t s = current_stream();
+      // Spin on the slot alone for up to 1 ms (a runtime query per turn slowed
+      // back-to-back one-token calls by ~3 us each), then also ask whether the
+      // stream has drained (a forward whose route launch writes no count).
+      const auto t0 = std::chrono::steady_clock::now();
+      bool query = false;
       for (int i = 0;; ++i) {
         bad = __atomic_load_n(host, __ATOMIC_ACQUIRE);
         if (bad != kPendingCount) break;
-        if (i % 64 == 63) {
-          const hipError_t q = hipStreamQuery(s);
-          if (q == hipSuccess) {  // the stream drained: the count is final (no route launch ran: no id checked)
-            bad = __atomic_load_n(host, __ATOMIC_ACQUIRE);
-            if (bad == kPendingCount) bad = 0;
-            break;
-          }
-          TORCH_CHECK(q == hipErrorNotReady, "fused MoE: stream error while waiting for the id check: ",
-                      hipGetErrorString(q));
-          std::this_thread::yield();
+        __builtin_ia32_pause();
+        if (i % 256 != 255) continue;
+        if (!query) {
+          query = std::chrono::steady_clock::now() - t0 > std::chrono::milliseconds(1);
+          if (!query) continue;
         }
+        const hipError_t q = hipStreamQuery(s);
+        if (q == hipSuccess) {  // the stream drained: the count is final (no route launch ran: no id checked)
+          bad = __atomic_load_n(host, __ATOMIC_ACQUIRE);
+          if (bad == kPendingCount) bad = 0;
+          break;
+        }
+        TORCH_CHECK(q == hipErrorNotReady, "fused MoE: stream error while waiting for the id check: ",
+                    hipGetErrorString(q));
+        std::this_thread::yield();
       }
     } else {
       bad = dev.item<int32_t>();

@@ -755,14 +755,15 @@ def measure(cfg, workload: str, args, device, want_cpu: bool, min_steps: int = 0
 
 
 # Extra workloads measured by default after the headline one, each on its own
-# layer: decode at small batches, the same C2 layer and T=1 with the default
-# id validation on (one device->host read of the invalid-id count per call),
-# the prefill configs, the BF16 configs, W8A16 at the C1 shape and at
-# T=4096. (workload, config, tokens, validate_ids)
-SECONDARY = [("c2_t1", "c2", 1, False), ("c2_t2", "c2", 2, False), ("c2_t8", "c2", 8, False),
-             ("c2_t32", "c2", 32, False), ("c2_validate_ids", "c2", 0, True), ("c2_t1_validate_ids", "c2", 1, True),
-             ("c3", "c3", 0, False), ("c4", "c4", 0, False), ("c1", "c1", 0, False), ("c0", "c0", 0, False),
-             ("c1w8", "c1w8", 0, False), ("c1w8_t4096", "c1w8", 4096, False)]
+# layer: decode at small batches, the same C2 layer and T=1 with the id check
+# off (FUSED_CPP_AMD_VALIDATE_IDS=0; every other line runs the operators'
+# default, the check on), the prefill configs, the BF16 configs, W8A16 at the
+# C1 shape and at T=4096. (workload, config, tokens, validate_ids)
+SECONDARY = [("c2_t1", "c2", 1, True), ("c2_t2", "c2", 2, True), ("c2_t8", "c2", 8, True),
+             ("c2_t32", "c2", 32, True), ("c2_no_validate_ids", "c2", 0, False),
+             ("c2_t1_no_validate_ids", "c2", 1, False),
+             ("c3", "c3", 0, True), ("c4", "c4", 0, True), ("c1", "c1", 0, True), ("c0", "c0", 0, True),
+             ("c1w8", "c1w8", 0, True), ("c1w8_t4096", "c1w8", 4096, True)]
 
 # The other operators of the drop-in surface, at DeepSeek-V3.2-shaped sizes
 # (public model config: hidden 7168, q_lora_rank 1536, main Q projection
@@ -1137,7 +1138,9 @@ def main() -> int:
         print(json.dumps({"error": "this build measures one GPU only: every box has one MI355X; "
                                    "run with --gpus 1"}))
         return 2
-    os.environ.setdefault("FUSED_CPP_AMD_VALIDATE_IDS", "0")  # no host read inside the timed loop
+    # the operators' default: the id check on (it waits only for each call's
+    # route launch)
+    os.environ.setdefault("FUSED_CPP_AMD_VALIDATE_IDS", "1")
     import torch
 
     device = torch.device("cuda", 0)
@@ -1177,15 +1180,16 @@ def main() -> int:
         for wl, name, tokens, validate in SECONDARY:
             c = CONFIGS[name] if tokens <= 0 else dict(CONFIGS[name], T=tokens,
                                                        desc=f"{CONFIGS[name]['desc']}, run at T={tokens}")
-            if validate:
-                c = dict(c, desc=f"{c['desc']}, default id validation on (one device->host read per call)")
+            if not validate:
+                c = dict(c, desc=f"{c['desc']}, id check off (FUSED_CPP_AMD_VALIDATE_IDS=0)")
             log(f"[bench] secondary {wl}: {c['desc']}")
+            default_validate = os.environ["FUSED_CPP_AMD_VALIDATE_IDS"]
             os.environ["FUSED_CPP_AMD_VALIDATE_IDS"] = "1" if validate else "0"
             try:
                 sec = measure(c, wl, args, device, want_cpu=not args.no_cpu_baseline,
                               min_steps=DECODE_MIN_STEPS if c["T"] <= 8 else 0)
             finally:
-                os.environ["FUSED_CPP_AMD_VALIDATE_IDS"] = "0"
+                os.environ["FUSED_CPP_AMD_VALIDATE_IDS"] = default_validate
             entry = {"workload": c["desc"], "name": wl, "validate_ids": validate,
                      "dtype": "int8" if c["kind"] == "w8a8" else "bf16",
                      "tokens_per_s": round(sec["tokens_per_s"], 1), "ms_per_step": round(sec["ms"], 4), "steps": sec["steps"],

@@ -1139,14 +1139,33 @@ extern "C" size_t fcmoe_i8gemm_workspace_bytes(int64_t m, int64_t k, int64_t n) 
   return ar.used + 256;
 }
 
-extern "C" size_t fcmoe_i8gemm_pair_workspace_bytes(int64_t m, int64_t k, int64_t n1, int64_t n2) {
+namespace {
+// Both GEMMs of a pair on the small-M kernel run as one launch, so their
+// partial sums need room side by side; otherwise the two GEMMs run one after
+// the other and share it.
+bool pair_smallm(int64_t m, int64_t k, int64_t n1, int64_t n2) {
+  return smallm_splits(m, k, n1) > 0 && smallm_splits(m, k, n2) > 0;
+}
+size_t pair_partial_bytes(int64_t m, int64_t k, int64_t n1, int64_t n2) {
+  if (pair_smallm(m, k, n1, n2)) return smallm_pair_workspace_bytes(m, k, n1, n2);
   const size_t p1 = i8gemm_partial_bytes(m, k, n1), p2 = i8gemm_partial_bytes(m, k, n2);
+  return p1 > p2 ? p1 : p2;
+}
+}  // namespace
+
+extern "C" size_t fcmoe_i8gemm_pair_workspace_bytes(int64_t m, int64_t k, int64_t n1, int64_t n2) {
   Arena ar;
-  i8_layout(m, k, p1 > p2 ? p1 : p2, ar);
+  i8_layout(m, k, pair_partial_bytes(m, k, n1, n2), ar);
   return ar.used + 256;
 }
 
 namespace {
+
+// FCMOE_I8GEMM_PAIR_FUSED=0: the pair's small-M GEMMs as two launches
+bool pair_fused() {
+  const char* v = getenv("FCMOE_I8GEMM_PAIR_FUSED");
+  return !(v && v[0] == '0');
+}
 
 // One int8 GEMM of the quantised rows in L against a packed [n, k] weight.
 int i8gemm_run(const I8Layout& L, int64_t k, const void* w_packed, const float* w_scale, int64_t n, const float* bias,
@@ -1255,9 +1274,13 @@ extern "C" int fcmoe_i8gemm_pair(const uint16_t* x, int64_t m, int64_t k, const 
   if (m > INT32_MAX / 2) return fail(FCMOE_EINVAL, "i8gemm_pair: too many rows");
   if (!x || !out1 || !out2) return fail(FCMOE_EINVAL, "i8gemm_pair: NULL tensor");
   I8Layout L;
-  const size_t p1 = i8gemm_partial_bytes(m, k, n1), p2 = i8gemm_partial_bytes(m, k, n2);
-  int rc = i8gemm_prologue(x, 0, m, k, p1 > p2 ? p1 : p2, workspace, workspace_bytes, &L, stream);
+  int rc = i8gemm_prologue(x, 0, m, k, pair_partial_bytes(m, k, n1, n2), workspace, workspace_bytes, &L, stream);
   if (rc) return rc;
+  if (pair_smallm(m, k, n1, n2) && pair_fused()) {
+    Stage st(FCMOE_STAGE_W13_CLASS0 + class_slot(16), stream);
+    return smallm_i8gemm_pair_launch(L.xq, L.kp, m, k, L.xs, w1_packed, w1_scale, n1, out1, w2_packed, w2_scale, n2,
+                                     out2, L.partial, L.partial_bytes, stream);
+  }
   if ((rc = i8gemm_run(L, k, w1_packed, w1_scale, n1, nullptr, out1, 1, stream))) return rc;
   return i8gemm_run(L, k, w2_packed, w2_scale, n2, nullptr, out2, 1, stream);
 }

@@ -83,8 +83,10 @@ __device__ __forceinline__ void sm_store(const SmallMArgs& p, int row, int64_t c
     ((float*)p.out)[(int64_t)row * p.ldo + ch] = v;
 }
 
+// Workgroup (bx, by) of one small-M GEMM: weight tiles 8 bx .. 8 bx + 7, K
+// split by.
 template <bool I8, int FM>
-__global__ __launch_bounds__(kSmWaves * kWave) void smallm_kernel(SmallMArgs p) {
+__device__ __forceinline__ void smallm_body(const SmallMArgs& p, int bx, int by) {
 #if __HIP_DEVICE_COMPILE__
   constexpr int D = kSmDepth;
   constexpr int ABYTES = FM * 1024;  // 16 FM rows x 64 bytes
@@ -95,9 +97,9 @@ __global__ __launch_bounds__(kSmWaves * kWave) void smallm_kernel(SmallMArgs p) 
   __shared__ __attribute__((aligned(1024))) uint8_t sa[D * ABYTES];
   const int lane = threadIdx.x % kWave;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-  const int64_t tile = (int64_t)blockIdx.x * kSmWaves + wave;  // packed tile (group-major)
+  const int64_t tile = (int64_t)bx * kSmWaves + wave;  // packed tile (group-major)
   const bool tv = tile < p.n_groups * p.n_tiles;
-  const int64_t c0 = (int64_t)blockIdx.y * p.cps;
+  const int64_t c0 = (int64_t)by * p.cps;
   const int64_t c1 = c0 + p.cps < p.kc ? c0 + p.cps : p.kc;
   // 32-bit chunk counters keep the loop's compares scalar (a 64-bit compare
   // took a VGPR with a load in flight and drained the ring every 8 chunks)
@@ -200,7 +202,7 @@ __global__ __launch_bounds__(kSmWaves * kWave) void smallm_kernel(SmallMArgs p) 
     for (int q = 0; q < 4; ++q) {
       const int row = i * 16 + (lane / 16) * 4 + q;
       if (row >= p.m) continue;
-      const int64_t e = ((int64_t)blockIdx.y * p.m + row) * p.n + ch;
+      const int64_t e = ((int64_t)by * p.m + row) * p.n + ch;
       if constexpr (I8) {
         if (p.partial)
           ((int32_t*)p.partial)[e] = acc[i][q];
@@ -211,6 +213,25 @@ __global__ __launch_bounds__(kSmWaves * kWave) void smallm_kernel(SmallMArgs p) 
       }
     }
 #endif
+}
+
+template <bool I8, int FM>
+__global__ __launch_bounds__(kSmWaves * kWave) void smallm_kernel(SmallMArgs p) {
+  smallm_body<I8, FM>(p, (int)blockIdx.x, (int)blockIdx.y);
+}
+
+// Two int8 GEMMs of the same rows in one launch (the i8gemm pair): workgroups
+// x < x1 run the first (splits s1), the rest the second (splits s2); grid.y
+// covers the larger split count and workgroups past their GEMM's splits exit.
+template <int FM>
+__global__ __launch_bounds__(kSmWaves * kWave) void smallm_pair_kernel(SmallMArgs p1, SmallMArgs p2, int x1, int s1,
+                                                                        int s2) {
+  const int bx = (int)blockIdx.x, by = (int)blockIdx.y;
+  if (bx < x1) {
+    if (by < s1) smallm_body<true, FM>(p1, bx, by);
+  } else if (by < s2) {
+    smallm_body<true, FM>(p2, bx - x1, by);
+  }
 }
 
 // Adds the splits' partial sums (split order) and applies the epilogue; one
@@ -358,6 +379,10 @@ size_t smallm_workspace_bytes(int64_t m, int64_t k, int64_t n) {
   return s > 1 ? (size_t)(s * m * n) * sizeof(int32_t) : 0;
 }
 
+size_t smallm_pair_workspace_bytes(int64_t m, int64_t k, int64_t n1, int64_t n2) {
+  return smallm_workspace_bytes(m, k, n1) + smallm_workspace_bytes(m, k, n2);
+}
+
 int smallm_i8gemm_launch(const int8_t* a, int64_t lda, int64_t m, int64_t k, const void* w_packed,
                          const float* scale_row, const float* scale_col, int64_t n, const float* bias, void* out,
                          int out_bf16, int32_t* partial, size_t partial_bytes, hipStream_t stream) {
@@ -388,6 +413,64 @@ int smallm_i8gemm_launch(const int8_t* a, int64_t lda, int64_t m, int64_t k, con
   if (rc || splits == 1) return rc;
   hipLaunchKernelGGL(smallm_reduce_kernel, dim3(reduce_blocks(m * n)), dim3(256), 0, stream, p, (int)splits);
   return check_launch("smallm_reduce");
+}
+
+int smallm_i8gemm_pair_launch(const int8_t* a, int64_t lda, int64_t m, int64_t k, const float* scale_row,
+                              const void* w1, const float* sc1, int64_t n1, uint16_t* out1, const void* w2,
+                              const float* sc2, int64_t n2, uint16_t* out2, int32_t* partial, size_t partial_bytes,
+                              hipStream_t stream) {
+  const int64_t s1 = smallm_splits(m, k, n1), s2 = smallm_splits(m, k, n2);
+  if (s1 <= 0 || s2 <= 0) return fail(FCMOE_EINVAL, "small-M i8gemm pair: shape outside its domain");
+  if (lda % 64 || lda < round_up(k, 64) || (int64_t)m * lda >= 0x7ffffff0)
+    return fail(FCMOE_EINVAL, "small-M i8gemm pair: bad row stride");
+  if (partial_bytes < smallm_pair_workspace_bytes(m, k, n1, n2) || (!partial && partial_bytes))
+    return fail(FCMOE_ESPACE, "small-M i8gemm pair: partial-sum workspace too small");
+  SmallMArgs p[2]{};
+  const void* ws[2] = {w1, w2};
+  const float* scs[2] = {sc1, sc2};
+  const int64_t ns[2] = {n1, n2}, ss[2] = {s1, s2};
+  uint16_t* outs[2] = {out1, out2};
+  int32_t* part = partial;
+  for (int g = 0; g < 2; ++g) {
+    SmallMArgs& q = p[g];
+    q.a = a;
+    q.lda = lda;
+    q.m = (int)m;
+    q.kc = ceil_div(k, 64);
+    q.cps = ceil_div(q.kc, ss[g]);
+    q.w = ws[g];
+    q.n_groups = 1;
+    q.n_tiles = ceil_div(ns[g], 16);
+    q.n_half = ns[g];
+    q.n = ns[g];
+    q.scale_row = scale_row;
+    q.scale_col = scs[g];
+    q.out = outs[g];
+    q.out_bf16 = 1;
+    q.ldo = ns[g];
+    q.partial = ss[g] > 1 ? part : nullptr;
+    if (ss[g] > 1) part += ss[g] * m * ns[g];
+  }
+  const int x1 = (int)ceil_div(p[0].n_tiles, kSmWaves), x2 = (int)ceil_div(p[1].n_tiles, kSmWaves);
+  const dim3 grid((unsigned)(x1 + x2), (unsigned)(s1 > s2 ? s1 : s2)), block(kSmWaves * kWave);
+  const int fm = (int)ceil_div(m, 16);
+  if (fm == 1)
+    hipLaunchKernelGGL(smallm_pair_kernel<1>, grid, block, 0, stream, p[0], p[1], x1, (int)s1, (int)s2);
+  else if (fm == 2)
+    hipLaunchKernelGGL(smallm_pair_kernel<2>, grid, block, 0, stream, p[0], p[1], x1, (int)s1, (int)s2);
+  else if (fm <= 4)
+    hipLaunchKernelGGL(smallm_pair_kernel<4>, grid, block, 0, stream, p[0], p[1], x1, (int)s1, (int)s2);
+  else if (fm <= 8)
+    hipLaunchKernelGGL(smallm_pair_kernel<8>, grid, block, 0, stream, p[0], p[1], x1, (int)s1, (int)s2);
+  else
+    hipLaunchKernelGGL(smallm_pair_kernel<16>, grid, block, 0, stream, p[0], p[1], x1, (int)s1, (int)s2);
+  int rc = check_launch("smallm_pair_gemm");
+  for (int g = 0; g < 2 && !rc; ++g) {
+    if (ss[g] <= 1) continue;
+    hipLaunchKernelGGL(smallm_reduce_kernel, dim3(reduce_blocks(m * ns[g])), dim3(256), 0, stream, p[g], (int)ss[g]);
+    rc = check_launch("smallm_reduce");
+  }
+  return rc;
 }
 
 int i8gemm_reduce_launch(const int32_t* partial, int64_t splits, int64_t m, int64_t n, const float* scale_row,

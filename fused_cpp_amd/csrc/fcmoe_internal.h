@@ -222,6 +222,14 @@ size_t smallm_workspace_bytes(int64_t m, int64_t k, int64_t n);
 int smallm_i8gemm_launch(const int8_t* a, int64_t lda, int64_t m, int64_t k, const void* w_packed,
                          const float* scale_row, const float* scale_col, int64_t n, const float* bias, void* out,
                          int out_bf16, int32_t* partial, size_t partial_bytes, hipStream_t stream);
+// The i8gemm pair at few rows: both GEMMs of the same quantised rows in one
+// launch (bf16 outputs, no bias), then a reduce per GEMM with more than one
+// split; the partial sums of the two sit back to back in `partial`.
+size_t smallm_pair_workspace_bytes(int64_t m, int64_t k, int64_t n1, int64_t n2);
+int smallm_i8gemm_pair_launch(const int8_t* a, int64_t lda, int64_t m, int64_t k, const float* scale_row,
+                              const void* w1, const float* sc1, int64_t n1, uint16_t* out1, const void* w2,
+                              const float* sc2, int64_t n2, uint16_t* out2, int32_t* partial, size_t partial_bytes,
+                              hipStream_t stream);
 // The BF16 dense MLP at few rows on the same kernel: W13 (out_row null: the
 // activation store into y, bf16 [m, ldo]) or W2 (the fp32 route store into
 // out at row out_row[r]). k_chunks: 64-byte K chunks; weights packed bf16

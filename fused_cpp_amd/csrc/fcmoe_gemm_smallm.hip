@@ -379,8 +379,18 @@ size_t smallm_workspace_bytes(int64_t m, int64_t k, int64_t n) {
   return s > 1 ? (size_t)(s * m * n) * sizeof(int32_t) : 0;
 }
 
+// The pair's one launch: the split count that brings both GEMMs' workgroups
+// together to about one per CU (DeepSeek V4's [24576 + 8192, 1536] at 64 rows:
+// 192 + 64 workgroups, one split, no reduce: 0.0275 -> 0.018 ms against each
+// GEMM split on its own, 1 and 3 ways).
+int64_t smallm_pair_splits(int64_t m, int64_t k, int64_t n1, int64_t n2) {
+  if (smallm_splits(m, k, n1) <= 0 || smallm_splits(m, k, n2) <= 0) return 0;
+  return splits_for(m, ceil_div(k, 64), round_up(ceil_div(n1, 16), kSmWaves) + round_up(ceil_div(n2, 16), kSmWaves));
+}
+
 size_t smallm_pair_workspace_bytes(int64_t m, int64_t k, int64_t n1, int64_t n2) {
-  return smallm_workspace_bytes(m, k, n1) + smallm_workspace_bytes(m, k, n2);
+  const int64_t s = smallm_pair_splits(m, k, n1, n2);
+  return s > 1 ? (size_t)(s * m * (n1 + n2)) * sizeof(int32_t) : 0;
 }
 
 int smallm_i8gemm_launch(const int8_t* a, int64_t lda, int64_t m, int64_t k, const void* w_packed,
@@ -419,8 +429,8 @@ int smallm_i8gemm_pair_launch(const int8_t* a, int64_t lda, int64_t m, int64_t k
                               const void* w1, const float* sc1, int64_t n1, uint16_t* out1, const void* w2,
                               const float* sc2, int64_t n2, uint16_t* out2, int32_t* partial, size_t partial_bytes,
                               hipStream_t stream) {
-  const int64_t s1 = smallm_splits(m, k, n1), s2 = smallm_splits(m, k, n2);
-  if (s1 <= 0 || s2 <= 0) return fail(FCMOE_EINVAL, "small-M i8gemm pair: shape outside its domain");
+  const int64_t s1 = smallm_pair_splits(m, k, n1, n2), s2 = s1;
+  if (s1 <= 0) return fail(FCMOE_EINVAL, "small-M i8gemm pair: shape outside its domain");
   if (lda % 64 || lda < round_up(k, 64) || (int64_t)m * lda >= 0x7ffffff0)
     return fail(FCMOE_EINVAL, "small-M i8gemm pair: bad row stride");
   if (partial_bytes < smallm_pair_workspace_bytes(m, k, n1, n2) || (!partial && partial_bytes))

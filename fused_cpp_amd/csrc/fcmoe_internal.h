@@ -225,6 +225,8 @@ int smallm_i8gemm_launch(const int8_t* a, int64_t lda, int64_t m, int64_t k, con
 // The i8gemm pair at few rows: both GEMMs of the same quantised rows in one
 // launch (bf16 outputs, no bias), then a reduce per GEMM with more than one
 // split; the partial sums of the two sit back to back in `partial`.
+// (one split count for both: about one workgroup per CU over the two)
+int64_t smallm_pair_splits(int64_t m, int64_t k, int64_t n1, int64_t n2);
 size_t smallm_pair_workspace_bytes(int64_t m, int64_t k, int64_t n1, int64_t n2);
 int smallm_i8gemm_pair_launch(const int8_t* a, int64_t lda, int64_t m, int64_t k, const float* scale_row,
                               const void* w1, const float* sc1, int64_t n1, uint16_t* out1, const void* w2,

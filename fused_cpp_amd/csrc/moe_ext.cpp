@@ -349,7 +349,9 @@ struct InvalidCheck {
       for (int i = 0;; ++i) {
         bad = __atomic_load_n(host, __ATOMIC_ACQUIRE);
         if (bad != kPendingCount) break;
+#if defined(__x86_64__) || defined(__i386__)
         __builtin_ia32_pause();
+#endif
         if (i % 256 != 255) continue;
         if (!query) {
           query = std::chrono::steady_clock::now() - t0 > std::chrono::milliseconds(1);

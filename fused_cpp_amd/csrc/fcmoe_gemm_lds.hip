@@ -954,7 +954,9 @@ int launch_lds_bm(int bm, const GemmParams& p, int64_t max_tiles, hipStream_t st
       // The mixed plan's persistent launch: 2 x 4 waves of 128 x 64 (at most
       // 216 VGPRs, 115 KB of LDS), so that the 16-row streaming launch's
       // waves (64 VGPRs) fit on every SIMD beside two of its waves.
-      if (p.persist > 0) return launch_lds_cfg<I8, EPI, 8, 4, 2, 3, 0, 128, 2, 4, true>(p, max_tiles, stream);
+      // (not for the raw-sum diagnostic, which never runs persistent)
+      if constexpr (EPI != kEpiRawI32)
+        if (p.persist > 0) return launch_lds_cfg<I8, EPI, 8, 4, 2, 3, 0, 128, 2, 4, true>(p, max_tiles, stream);
       // W13 (gate/up pairs) on 4-wave workgroups, two per CU (2 x 2 waves of
       // 128 x 96, 72 KB of LDS): another workgroup's K loop overlaps each
       // item's epilogue (C3 W13 0.938 -> 0.927 ms, C4 0.455 -> 0.417 ms). W2

@@ -95,10 +95,11 @@ def test_pair_equals_two_single_projections(gpu, m, k, n1, n2):
 
 
 def test_pair_with_split_counts_differing_equals_singles(gpu):
-    """64 rows: the first GEMM (32768 channels: 256 workgroups of 8 tiles)
-    runs unsplit, the second (8192) splits K three ways and needs the
-    partial-sum workspace the first does not; the pair equals the two single
-    GEMMs bit for bit (each checked against the oracle elsewhere)."""
+    """64 rows: alone, the first GEMM (32768 channels: 256 workgroups of 8
+    tiles) runs unsplit and the second (8192) splits K three ways; in the
+    pair's one launch both run unsplit (320 workgroups) while (7, 7168, 1536,
+    512) above splits both 14 ways. The pair equals the two single GEMMs bit
+    for bit (each checked against the oracle elsewhere)."""
     from fused_cpp_amd.deepseek_v4_w8a8 import (deepseek_v4_w8a8_linear, deepseek_v4_w8a8_linear_pair,
                                                  prepare_deepseek_v4_w8a8_linear_quantized_weight)
 

@@ -1079,6 +1079,82 @@ def probes() -> int:
     return 0
 
 
+def item_trace(cfg) -> int:
+    """Per-item timing of the persistent LDS launches (W13 and W2 epilogues)
+    of one forward, from a diagnostic build's item trace: per row-count class
+    the mean K-loop and epilogue microseconds, the launch span, the idle
+    fraction of the workgroups' time and the per-XCD end times. Once with the
+    production launch path, once with the serial stage-timing path."""
+    import ctypes
+
+    import torch
+
+    from fused_cpp_amd import cabi
+    from fused_cpp_amd.moe import fused_moe_w8a8_tiled_with_shared
+
+    L = cabi.lib()
+    if not hasattr(L, "fcmoe_diag_item_trace"):
+        print(json.dumps({"error": "libfcmoe.so is not a diagnostic build with the item trace (--diag 4)",
+                          "lib": str(cabi.LIB_PATH)}))
+        return 2
+    fn = L.fcmoe_diag_item_trace
+    fn.restype, fn.argtypes = ctypes.c_int, [ctypes.c_void_p, ctypes.c_int]
+    dev = torch.device("cuda", 0)
+    weights, _ = get_layer(cfg, dev)
+    ids, w, _ = make_routing(cfg)
+    x = make_x(cfg, dev)
+    ids_d, w_d = torch.from_numpy(ids).to(dev), torch.from_numpy(w).to(dev)
+    out = torch.empty_like(x)
+
+    def forward():
+        fused_moe_w8a8_tiled_with_shared(x, weights, w_d, ids_d, routed_scaling_factor=cfg["scale"], out=out)
+
+    for _ in range(3):
+        forward()
+    torch.cuda.synchronize()
+    buf = np.zeros(2 * 256 * 64 * 4, dtype=np.uint64)
+    res = {"workload": cfg["desc"], "clock_MHz": 100}
+    for mode in ("production", "serial"):
+        cabi.stage_timing_enable(mode == "serial")
+        zeros = np.zeros_like(buf)
+        cabi.check(fn(zeros.ctypes.data, 1), "item trace clear")
+        forward()
+        torch.cuda.synchronize()
+        cabi.stage_timing_read()
+        cabi.check(fn(buf.ctypes.data, 0), "item trace read")
+        t = buf.reshape(2, 256, 64, 4).astype(np.int64)
+        valid = t[..., 0] > 0
+        t0 = t[..., 0][valid].min() if valid.any() else 0
+        launches = {}
+        for e, name in ((0, "w13"), (1, "w2")):
+            v = valid[e]
+            if not v.any():
+                continue
+            T = (t[e, :, :, :3] - t0) / 100.0  # us
+            rows = (t[e, :, :, 3] >> 32) & 0xFFFF
+            ends = np.where(v, T[:, :, 2], -np.inf).max(1)
+            starts = np.where(v, T[:, :, 0], np.inf).min(1)
+            used = v.any(1)
+            span = float(ends[used].max() - starts[used].min())
+            busy = ((T[:, :, 2] - T[:, :, 0]) * v).sum(1)[used]
+            kl, ep, r = (T[:, :, 1] - T[:, :, 0])[v], (T[:, :, 2] - T[:, :, 1])[v], rows[v]
+            classes = {}
+            for lo, hi in ((1, 16), (17, 128), (129, 192), (193, 255), (256, 256)):
+                m = (r >= lo) & (r <= hi)
+                if m.any():
+                    classes[f"{lo}-{hi}"] = {"items": int(m.sum()), "kloop_us": round(float(kl[m].mean()), 1),
+                                             "epilogue_us": round(float(ep[m].mean()), 1),
+                                             "cu_us_per_wg": round(float((kl + ep)[m].sum() / used.sum()), 1)}
+            xe = [round(float(ends[x::8][used[x::8]].max()), 1) if used[x::8].any() else None for x in range(8)]
+            launches[name] = {"workgroups": int(used.sum()), "span_us": round(span, 1),
+                              "idle_frac": round(1 - float(busy.mean()) / span, 3), "xcd_end_us": xe,
+                              "rows_classes": classes}
+        res[mode] = launches
+    cabi.stage_timing_enable(False)
+    print(json.dumps({"item_trace": res}))
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -1108,7 +1184,13 @@ def main() -> int:
     ap.add_argument("--ops", action="store_true",
                     help="only run the operator entries (i8gemm, i8gemm pair, shared MLP at the DeepSeek V4 "
                          "shapes) and print them as one JSON line")
+    ap.add_argument("--item-trace", action="store_true",
+                    help="only trace the persistent prefill launches' items (a diagnostic build: python -m "
+                         "fused_cpp_amd.build --diag 4 --out DIR, run with LD_LIBRARY_PATH=DIR FCMOE_LIB_DIR=DIR) "
+                         "for one production and one serial forward of --config; prints one JSON line")
     args = ap.parse_args()
+    if args.item_trace:
+        return item_trace(CONFIGS[args.config])
     if args.ops:
         if args.gpus != 1:
             print(json.dumps({"error": "this build measures one GPU only: run with --gpus 1"}))

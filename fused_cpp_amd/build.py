@@ -77,24 +77,33 @@ def _check_no_scratch(src: str, remarks: str) -> None:
         raise RuntimeError(f"{src}: kernels use scratch (register spills): {spilled[:4]}")
 
 
-def build_lib() -> Path:
-    """Compile every HIP source to an object in parallel, then link libfcmoe.so."""
-    BUILD_DIR.mkdir(exist_ok=True)
+def build_lib(out_dir: Path | None = None, diag: int = 0) -> Path:
+    """Compile every HIP source to an object in parallel, then link libfcmoe.so
+    (and libfcmoe_probe.so). With out_dir, only libfcmoe.so is built, into
+    out_dir, with the diagnostic bits `diag` of fcmoe_gemm_lds.hip (FCMOE_DIAG:
+    timing-only variants and the persistent launches' item trace); the
+    package's own library is always built without them."""
+    lib_path = LIB if out_dir is None else Path(out_dir) / "libfcmoe.so"
+    build_dir = BUILD_DIR if out_dir is None else Path(out_dir) / "_obj"
+    build_dir.mkdir(parents=True, exist_ok=True)
     hipcc = str(ROCM / "bin" / "hipcc")
+    flags = HIP_FLAGS + ([f"-DFCMOE_DIAG={int(diag)}"] if diag else [])
 
     def compile_one(src: str) -> str:
-        obj = BUILD_DIR / (src + ".o")
-        remarks = _run([hipcc, *HIP_FLAGS, "-Rpass-analysis=kernel-resource-usage", "-c", str(CSRC / src), "-o",
+        obj = build_dir / (src + ".o")
+        remarks = _run([hipcc, *flags, "-Rpass-analysis=kernel-resource-usage", "-c", str(CSRC / src), "-o",
                         str(obj)])
         _check_no_scratch(src, remarks)
         return str(obj)
 
-    srcs = HIP_SOURCES + PROBE_SOURCES
+    srcs = HIP_SOURCES + (PROBE_SOURCES if out_dir is None else [])
     with ThreadPoolExecutor(max_workers=min(len(srcs), os.cpu_count() or 1)) as ex:
         objs = dict(zip(srcs, ex.map(compile_one, srcs)))
-    tmp = LIB.with_suffix(".so.tmp")
+    tmp = lib_path.with_suffix(".so.tmp")
     _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *[objs[s] for s in HIP_SOURCES]])
-    os.replace(tmp, LIB)
+    os.replace(tmp, lib_path)
+    if out_dir is not None:
+        return lib_path
     tmp = PROBE_LIB.with_suffix(".so.tmp")
     _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *[objs[s] for s in PROBE_SOURCES],
           f"-L{PKG}", "-lfcmoe", "-Wl,-rpath,$ORIGIN"])
@@ -150,5 +159,18 @@ def build() -> None:
 
 
 if __name__ == "__main__":
-    build()
-    print(f"built {LIB.name} and {EXT.name}")
+    import argparse
+
+    ap = argparse.ArgumentParser(description="build libfcmoe.so and the torch extension in-tree")
+    ap.add_argument("--diag", type=int, default=0,
+                    help="with --out: diagnostic bits of the LDS-staged GEMM (1 no epilogues, 2 no stage loads, "
+                         "8 no fragment reads or MFMAs, 4 item trace); load the result with LD_LIBRARY_PATH=DIR FCMOE_LIB_DIR=DIR")
+    ap.add_argument("--out", default=None, help="directory for a diagnostic libfcmoe.so (the package's is untouched)")
+    args = ap.parse_args()
+    if args.out:
+        print(f"built {build_lib(Path(args.out), args.diag)}")
+    else:
+        if args.diag:
+            raise SystemExit("--diag needs --out: the package's library is built without diagnostics")
+        build()
+        print(f"built {LIB.name} and {EXT.name}")

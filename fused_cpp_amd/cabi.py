@@ -9,9 +9,13 @@ with the current torch HIP stream.
 from __future__ import annotations
 
 import ctypes
+import os
 from pathlib import Path
 
-LIB_PATH = Path(__file__).resolve().parent / "libfcmoe.so"
+# FCMOE_LIB_DIR: a diagnostic build's directory (python -m fused_cpp_amd.build
+# --diag N --out DIR), loaded together with LD_LIBRARY_PATH=DIR so that the
+# torch extension resolves the same library
+LIB_PATH = Path(os.environ.get("FCMOE_LIB_DIR") or Path(__file__).resolve().parent) / "libfcmoe.so"
 
 FCMOE_ACT_SILU = 0
 FCMOE_ACT_GELU = 1

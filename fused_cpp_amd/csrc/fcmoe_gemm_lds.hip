@@ -69,6 +69,22 @@ __device__ __forceinline__ void wait_vmcnt() {
 // belong to one expert) are both fetched from HBM once per window.
 // gm = 0 keeps plain tile-major order.
 constexpr int kXcds = 8;
+
+// Diagnostic builds only (python -m fused_cpp_amd.build --diag N --out DIR;
+// the library in the package is always built with 0). Bits: 1 skips the
+// LDS-staged launches' epilogues, 2 their stage loads, 8 their fragment reads
+// and MFMAs (all timing only: the results are wrong), 4 records each persistent-launch item of the W13 / W2
+// epilogues (start, end of the K loop, end of the epilogue: s_memrealtime,
+// 100 MHz; tile, channel block, rows, expert) into g_item_trace, read by
+// fcmoe_diag_item_trace.
+#ifndef FCMOE_DIAG
+#define FCMOE_DIAG 0
+#endif
+constexpr int kDiag = FCMOE_DIAG;
+constexpr int kTraceWgs = 256, kTraceItems = 64;
+#if FCMOE_DIAG & 4
+__device__ unsigned long long g_item_trace[2 * kTraceWgs * kTraceItems * 4];  // [W13 / W2][wg][item][4]
+#endif
 constexpr int kLdsGroupTiles = 4;
 // gm value of a persistent launch that deals whole row tiles to the XCDs
 // round-robin (see lds_work_item).
@@ -537,6 +553,18 @@ __device__ __forceinline__ void lds_gemm_body(const GemmParams& p, int n_blocks,
   const int rows_left = p.counts[expert] - m0;
   const int rows = rows_left < BM ? rows_left : BM;
   const int pos0 = p.offsets[expert] + m0;
+#if FCMOE_DIAG & 4
+  unsigned long long* const trp =
+      PERSIST && (EPI == kEpiW13SwigluI8 || EPI == kEpiW2RouteI8) && blockIdx.x < kTraceWgs && it < kTraceItems &&
+              threadIdx.x == 0
+          ? g_item_trace + (((EPI == kEpiW2RouteI8 ? kTraceWgs : 0) + blockIdx.x) * kTraceItems + it) * 4
+          : nullptr;
+  if (trp) {
+    trp[0] = __builtin_amdgcn_s_memrealtime();
+    trp[3] = (unsigned long long)tile_idx | ((unsigned long long)nb << 16) | ((unsigned long long)rows << 32) |
+             ((unsigned long long)expert << 48);
+  }
+#endif
 
   const int lane = threadIdx.x % kWave;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -620,6 +648,7 @@ __device__ __forceinline__ void lds_gemm_body(const GemmParams& p, int n_blocks,
   const int64_t a_stages = APAIR ? (kc + 1) / 2 : kc;
   const bool a_hi = AWIDE && ((lane % 8) ^ ((((wave & 1) << 2) | (lane >> 4)) & 7)) >= 4;
   auto issue_a = [&](int64_t c, int stage) {
+    if constexpr (kDiag & 2) return;
     const int64_t cc = c < a_stages ? c : a_stages - 1;
     const int soff = (int)(kbeg * 64 + cc * AW);
     const bool fold = APAIR && kbeg + 2 * cc + 1 >= ktot;
@@ -629,6 +658,7 @@ __device__ __forceinline__ void lds_gemm_body(const GemmParams& p, int n_blocks,
                                                fold && a_hi ? voff_a[u] - 64 : voff_a[u], soff, 0, 0);
   };
   auto issue_b = [&](int64_t c, int stage) {
+    if constexpr (kDiag & 2) return;
     const int soff = (int)((kbeg + (c < kc ? c : kc - 1)) * 1024);
 #pragma unroll
     for (int u = 0; u < LPB; ++u)
@@ -736,6 +766,7 @@ __device__ __forceinline__ void lds_gemm_body(const GemmParams& p, int n_blocks,
   // pinned: left to itself the compiler sinks each read next to its first use
   // and every row then waits out the LDS latency.
   auto compute = [&](const uint8_t* sta, const uint8_t* stb) {
+    if constexpr (kDiag & 8) return;
     v4i bf[FN];
     v4i af[3];
     af[0] = *(const v4i*)(sta);
@@ -839,6 +870,9 @@ __device__ __forceinline__ void lds_gemm_body(const GemmParams& p, int n_blocks,
     }
   }
   wait_vmcnt<0>();  // the trailing (unused) stage loads
+#if FCMOE_DIAG & 4
+  if (trp) trp[1] = __builtin_amdgcn_s_memrealtime();
+#endif
 
   int64_t gtile[FN];
   bool tvalid[FN];
@@ -849,11 +883,24 @@ __device__ __forceinline__ void lds_gemm_body(const GemmParams& p, int n_blocks,
     static_assert(WAVES * staged_slice_bytes<FN>(EPI) <= SA * A_BYTES + SB * B_BYTES, "staging slices fit the stages");
     // every wave is past its last chunk's fragment reads: the stages are free
     __builtin_amdgcn_s_barrier();
-    staged_epilogue<EPI, FM, FN>(p, acc, gtile, tvalid, wm * FM * 16, rows, pos0, expert, lane, meta,
-                                 (lds_u8_ptr)(smem + wave * staged_slice_bytes<FN>(EPI)));
+    if constexpr (!(kDiag & 1))
+      staged_epilogue<EPI, FM, FN>(p, acc, gtile, tvalid, wm * FM * 16, rows, pos0, expert, lane, meta,
+                                   (lds_u8_ptr)(smem + wave * staged_slice_bytes<FN>(EPI)));
   } else {
-    gemm_epilogue<I8, EPI, FM, FN, true>(p, acc, gtile, tvalid, wm * FM * 16, rows, pos0, expert, lane, meta);
+    if constexpr (!(kDiag & 1))
+      gemm_epilogue<I8, EPI, FM, FN, true>(p, acc, gtile, tvalid, wm * FM * 16, rows, pos0, expert, lane, meta);
   }
+  if constexpr (kDiag & 1) {
+    // no epilogue: every accumulator is still consumed (an empty asm
+    // statement), so the fragment reads and MFMAs stay
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j) asm volatile("" ::"v"(acc[i][j]));
+  }
+#if FCMOE_DIAG & 4
+  if (trp) trp[2] = __builtin_amdgcn_s_memrealtime();
+#endif
   }
 #endif
 }
@@ -1014,6 +1061,17 @@ int launch_lds_w8(int bm, const GemmParams& p, int64_t max_tiles, hipStream_t st
 }
 
 }  // namespace
+
+#if FCMOE_DIAG & 4
+// Diagnostic builds: the item trace (2 x 256 workgroups x 64 items x 4
+// 64-bit words) copied to host (write = 0), or overwritten from host (write =
+// 1: the caller passes zeros to clear it).
+extern "C" int fcmoe_diag_item_trace(void* host, int write) {
+  const hipError_t e = write ? hipMemcpyToSymbol(HIP_SYMBOL(g_item_trace), host, sizeof(g_item_trace))
+                             : hipMemcpyFromSymbol(host, HIP_SYMBOL(g_item_trace), sizeof(g_item_trace));
+  return e == hipSuccess ? 0 : -1;
+}
+#endif
 
 int gemm_lds_launch(int epi, int bm, const GemmParams& p, int64_t max_tiles, hipStream_t stream) {
   switch (epi) {

@@ -1141,15 +1141,18 @@ extern "C" size_t fcmoe_i8gemm_workspace_bytes(int64_t m, int64_t k, int64_t n) 
 
 namespace {
 // Both GEMMs of a pair on the small-M kernel run as one launch, so their
-// partial sums need room side by side; otherwise the two GEMMs run one after
-// the other and share it.
+// partial sums need room side by side; otherwise (and with the fused launch
+// turned off) the two GEMMs run one after the other and share it. The
+// workspace covers either.
 bool pair_smallm(int64_t m, int64_t k, int64_t n1, int64_t n2) {
   return smallm_splits(m, k, n1) > 0 && smallm_splits(m, k, n2) > 0;
 }
 size_t pair_partial_bytes(int64_t m, int64_t k, int64_t n1, int64_t n2) {
-  if (pair_smallm(m, k, n1, n2)) return smallm_pair_workspace_bytes(m, k, n1, n2);
   const size_t p1 = i8gemm_partial_bytes(m, k, n1), p2 = i8gemm_partial_bytes(m, k, n2);
-  return p1 > p2 ? p1 : p2;
+  const size_t sep = p1 > p2 ? p1 : p2;  // the two GEMMs one after the other (FCMOE_I8GEMM_PAIR_FUSED=0 too)
+  if (!pair_smallm(m, k, n1, n2)) return sep;
+  const size_t fused = smallm_pair_workspace_bytes(m, k, n1, n2);
+  return fused > sep ? fused : sep;
 }
 }  // namespace
 

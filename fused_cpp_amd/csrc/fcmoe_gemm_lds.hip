@@ -493,47 +493,29 @@ __device__ __forceinline__ void lds_gemm_body(const GemmParams& p, int n_blocks,
   // vmcnt(0) per chunk, see above)
   int* const next_k = (int*)(smem + META + 8 * BM + 64 * NT);
   const int xcd = (int)blockIdx.x % kXcds;
-  // valid slots of XCD x (lds_work_item's layout)
-  auto items_of = [&](int x) -> int {
+  int xcd_items = 0;  // valid slots of this XCD (lds_work_item's layout)
+  if constexpr (PERSIST) {
     const int nbf = partial ? n_blocks - 1 : n_blocks;
     const int F = count * nbf, P = partial ? count : 0;
-    if (gm <= 0) return grid_items;  // plain order: slots are not XCD-local
-    if (gm == kLdsDealTiles) return deal_tiles(count, x) * (nbf + (partial ? 1 : 0));
-    return F / kXcds + (x < F % kXcds ? 1 : 0) + P / kXcds + (x < P % kXcds ? 1 : 0);
-  };
-  // Once its own XCD's queue is empty a workgroup takes items from the other
-  // XCDs' queues in turn (their operands then come from another L2): the
-  // queues drained up to ~140 us apart (C3's W13 launch, production timeline);
-  // C4 4.474 -> 4.465 ms, C3 2.695 -> 2.693 (four runs each, same box).
-  const bool steal = PERSIST && queue && gm > 0 && p.steal;
-  // (k, kx): item k of XCD kx's list
-  auto fetch_k = [&](int k_static, int* kx) -> int {
-    *kx = xcd;
+    xcd_items = F / kXcds + (xcd < F % kXcds ? 1 : 0) + P / kXcds + (xcd < P % kXcds ? 1 : 0);
+    if (gm == kLdsDealTiles) xcd_items = deal_tiles(count, xcd) * (nbf + (partial ? 1 : 0));
+    if (gm <= 0) xcd_items = grid_items;  // plain order: slots are not XCD-local
+  }
+  auto fetch_k = [&](int k_static) -> int {
     if (!PERSIST || !queue) return k_static;
     __syncthreads();  // everyone has read the previous next_k
-    if (threadIdx.x == 0) {
-      int x = xcd;
-      int kk = __hip_atomic_fetch_add(queue + x, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      for (int d = 1; steal && d < kXcds && kk >= items_of(x); ++d) {
-        x = (xcd + d) % kXcds;
-        kk = __hip_atomic_fetch_add(queue + x, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-      next_k[0] = kk;
-      next_k[1] = x;
-    }
+    if (threadIdx.x == 0) *next_k = __hip_atomic_fetch_add(queue + xcd, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
-    *kx = next_k[1];
-    return next_k[0];
+    return *next_k;
   };
-  int kx = xcd;
-  int k = PERSIST ? fetch_k((int)blockIdx.x / kXcds, &kx) : 0;
-  for (int it = 0, slot = (int)blockIdx.x; PERSIST ? k < items_of(kx) : it < 1; ++it) {
-  if constexpr (PERSIST) slot = gm <= 0 ? (int)blockIdx.x + it * (int)gridDim.x : k * kXcds + kx;
+  int k = PERSIST ? fetch_k((int)blockIdx.x / kXcds) : 0;
+  for (int it = 0, slot = (int)blockIdx.x; PERSIST ? k < xcd_items : it < 1; ++it) {
+  if constexpr (PERSIST) slot = gm <= 0 ? (int)blockIdx.x + it * (int)gridDim.x : k * kXcds + xcd;
   int tile_idx, nb;
   const bool have = lds_work_item(slot, count, n_blocks, partial != 0, gm, tile_idx, nb);
   if constexpr (PERSIST) {
-    k = fetch_k(k + (int)gridDim.x / kXcds, &kx);
-    if (gm <= 0) k = slot + (int)gridDim.x < grid_items ? 0 : grid_items;  // plain order: stride over all slots
+    k = fetch_k(k + (int)gridDim.x / kXcds);
+    if (gm <= 0) k = slot + (int)gridDim.x < grid_items ? 0 : xcd_items;  // plain order: stride over all slots
     if (!have) continue;
     if (it > 0) __syncthreads();  // the previous item's epilogue is done with the stages
   } else {
@@ -930,13 +912,7 @@ int64_t lds_blocks(int wn, int fn, const GemmParams& p) {
 
 template <bool I8, int EPI, int FM, int FN, int SA, int SB, int BPOL, int AW, int WMW = kWM, int WNW = kWN,
           bool PERSIST = false>
-int launch_lds_cfg(const GemmParams& p0, int64_t max_tiles, hipStream_t stream) {
-  GemmParams p = p0;
-  static const bool steal = [] {
-    const char* v = getenv("FCMOE_LDS_STEAL");
-    return !(v && v[0] == '0');
-  }();
-  p.steal = steal ? 1 : 0;
+int launch_lds_cfg(const GemmParams& p, int64_t max_tiles, hipStream_t stream) {
   const int64_t n_blocks = lds_blocks<EPI>(WNW, FN, p);
   if (max_tiles * n_blocks <= 0) return FCMOE_OK;
   constexpr bool PAIR = epi_pair(EPI);

@@ -182,9 +182,6 @@ struct GemmParams {
   int64_t k_total;
   int32_t* split_out;
   int64_t split_rows;
-  // Persistent LDS launches with queues: take other XCDs' items once the own
-  // XCD's are done (set by the launch; FCMOE_LDS_STEAL=0 turns it off).
-  int steal;
 };
 
 // Whether a launch's plan gate lets it run (device side).
